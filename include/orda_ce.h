@@ -1,0 +1,182 @@
+/*
+ * orda_ce.h -- C ABI of liborda_ce.so, the MI355X (gfx950) implementation of
+ * the fused LM-head cross-entropy + knowledge-distillation loss.
+ *
+ * The reference (orda_ce_kernel, Python + Triton) has no native library; its
+ * hot path is the chunk loop inside the three autograd Functions.  Each entry
+ * point below replaces one piece of that loop, named in its comment as
+ * reference-file:line (paths relative to the reference's src/orda_ce_kernel/).
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated otherwise.  The library
+ *     never allocates or frees device memory: the caller (PyTorch) owns every
+ *     input, output, saved and workspace buffer.
+ *   - All matrices are dense row-major with the leading dimension equal to
+ *     the row length (the Python layer calls .contiguous() first, as the
+ *     reference does at ops/tied_teacher.py:334-339).
+ *   - Launches are asynchronous on the given stream; nothing synchronises the
+ *     host.  Calls on different streams may run concurrently if they use
+ *     different workspace buffers.
+ *   - Return value: 0 on success, a negative ORDA_E* code otherwise; the
+ *     message is available from orda_last_error() (thread-local).
+ */
+#ifndef ORDA_CE_H
+#define ORDA_CE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORDA_ABI_VERSION 1
+
+/* Teacher modes (reference api.py:21-52, ops/separate_teacher.py:1102). */
+enum orda_mode {
+  ORDA_MODE_TIED = 0,               /* student and teacher share W          */
+  ORDA_MODE_SEPARATE = 1,           /* teacher (hidden_t, W_t)              */
+  ORDA_MODE_PRECOMPUTED_LOGITS = 2, /* teacher logits [N x V] given         */
+  ORDA_MODE_PRECOMPUTED_HIDDEN = 3  /* frozen (hidden_t, W_t), no grads     */
+};
+
+/* Element types. */
+enum orda_dtype { ORDA_BF16 = 0, ORDA_F16 = 1, ORDA_F32 = 2 };
+
+/* Divergences for the distillation term.  ORDA_DIV_FORWARD_KL is the only one
+ * the reference has (ops/tied_teacher.py:182,189); the others are additions
+ * selected by a keyword whose default keeps forward KL. */
+enum orda_divergence {
+  ORDA_DIV_FORWARD_KL = 0,
+  ORDA_DIV_REVERSE_KL = 1,
+  ORDA_DIV_SYMMETRIC_KL = 2,
+  ORDA_DIV_SOFT_TARGET_CE = 3,
+  ORDA_DIV_HELLINGER = 4,
+  ORDA_DIV_BHATTACHARYYA = 5,
+  ORDA_DIV_RENYI = 6,
+  ORDA_DIV_AMARI_ALPHA = 7,
+  ORDA_DIV_CHI_SQUARED = 8,
+  ORDA_DIV_SQUARED_L2 = 9,
+  ORDA_DIV_AB = 10,
+  ORDA_DIV_JSD = 11,
+  ORDA_DIV_SKEW_FORWARD_KL = 12,
+  ORDA_DIV_SKEW_REVERSE_KL = 13,
+  ORDA_DIV_TVD = 14,
+  ORDA_DIV_COUNT = 15
+};
+
+/* Problem flags. */
+#define ORDA_NEED_GRAD_STUDENT_HIDDEN (1u << 0)
+#define ORDA_NEED_GRAD_WEIGHT (1u << 1)
+#define ORDA_NEED_GRAD_TEACHER_HIDDEN (1u << 2)
+#define ORDA_NEED_GRAD_TEACHER_WEIGHT (1u << 3)
+#define ORDA_COMPUTE_TEACHER_CE (1u << 4) /* teacher CE value (and its grads) */
+#define ORDA_COMPUTE_DIVERGENCE (1u << 5) /* kl_weight != 0                  */
+#define ORDA_REDUCTION_SUM (1u << 6)      /* else mean                        */
+
+/* Error codes. */
+#define ORDA_OK 0
+#define ORDA_EINVAL (-1)
+#define ORDA_EWORKSPACE (-2)
+#define ORDA_ELAUNCH (-3)
+#define ORDA_EUNSUPPORTED (-4)
+
+/* Shapes, dtypes and scalar arguments of one loss evaluation. */
+typedef struct orda_problem {
+  int32_t abi_version;    /* must equal ORDA_ABI_VERSION                      */
+  int32_t mode;           /* enum orda_mode                                   */
+  int32_t dtype;          /* compute dtype of hidden states and weights       */
+  int32_t logits_dtype;   /* dtype of teacher logits (PRECOMPUTED_LOGITS)     */
+  int64_t n_rows;         /* N = batch x sequence                             */
+  int64_t vocab;          /* V                                                */
+  int64_t hidden;         /* H of the student                                 */
+  int64_t teacher_hidden; /* H of the teacher (== hidden for TIED)            */
+  int64_t ignore_index;
+  int64_t vocab_chunk;    /* V columns per backward chunk; 0 = library choice */
+  uint32_t flags;         /* ORDA_* flags above                               */
+  int32_t divergence;     /* enum orda_divergence                             */
+  float temperature;      /* > 0                                              */
+  float student_ce_weight;
+  float teacher_ce_weight;
+  float kl_weight;
+  float div_alpha;        /* alpha of renyi, amari_alpha, ab, skew_*_kl       */
+  float div_beta;         /* beta of jsd and ab                               */
+} orda_problem_t;
+
+/* Tensors of one loss evaluation.  Unused pointers may be NULL. */
+typedef struct orda_tensors {
+  const void* student_hidden;  /* [N x H]   dtype                            */
+  const void* weight;          /* [V x H]   dtype                            */
+  const void* teacher_hidden;  /* [N x Ht]  dtype (TIED: Ht == H)            */
+  const void* teacher_weight;  /* [V x Ht]  dtype (SEPARATE / PRE_HIDDEN)    */
+  const void* teacher_logits;  /* [N x V]   logits_dtype (PRE_LOGITS)        */
+  const int64_t* labels;       /* [N]                                        */
+  /* forward outputs: fp32 scalars */
+  float* out_loss;
+  float* out_student_ce;
+  float* out_teacher_ce;
+  float* out_kl;
+  /* state kept from forward to backward: orda_saved_bytes() bytes          */
+  void* saved;
+  /* backward inputs / outputs */
+  const float* grad_output;      /* fp32 scalar, d(total)/d(loss)           */
+  void* grad_student_hidden;     /* [N x H]  dtype                          */
+  void* grad_weight;             /* [V x H]  dtype                          */
+  void* grad_teacher_hidden;     /* [N x Ht] dtype                          */
+  void* grad_teacher_weight;     /* [V x Ht] dtype                          */
+} orda_tensors_t;
+
+/* ABI version of the loaded library (ORDA_ABI_VERSION). */
+int orda_abi_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* orda_last_error(void);
+
+/* Bytes of the buffer that carries per-row statistics from orda_forward to
+ * orda_backward.  Replaces the tensors saved by ctx.save_for_backward at
+ * ops/tied_teacher.py:519 (and separate_teacher.py:696,971,
+ * precomputed_teacher.py:478); this build saves O(N) statistics instead of
+ * full gradients. */
+size_t orda_saved_bytes(const orda_problem_t* p);
+
+/* Scratch bytes orda_forward needs.  Replaces the per-chunk logits and loss
+ * buffers of ops/tied_teacher.py:356-358,444-445. */
+size_t orda_forward_workspace_bytes(const orda_problem_t* p);
+
+/* Scratch bytes orda_backward needs for p->vocab_chunk (0: library choice).
+ * Bounded by O(vocab_chunk x N + N x H): no [N x V] tensor is ever formed. */
+size_t orda_backward_workspace_bytes(const orda_problem_t* p);
+
+/* Forward: losses and per-row statistics.  Replaces the chunk loop of
+ * TiedCEFunction.forward (ops/tied_teacher.py:366-516),
+ * SeparateStudentCEFunction.forward (ops/separate_teacher.py:568-693),
+ * SeparateFullCEFunction.forward (ops/separate_teacher.py:828-968) and
+ * PrecomputedCEFunction.forward (ops/precomputed_teacher.py:358-475): the
+ * logits GEMMs (tied_teacher.py:444-445), the Triton row kernels
+ * (tied_teacher.py:13-189) and the loss reduction (tied_teacher.py:499-516).
+ * Writes out_loss/out_student_ce/out_teacher_ce/out_kl and `saved`. */
+int orda_forward(const orda_problem_t* p, const orda_tensors_t* t,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward: all requested gradients, already multiplied by
+ * grad_output * mean_scale.  Replaces the gradient GEMMs computed inside
+ * forward (ops/tied_teacher.py:468-495, separate_teacher.py:660-674,
+ * 919-948, precomputed_teacher.py:443-457) and the scaling in backward
+ * (ops/tied_teacher.py:531-564 and analogues).  Reads `saved` from the
+ * matching orda_forward call. */
+int orda_backward(const orda_problem_t* p, const orda_tensors_t* t,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Plain C = A * B^T with A [M x K], B [N x K] (both K-contiguous) and C
+ * [M x N] in `dtype`, fp32 accumulation (the engine behind every GEMM of the
+ * path).  Exposed for tests and for callers that want the MFMA engine alone;
+ * replaces nothing in the reference directly (it stands for the torch
+ * matmuls at ops/tied_teacher.py:445,473,493). */
+int orda_gemm_abt(int32_t dtype, int64_t M, int64_t N, int64_t K,
+                  const void* A, const void* B, void* C, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORDA_CE_H */

@@ -1,0 +1,507 @@
+// abi.hip -- the C ABI of liborda_ce.so (declared in include/orda_ce.h):
+// argument validation, the tile / workspace plan, and the launch sequences
+// of the forward and backward passes.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/orda_ce.h"
+#include "launch.hpp"
+#include "orda_core.hpp"
+
+using namespace orda;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+constexpr size_t kAlign = 256;
+inline size_t carve(size_t& off, size_t bytes) {
+  const size_t at = (off + kAlign - 1) / kAlign * kAlign;
+  off = at + bytes;
+  return at;
+}
+
+// Default staging budget of one backward vocabulary chunk.
+constexpr int64_t kDefaultStagingBytes = 512ll << 20;
+// Target number of workgroups of a forward scan launch.
+constexpr int64_t kScanTargetGroups = 2048;
+
+struct Plan {
+  int mode, dtype, eb, kelems;
+  int64_t N, V, H, Ht;
+  bool div_on, teacher_ce, two_pass, t1;
+  int tsrc, div, fam, npow;
+  float pa[3], pb[3];
+  // forward
+  int n_ttiles, n_vtiles, n_vranges, tiles_per_range;
+  size_t off_partial, off_labelx, off_rowv, fwd_bytes;
+  size_t saved_bytes;
+  // backward
+  bool need_gs, need_gw, need_gt, need_gwt;
+  bool w_dlt_s, w_dlt_t, w_dln_s, w_dln_t, bwd_teacher;
+  int bwd_tsrc;
+  int64_t NP, ldT, ldh, Vc, nchunks;
+  size_t off_hT, off_htT, off_dLT, off_dLNs, off_dLNt, off_WT, off_WtT, off_g32s, off_g32t, bwd_bytes;
+};
+
+constexpr int kScalFloats = 64;  // scalars at the head of the saved buffer
+
+int make_plan(const orda_problem_t* p, Plan& pl) {
+  if (!p) return fail(ORDA_EINVAL, "problem is NULL");
+  if (p->abi_version != ORDA_ABI_VERSION)
+    return fail(ORDA_EINVAL, "abi_version %d does not match library version %d", p->abi_version,
+                ORDA_ABI_VERSION);
+  if (p->mode < ORDA_MODE_TIED || p->mode > ORDA_MODE_PRECOMPUTED_HIDDEN)
+    return fail(ORDA_EINVAL, "unknown mode %d", p->mode);
+  if (p->dtype < ORDA_BF16 || p->dtype > ORDA_F32) return fail(ORDA_EINVAL, "unknown dtype %d", p->dtype);
+  if (p->n_rows <= 0 || p->vocab <= 0 || p->hidden <= 0)
+    return fail(ORDA_EINVAL, "n_rows, vocab and hidden must be > 0 (got %lld, %lld, %lld)",
+                (long long)p->n_rows, (long long)p->vocab, (long long)p->hidden);
+  if (p->n_rows > (1ll << 30) || p->vocab > (1ll << 30) || p->hidden > (1ll << 24))
+    return fail(ORDA_EINVAL, "shape too large");
+  if (!(p->temperature > 0.f) || !std::isfinite(p->temperature))
+    return fail(ORDA_EINVAL, "temperature must be > 0, got %g", (double)p->temperature);
+  if (p->student_ce_weight < 0.f || p->teacher_ce_weight < 0.f || p->kl_weight < 0.f)
+    return fail(ORDA_EINVAL, "loss weights must be >= 0");
+  if (p->divergence < 0 || p->divergence >= ORDA_DIV_COUNT)
+    return fail(ORDA_EINVAL, "unknown divergence %d", p->divergence);
+
+  pl.mode = p->mode;
+  pl.dtype = p->dtype;
+  pl.eb = p->dtype == ORDA_F32 ? 4 : 2;
+  pl.kelems = 16 / pl.eb;
+  pl.N = p->n_rows;
+  pl.V = p->vocab;
+  pl.H = p->hidden;
+  pl.Ht = (p->mode == ORDA_MODE_TIED) ? p->hidden : p->teacher_hidden;
+  pl.div_on = (p->flags & ORDA_COMPUTE_DIVERGENCE) != 0;
+  pl.teacher_ce = (p->flags & ORDA_COMPUTE_TEACHER_CE) != 0;
+  pl.t1 = p->temperature == 1.0f;
+  const bool need_teacher = pl.div_on || pl.teacher_ce;
+  if (!need_teacher) pl.tsrc = TSRC_NONE;
+  else if (p->mode == ORDA_MODE_TIED) pl.tsrc = TSRC_SHARED;
+  else if (p->mode == ORDA_MODE_PRECOMPUTED_LOGITS) pl.tsrc = TSRC_MEM;
+  else pl.tsrc = TSRC_SEP;
+  if (pl.tsrc == TSRC_SEP && pl.Ht <= 0) return fail(ORDA_EINVAL, "teacher_hidden must be > 0");
+  if (pl.tsrc == TSRC_MEM && (p->logits_dtype < ORDA_BF16 || p->logits_dtype > ORDA_F32))
+    return fail(ORDA_EINVAL, "unknown logits_dtype %d", p->logits_dtype);
+  if (pl.H % pl.kelems != 0)
+    return fail(ORDA_EINVAL, "hidden (%lld) must be a multiple of %d for this dtype", (long long)pl.H, pl.kelems);
+  if (pl.tsrc == TSRC_SEP && pl.Ht % pl.kelems != 0)
+    return fail(ORDA_EINVAL, "teacher_hidden (%lld) must be a multiple of %d for this dtype", (long long)pl.Ht,
+                pl.kelems);
+
+  // divergence
+  pl.div = pl.div_on ? p->divergence : -1;
+  pl.fam = pl.div_on ? div_family(p->divergence) : FAM_NONE;
+  pl.two_pass = pl.fam == FAM_TWO;
+  pl.npow = 0;
+  for (int i = 0; i < 3; ++i) pl.pa[i] = pl.pb[i] = 0.f;
+  const float a = p->div_alpha, b = p->div_beta;
+  if (pl.div_on) {
+    switch (p->divergence) {
+      case ORDA_DIV_HELLINGER: case ORDA_DIV_BHATTACHARYYA:
+        pl.npow = 1; pl.pa[0] = 0.5f; pl.pb[0] = 0.5f; break;
+      case ORDA_DIV_RENYI:
+        if (!(a > 0.f) || a == 1.f) return fail(ORDA_EINVAL, "renyi needs alpha > 0 and != 1, got %g", (double)a);
+        pl.npow = 1; pl.pa[0] = a; pl.pb[0] = 1.f - a; break;
+      case ORDA_DIV_AMARI_ALPHA:
+        if (a == 0.f || a == 1.f) return fail(ORDA_EINVAL, "amari_alpha needs alpha not in {0, 1}, got %g", (double)a);
+        pl.npow = 1; pl.pa[0] = a; pl.pb[0] = 1.f - a; break;
+      case ORDA_DIV_CHI_SQUARED:
+        pl.npow = 1; pl.pa[0] = 2.f; pl.pb[0] = -1.f; break;
+      case ORDA_DIV_SQUARED_L2:
+        pl.npow = 3; pl.pa[0] = 2.f; pl.pb[0] = 0.f; pl.pa[1] = 0.f; pl.pb[1] = 2.f; pl.pa[2] = 1.f; pl.pb[2] = 1.f;
+        break;
+      case ORDA_DIV_AB:
+        if (a == 0.f || b == 0.f || a + b == 0.f)
+          return fail(ORDA_EINVAL, "ab divergence needs alpha, beta, alpha+beta != 0");
+        pl.npow = 3; pl.pa[0] = a; pl.pb[0] = b; pl.pa[1] = a + b; pl.pb[1] = 0.f; pl.pa[2] = 0.f; pl.pb[2] = a + b;
+        break;
+      case ORDA_DIV_JSD:
+        if (!(b > 0.f && b < 1.f)) return fail(ORDA_EINVAL, "jsd needs 0 < beta < 1, got %g", (double)b);
+        break;
+      case ORDA_DIV_SKEW_FORWARD_KL: case ORDA_DIV_SKEW_REVERSE_KL:
+        if (!(a >= 0.f && a < 1.f)) return fail(ORDA_EINVAL, "skew divergences need 0 <= alpha < 1, got %g", (double)a);
+        break;
+      default: break;
+    }
+  }
+
+  // forward plan
+  pl.n_ttiles = (int)cdiv(pl.N, 128);
+  pl.n_vtiles = (int)cdiv(pl.V, 256);
+  int64_t nvr = cdiv(kScanTargetGroups, pl.n_ttiles);
+  if (nvr < 1) nvr = 1;
+  if (nvr > pl.n_vtiles) nvr = pl.n_vtiles;
+  pl.tiles_per_range = (int)cdiv(pl.n_vtiles, nvr);
+  pl.n_vranges = (int)cdiv(pl.n_vtiles, pl.tiles_per_range);
+  if ((int64_t)pl.n_ttiles * pl.n_vranges > 0x7fffffffll) return fail(ORDA_EINVAL, "grid too large");
+  size_t off = 0;
+  pl.off_partial = carve(off, (size_t)pl.n_vranges * kNStat * pl.N * 4);
+  pl.off_labelx = carve(off, (size_t)2 * pl.N * 4);
+  pl.off_rowv = carve(off, (size_t)3 * pl.N * 4);
+  pl.fwd_bytes = off + kAlign;
+  pl.saved_bytes = (size_t)kScalFloats * 4 + (size_t)kNRowP * pl.N * 4;
+
+  // backward plan
+  const uint32_t f = p->flags;
+  const bool tied = p->mode == ORDA_MODE_TIED, sep = p->mode == ORDA_MODE_SEPARATE;
+  pl.need_gs = (f & ORDA_NEED_GRAD_STUDENT_HIDDEN) != 0;
+  pl.need_gw = (f & ORDA_NEED_GRAD_WEIGHT) != 0;
+  pl.need_gt = (f & ORDA_NEED_GRAD_TEACHER_HIDDEN) != 0 && (tied || sep);
+  pl.need_gwt = (f & ORDA_NEED_GRAD_TEACHER_WEIGHT) != 0 && sep;
+  const bool tgrad = pl.teacher_ce && (tied || sep);
+  pl.w_dlt_s = pl.need_gw;
+  pl.w_dln_s = pl.need_gs;
+  pl.w_dlt_t = tgrad && ((tied && pl.need_gw) || (sep && pl.need_gwt));
+  pl.w_dln_t = tgrad && pl.need_gt;
+  pl.bwd_teacher = pl.w_dlt_t || pl.w_dln_t;
+  pl.bwd_tsrc = (pl.div_on || pl.bwd_teacher) ? pl.tsrc : TSRC_NONE;
+  if (pl.bwd_teacher && pl.tsrc == TSRC_NONE) pl.bwd_tsrc = tied ? TSRC_SHARED : TSRC_SEP;
+  pl.NP = round_up(pl.N, 8);
+  pl.ldT = pl.w_dlt_t ? 2 * pl.NP : pl.NP;
+  pl.ldh = (tied && pl.w_dlt_t) ? 2 * pl.NP : pl.NP;
+  const int64_t Vmax = round_up(pl.V, 256);
+  int64_t per_col = 0;
+  if (pl.w_dlt_s || pl.w_dlt_t) per_col += pl.ldT;
+  if (pl.w_dln_s) per_col += pl.N;
+  if (pl.w_dln_t) per_col += pl.N;
+  if (pl.need_gs || (tied && pl.w_dln_t)) per_col += pl.H;
+  if (sep && pl.w_dln_t) per_col += pl.Ht;
+  per_col *= pl.eb;
+  if (p->vocab_chunk > 0) {
+    pl.Vc = round_up(p->vocab_chunk, 256);
+  } else {
+    pl.Vc = per_col > 0 ? (kDefaultStagingBytes / per_col) / 256 * 256 : Vmax;
+  }
+  if (pl.Vc < 256) pl.Vc = 256;
+  if (pl.Vc > Vmax) pl.Vc = Vmax;
+  pl.nchunks = cdiv(pl.V, pl.Vc);
+  off = 0;
+  pl.off_hT = pl.need_gw ? carve(off, (size_t)pl.H * pl.ldh * pl.eb) : 0;
+  pl.off_htT = (sep && pl.w_dlt_t) ? carve(off, (size_t)pl.Ht * pl.NP * pl.eb) : 0;
+  pl.off_dLT = (pl.w_dlt_s || pl.w_dlt_t) ? carve(off, (size_t)pl.Vc * pl.ldT * pl.eb) : 0;
+  pl.off_dLNs = pl.w_dln_s ? carve(off, (size_t)pl.N * pl.Vc * pl.eb) : 0;
+  pl.off_dLNt = pl.w_dln_t ? carve(off, (size_t)pl.N * pl.Vc * pl.eb) : 0;
+  pl.off_WT = (pl.need_gs || (tied && pl.w_dln_t)) ? carve(off, (size_t)pl.H * pl.Vc * pl.eb) : 0;
+  pl.off_WtT = (sep && pl.w_dln_t) ? carve(off, (size_t)pl.Ht * pl.Vc * pl.eb) : 0;
+  pl.off_g32s = (pl.need_gs && pl.nchunks > 1) ? carve(off, (size_t)pl.N * pl.H * 4) : 0;
+  pl.off_g32t = (pl.w_dln_t && pl.nchunks > 1) ? carve(off, (size_t)pl.N * pl.Ht * 4) : 0;
+  pl.bwd_bytes = off + kAlign;
+  return ORDA_OK;
+}
+
+inline char* aligned_base(void* ws) {
+  const uintptr_t u = reinterpret_cast<uintptr_t>(ws);
+  return reinterpret_cast<char*>((u + kAlign - 1) / kAlign * kAlign);
+}
+
+inline bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+#define ORDA_CHECK_LAUNCH(expr)                                                        \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess) return fail(ORDA_ELAUNCH, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+template <class T>
+int run_forward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, char* ws, hipStream_t s) {
+  float* partial = reinterpret_cast<float*>(ws + pl.off_partial);
+  float* labelx = reinterpret_cast<float*>(ws + pl.off_labelx);
+  float* rowv = reinterpret_cast<float*>(ws + pl.off_rowv);
+  float* scal = static_cast<float*>(t->saved);
+  float* rowp = scal + kScalFloats;
+
+  LabelParams L{};
+  L.hs = t->student_hidden; L.W = t->weight; L.ht = t->teacher_hidden; L.Wt = t->teacher_weight;
+  L.Lt = t->teacher_logits; L.labels = t->labels;
+  L.N = pl.N; L.V = pl.V; L.H = pl.H; L.Ht = pl.Ht; L.ignore_index = p->ignore_index;
+  L.tsrc = pl.tsrc; L.lt_dtype = p->logits_dtype; L.out = labelx;
+  ORDA_CHECK_LAUNCH(launch_label<T>(L, s));
+
+  FusedParams F{};
+  F.W = t->weight; F.hs = t->student_hidden; F.ht = t->teacher_hidden; F.Wt = t->teacher_weight;
+  F.Lt = t->teacher_logits; F.labels = t->labels;
+  F.N = pl.N; F.V = pl.V; F.H = pl.H; F.Ht = pl.Ht; F.ignore_index = p->ignore_index;
+  F.tsrc = pl.tsrc; F.lt_dtype = p->logits_dtype;
+  F.div = pl.div; F.fam = pl.fam; F.t_is_one = pl.t1; F.tgrad = 0;
+  F.temperature = p->temperature; F.invT = 1.0f / p->temperature;
+  F.alpha = p->div_alpha; F.beta = p->div_beta;
+  F.log_alpha = std::log(p->div_alpha); F.log_1m_alpha = std::log1p(-p->div_alpha);
+  F.log_beta = std::log(p->div_beta); F.log_1m_beta = std::log1p(-p->div_beta);
+  for (int i = 0; i < 3; ++i) { F.pa[i] = pl.pa[i]; F.pb[i] = pl.pb[i]; }
+  F.npow = pl.npow;
+  F.phase = 0; F.n_ttiles = pl.n_ttiles; F.n_vranges = pl.n_vranges;
+  F.tiles_per_range = pl.tiles_per_range; F.n_vtiles = pl.n_vtiles;
+  F.partial = partial; F.rowp = rowp;
+  const int grid = pl.n_ttiles * pl.n_vranges;
+  ORDA_CHECK_LAUNCH(launch_scan<T>(F, grid, s));
+
+  MergeParams M{};
+  M.partial = partial; M.n_vranges = pl.n_vranges; M.N = pl.N; M.V = pl.V; M.ignore_index = p->ignore_index;
+  M.labels = t->labels; M.label_x = labelx; M.phase = 0; M.fam = pl.fam; M.div = pl.div;
+  M.t_is_one = pl.t1; M.has_t = pl.tsrc != TSRC_NONE; M.teacher_ce = pl.teacher_ce; M.div_on = pl.div_on;
+  M.invT = F.invT; M.temperature = p->temperature; M.alpha = p->div_alpha; M.beta = p->div_beta;
+  for (int i = 0; i < 3; ++i) { M.pa[i] = pl.pa[i]; M.pb[i] = pl.pb[i]; }
+  M.npow = pl.npow; M.rowp = rowp; M.rowv = rowv;
+  ORDA_CHECK_LAUNCH(launch_merge(M, s));
+
+  if (pl.two_pass) {
+    F.phase = 1;
+    ORDA_CHECK_LAUNCH(launch_scan<T>(F, grid, s));
+    M.phase = 1;
+    ORDA_CHECK_LAUNCH(launch_merge(M, s));
+  }
+
+  FinalizeParams Z{};
+  Z.rowv = rowv; Z.labels = t->labels; Z.N = pl.N; Z.ignore_index = p->ignore_index;
+  Z.reduction_sum = (p->flags & ORDA_REDUCTION_SUM) != 0;
+  Z.teacher_ce = pl.teacher_ce; Z.div_on = pl.div_on;
+  Z.w_s = p->student_ce_weight; Z.w_t = p->teacher_ce_weight; Z.w_kl = p->kl_weight;
+  Z.out_loss = t->out_loss; Z.out_ce_s = t->out_student_ce; Z.out_ce_t = t->out_teacher_ce; Z.out_kl = t->out_kl;
+  Z.scal = scal;
+  ORDA_CHECK_LAUNCH(launch_finalize(Z, s));
+  return ORDA_OK;
+}
+
+template <class T>
+int gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, float* C32, int64_t ldc, int64_t M,
+         int64_t N, int64_t K, int mode, hipStream_t s) {
+  GemmParams G{};
+  G.A = A; G.B = B; G.C = C; G.C32 = C32;
+  G.M = M; G.N = N; G.K = K; G.lda = lda; G.ldb = ldb; G.ldc = ldc;
+  G.tiles_m = (int)cdiv(M, 256); G.tiles_n = (int)cdiv(N, 256); G.mode = mode;
+  if ((int64_t)G.tiles_m * G.tiles_n > 0x7fffffffll) return fail(ORDA_EINVAL, "gemm grid too large");
+  ORDA_CHECK_LAUNCH(launch_gemm<T>(G, s));
+  return ORDA_OK;
+}
+
+#define ORDA_TRY(expr)      \
+  do {                      \
+    int rc_ = (expr);       \
+    if (rc_ != ORDA_OK) return rc_; \
+  } while (0)
+
+template <class T>
+int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, char* ws, hipStream_t s) {
+  const bool tied = pl.mode == ORDA_MODE_TIED, sep = pl.mode == ORDA_MODE_SEPARATE;
+  const int eb = pl.eb;
+  const int64_t N = pl.N, H = pl.H, Ht = pl.Ht, NP = pl.NP;
+  char* hT = ws + pl.off_hT;
+  char* htT = ws + pl.off_htT;
+  char* dLT = ws + pl.off_dLT;
+  char* dLNs = ws + pl.off_dLNs;
+  char* dLNt = ws + pl.off_dLNt;
+  char* WT = ws + pl.off_WT;
+  char* WtT = ws + pl.off_WtT;
+  float* g32s = reinterpret_cast<float*>(ws + pl.off_g32s);
+  float* g32t = reinterpret_cast<float*>(ws + pl.off_g32t);
+  float* scal = static_cast<float*>(t->saved);
+  float* rowp = scal + kScalFloats;
+
+  // Tied mode with teacher CE off: the teacher hidden gradient is zero
+  // (reference ops/tied_teacher.py:478-479).
+  if (tied && pl.need_gt && !pl.w_dln_t)
+    ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, H, N, 0, H, eb, s));
+
+  const bool any = pl.w_dlt_s || pl.w_dlt_t || pl.w_dln_s || pl.w_dln_t;
+  if (!any) return ORDA_OK;
+
+  // Transposed hidden states for the grad_W GEMMs (K = tokens), with zeroed
+  // padding columns so K can be rounded up to a multiple of 8.
+  if (pl.need_gw) {
+    ORDA_CHECK_LAUNCH(launch_zero2d(hT, pl.ldh, H, N, NP, eb, s));
+    ORDA_CHECK_LAUNCH(launch_transpose<T>(t->student_hidden, H, hT, pl.ldh, N, H, s));
+    if (tied && pl.w_dlt_t) {
+      ORDA_CHECK_LAUNCH(launch_zero2d(hT, pl.ldh, H, NP + N, 2 * NP, eb, s));
+      ORDA_CHECK_LAUNCH(launch_transpose<T>(t->teacher_hidden, H, hT + NP * eb, pl.ldh, N, H, s));
+    }
+  }
+  if (sep && pl.w_dlt_t) {
+    ORDA_CHECK_LAUNCH(launch_zero2d(htT, NP, Ht, N, NP, eb, s));
+    ORDA_CHECK_LAUNCH(launch_transpose<T>(t->teacher_hidden, Ht, htT, NP, N, Ht, s));
+  }
+  // padding columns of the staged dlogits (never written by the dL kernel)
+  if (pl.w_dlt_s || pl.w_dlt_t) ORDA_CHECK_LAUNCH(launch_zero2d(dLT, pl.ldT, pl.Vc, N, NP, eb, s));
+  if (pl.w_dlt_t) ORDA_CHECK_LAUNCH(launch_zero2d(dLT, pl.ldT, pl.Vc, NP + N, 2 * NP, eb, s));
+
+  FusedParams F{};
+  F.W = t->weight; F.hs = t->student_hidden; F.ht = t->teacher_hidden; F.Wt = t->teacher_weight;
+  F.Lt = t->teacher_logits; F.labels = t->labels;
+  F.N = N; F.V = pl.V; F.H = H; F.Ht = Ht; F.ignore_index = p->ignore_index;
+  F.tsrc = pl.bwd_tsrc; F.lt_dtype = p->logits_dtype;
+  F.div = pl.div; F.fam = pl.fam; F.t_is_one = pl.t1; F.tgrad = pl.bwd_teacher;
+  F.temperature = p->temperature; F.invT = 1.0f / p->temperature;
+  F.alpha = p->div_alpha; F.beta = p->div_beta;
+  F.log_alpha = std::log(p->div_alpha); F.log_1m_alpha = std::log1p(-p->div_alpha);
+  F.log_beta = std::log(p->div_beta); F.log_1m_beta = std::log1p(-p->div_beta);
+  F.n_ttiles = pl.n_ttiles; F.rowp = rowp;
+  F.w_s = p->student_ce_weight; F.w_t = p->teacher_ce_weight; F.w_kl = pl.div_on ? p->kl_weight : 0.f;
+  F.grad_output = t->grad_output; F.mean_scale = scal;
+  F.dLT = dLT; F.ldT = pl.ldT; F.tcol = NP; F.dLNs = dLNs; F.dLNt = dLNt; F.ldN = pl.Vc;
+  F.w_dlt_s = pl.w_dlt_s; F.w_dlt_t = pl.w_dlt_t; F.w_dln_s = pl.w_dln_s; F.w_dln_t = pl.w_dln_t;
+
+  const int64_t Kw = (tied && pl.w_dlt_t) ? 2 * NP : NP;
+  for (int64_t c = 0; c < pl.nchunks; ++c) {
+    const int64_t vc0 = c * pl.Vc;
+    const int64_t vcc = (pl.V - vc0 < pl.Vc) ? pl.V - vc0 : pl.Vc;
+    const int64_t vck = round_up(vcc, pl.kelems);  // K of the grad_hidden GEMMs
+    const int gmode = pl.nchunks == 1 ? GEMM_STORE
+                      : c == 0 ? GEMM_ACC_FIRST
+                      : c == pl.nchunks - 1 ? GEMM_ACC_LAST : GEMM_ACC;
+    const bool needWT = pl.need_gs || (tied && pl.w_dln_t);
+    if (needWT) {
+      ORDA_CHECK_LAUNCH(launch_transpose<T>(static_cast<const char*>(t->weight) + vc0 * H * eb, H, WT, pl.Vc, vcc, H, s));
+      if (vck > vcc) ORDA_CHECK_LAUNCH(launch_zero2d(WT, pl.Vc, H, vcc, vck, eb, s));
+    }
+    if (sep && pl.w_dln_t) {
+      ORDA_CHECK_LAUNCH(launch_transpose<T>(static_cast<const char*>(t->teacher_weight) + vc0 * Ht * eb, Ht, WtT, pl.Vc, vcc, Ht, s));
+      if (vck > vcc) ORDA_CHECK_LAUNCH(launch_zero2d(WtT, pl.Vc, Ht, vcc, vck, eb, s));
+    }
+    if (vck > vcc) {
+      if (pl.w_dln_s) ORDA_CHECK_LAUNCH(launch_zero2d(dLNs, pl.Vc, N, vcc, vck, eb, s));
+      if (pl.w_dln_t) ORDA_CHECK_LAUNCH(launch_zero2d(dLNt, pl.Vc, N, vcc, vck, eb, s));
+    }
+    F.vc0 = vc0; F.vcc = vcc;
+    const int grid = (int)(cdiv(vcc, 256) * pl.n_ttiles);
+    ORDA_CHECK_LAUNCH(launch_dl<T>(F, grid, s));
+
+    if (pl.need_gw) {
+      ORDA_TRY(gemm<T>(dLT, pl.ldT, hT, pl.ldh, static_cast<char*>(t->grad_weight) + vc0 * H * eb, nullptr, H, vcc,
+                       H, Kw, GEMM_STORE, s));
+    }
+    if (sep && pl.need_gwt && pl.w_dlt_t) {
+      ORDA_TRY(gemm<T>(dLT + NP * eb, pl.ldT, htT, NP, static_cast<char*>(t->grad_teacher_weight) + vc0 * Ht * eb,
+                       nullptr, Ht, vcc, Ht, NP, GEMM_STORE, s));
+    }
+    if (pl.need_gs) {
+      ORDA_TRY(gemm<T>(dLNs, pl.Vc, WT, pl.Vc, t->grad_student_hidden, g32s, H, N, H, vck, gmode, s));
+    }
+    if (pl.w_dln_t) {
+      ORDA_TRY(gemm<T>(dLNt, pl.Vc, tied ? WT : WtT, pl.Vc, t->grad_teacher_hidden, g32t, Ht, N, Ht, vck, gmode, s));
+    }
+  }
+  // separate mode, teacher weight grad requested but teacher CE off: zero
+  if (sep && pl.need_gwt && !pl.w_dlt_t)
+    ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_weight, Ht, pl.V, 0, Ht, eb, s));
+  if (sep && pl.need_gt && !pl.w_dln_t)
+    ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, Ht, N, 0, Ht, eb, s));
+  return ORDA_OK;
+}
+
+int check_operands(const Plan& pl, const orda_tensors_t* t) {
+  if (!t) return fail(ORDA_EINVAL, "tensors is NULL");
+  if (!t->student_hidden || !t->weight || !t->labels) return fail(ORDA_EINVAL, "student_hidden, weight and labels are required");
+  if (!aligned16(t->student_hidden) || !aligned16(t->weight)) return fail(ORDA_EINVAL, "student_hidden and weight must be 16-byte aligned");
+  if (pl.tsrc == TSRC_SHARED && !t->teacher_hidden) return fail(ORDA_EINVAL, "tied mode needs teacher_hidden");
+  if (pl.tsrc == TSRC_SEP && (!t->teacher_hidden || !t->teacher_weight))
+    return fail(ORDA_EINVAL, "teacher_hidden and teacher_weight are required");
+  if ((pl.tsrc == TSRC_SHARED || pl.tsrc == TSRC_SEP) && !aligned16(t->teacher_hidden))
+    return fail(ORDA_EINVAL, "teacher_hidden must be 16-byte aligned");
+  if (pl.tsrc == TSRC_SEP && !aligned16(t->teacher_weight)) return fail(ORDA_EINVAL, "teacher_weight must be 16-byte aligned");
+  if (pl.tsrc == TSRC_MEM && !t->teacher_logits) return fail(ORDA_EINVAL, "teacher_logits are required");
+  if (!t->saved) return fail(ORDA_EINVAL, "saved buffer is required");
+  return ORDA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int orda_abi_version(void) { return ORDA_ABI_VERSION; }
+
+const char* orda_last_error(void) { return g_err.c_str(); }
+
+size_t orda_saved_bytes(const orda_problem_t* p) {
+  Plan pl;
+  if (make_plan(p, pl) != ORDA_OK) return 0;
+  return pl.saved_bytes;
+}
+
+size_t orda_forward_workspace_bytes(const orda_problem_t* p) {
+  Plan pl;
+  if (make_plan(p, pl) != ORDA_OK) return 0;
+  return pl.fwd_bytes;
+}
+
+size_t orda_backward_workspace_bytes(const orda_problem_t* p) {
+  Plan pl;
+  if (make_plan(p, pl) != ORDA_OK) return 0;
+  return pl.bwd_bytes;
+}
+
+int orda_forward(const orda_problem_t* p, const orda_tensors_t* t, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  g_err.clear();
+  Plan pl;
+  ORDA_TRY(make_plan(p, pl));
+  ORDA_TRY(check_operands(pl, t));
+  if (!t->out_loss || !t->out_student_ce || !t->out_teacher_ce || !t->out_kl)
+    return fail(ORDA_EINVAL, "forward outputs are required");
+  if (!workspace || workspace_bytes < pl.fwd_bytes)
+    return fail(ORDA_EWORKSPACE, "forward workspace too small: need %zu bytes, got %zu", pl.fwd_bytes, workspace_bytes);
+  char* ws = aligned_base(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (pl.dtype) {
+    case ORDA_BF16: return run_forward<bf16>(pl, p, t, ws, s);
+    case ORDA_F16: return run_forward<f16>(pl, p, t, ws, s);
+    default: return run_forward<float>(pl, p, t, ws, s);
+  }
+}
+
+int orda_backward(const orda_problem_t* p, const orda_tensors_t* t, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  g_err.clear();
+  Plan pl;
+  ORDA_TRY(make_plan(p, pl));
+  ORDA_TRY(check_operands(pl, t));
+  if (!t->grad_output) return fail(ORDA_EINVAL, "grad_output is required");
+  if (pl.need_gs && !t->grad_student_hidden) return fail(ORDA_EINVAL, "grad_student_hidden is required");
+  if (pl.need_gw && !t->grad_weight) return fail(ORDA_EINVAL, "grad_weight is required");
+  if (pl.need_gt && !t->grad_teacher_hidden) return fail(ORDA_EINVAL, "grad_teacher_hidden is required");
+  if (pl.need_gwt && !t->grad_teacher_weight) return fail(ORDA_EINVAL, "grad_teacher_weight is required");
+  if (pl.bwd_bytes > 0 && (!workspace || workspace_bytes < pl.bwd_bytes))
+    return fail(ORDA_EWORKSPACE, "backward workspace too small: need %zu bytes, got %zu", pl.bwd_bytes, workspace_bytes);
+  char* ws = aligned_base(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (pl.dtype) {
+    case ORDA_BF16: return run_backward<bf16>(pl, p, t, ws, s);
+    case ORDA_F16: return run_backward<f16>(pl, p, t, ws, s);
+    default: return run_backward<float>(pl, p, t, ws, s);
+  }
+}
+
+int orda_gemm_abt(int32_t dtype, int64_t M, int64_t N, int64_t K, const void* A, const void* B, void* C,
+                  void* stream) {
+  g_err.clear();
+  if (M <= 0 || N <= 0 || K <= 0) return fail(ORDA_EINVAL, "M, N, K must be > 0");
+  if (!A || !B || !C) return fail(ORDA_EINVAL, "A, B and C are required");
+  if (dtype < ORDA_BF16 || dtype > ORDA_F32) return fail(ORDA_EINVAL, "unknown dtype %d", dtype);
+  const int kel = dtype == ORDA_F32 ? 4 : 8;
+  if (K % kel != 0) return fail(ORDA_EINVAL, "K must be a multiple of %d", kel);
+  if (!aligned16(A) || !aligned16(B)) return fail(ORDA_EINVAL, "A and B must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ORDA_BF16: return gemm<bf16>(A, K, B, K, C, nullptr, N, M, N, K, GEMM_STORE, s);
+    case ORDA_F16: return gemm<f16>(A, K, B, K, C, nullptr, N, M, N, K, GEMM_STORE, s);
+    default: return gemm<float>(A, K, B, K, C, nullptr, N, M, N, K, GEMM_STORE, s);
+  }
+}
+
+}  // extern "C"

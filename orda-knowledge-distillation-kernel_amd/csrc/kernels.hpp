@@ -1,0 +1,699 @@
+// kernels.hpp -- kernel templates of liborda_ce.so, instantiated once per
+// element type by kernels_{bf16,f16,f32}.hip.
+#pragma once
+
+#include "launch.hpp"
+#include "orda_core.hpp"
+
+namespace orda {
+
+// Per-element divergence gradient dD/dz_s (z = x/T) given normalised log
+// probabilities at temperature T and the row constants c[] from the merge.
+template <int DIV>
+__device__ __forceinline__ float div_grad(float lps, float lpt, float psT, float ptT,
+                                          const float* c, float alpha, float beta) {
+  if constexpr (DIV == DIV_FKL || DIV == DIV_SOFT) {
+    return psT - ptT;
+  } else if constexpr (DIV == DIV_RKL) {
+    return psT * (lps - lpt - c[0]);
+  } else if constexpr (DIV == DIV_SYM) {
+    return psT - ptT + psT * (lps - lpt - c[0]);
+  } else if constexpr (DIV == DIV_HELL) {
+    return -0.5f * (fexp(0.5f * (lpt + lps)) - psT * fexp(c[0]));
+  } else if constexpr (DIV == DIV_BHAT) {
+    return -0.5f * (fexp(0.5f * (lpt + lps) - c[0]) - psT);
+  } else if constexpr (DIV == DIV_RENYI) {
+    return -(fexp(alpha * lpt + (1.0f - alpha) * lps - c[0]) - psT);
+  } else if constexpr (DIV == DIV_AMARI) {
+    return -(fexp(alpha * lpt + (1.0f - alpha) * lps) - psT * fexp(c[0])) / alpha;
+  } else if constexpr (DIV == DIV_CHI2) {
+    return -(fexp(2.0f * lpt - lps) - psT * fexp(c[0]));
+  } else if constexpr (DIV == DIV_L2) {
+    return 2.0f * (psT * psT - psT * fexp(c[1])) - 2.0f * (ptT * psT - psT * fexp(c[2]));
+  } else if constexpr (DIV == DIV_AB) {
+    const float q1 = fexp(alpha * lpt + beta * lps);
+    const float q3 = fexp((alpha + beta) * lps);
+    return -((q1 - psT * fexp(c[0])) - (q3 - psT * fexp(c[2]))) / alpha;
+  } else if constexpr (DIV == DIV_JSD) {
+    const float lm = logaddexp(flog(beta) + lpt, flog(1.0f - beta) + lps);
+    return (1.0f - beta) * psT * (lps - lm - c[1]);
+  } else if constexpr (DIV == DIV_SKEW_F) {
+    const float lm = logaddexp(flog(alpha) + lpt, flog(1.0f - alpha) + lps);
+    return -(1.0f - alpha) * psT * (fexp(lpt - lm) - c[1]);
+  } else if constexpr (DIV == DIV_SKEW_R) {
+    const float lm = logaddexp(flog(alpha) + lps, flog(1.0f - alpha) + lpt);
+    return psT * (lps - lm - alpha * fexp(lps - lm) - c[0] + alpha * c[1]);
+  } else {  // DIV_TVD
+    const float sg = (psT > ptT) ? 1.0f : ((psT < ptT) ? -1.0f : 0.0f);
+    return 0.5f * psT * (sg - c[1]);
+  }
+}
+
+// ------------------------------------------------------------- shared GEMMs
+// Runs the logits GEMM of one fused tile: acc[.][0..1] = student logits
+// (W rows v0.. x hs rows t0..), acc[.][2..3] = teacher logits of the same
+// tokens (tied: same W, teacher hidden; separate: W_t x teacher hidden;
+// precomputed logits: loaded from memory).
+template <class T>
+__device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][4], char* lds, const FusedParams& P,
+                                             int64_t v0, int64_t t0) {
+  zero_acc(acc);
+  const T* W = static_cast<const T*>(P.W);
+  const T* hs = static_cast<const T*>(P.hs);
+  const int64_t arows = P.V - v0, brows = P.N - t0;
+  if (P.tsrc == TSRC_SHARED) {
+    const T* ht = static_cast<const T*>(P.ht);
+    mainloop<T, true, true>(acc, lds, W + v0 * P.H, P.H, arows, hs + t0 * P.H, P.H, brows,
+                            ht + t0 * P.H, P.H, brows, P.H);
+  } else {
+    mainloop<T, true, false>(acc, lds, W + v0 * P.H, P.H, arows, hs + t0 * P.H, P.H, brows,
+                             nullptr, 0, 0, P.H);
+    if (P.tsrc == TSRC_SEP) {
+      const T* Wt = static_cast<const T*>(P.Wt);
+      const T* ht = static_cast<const T*>(P.ht);
+      mainloop<T, false, true>(acc, lds, Wt + v0 * P.Ht, P.Ht, arows, nullptr, 0, 0,
+                               ht + t0 * P.Ht, P.Ht, brows, P.Ht);
+    } else if (P.tsrc == TSRC_MEM) {
+      // Teacher logits [N x V] from memory into the unused teacher half.
+      const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+      const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t t = t0 + wn * 64 + j * 32 + (lane & 31);
+        if (t >= P.N) continue;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int64_t v = v0 + wm * 128 + acc_row(mb, g * 4, lane);
+            const int64_t off = t * P.V + v;
+            float x[4];
+            if (P.lt_dtype == DT_F32) {
+              const float* src = static_cast<const float*>(P.Lt) + off;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x[e] = (v + e < P.V) ? src[e] : 0.f;
+            } else if (P.lt_dtype == DT_BF16) {
+              const bf16* src = static_cast<const bf16*>(P.Lt) + off;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x[e] = (v + e < P.V) ? (float)src[e] : 0.f;
+            } else {
+              const f16* src = static_cast<const f16*>(P.Lt) + off;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x[e] = (v + e < P.V) ? (float)src[e] : 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[mb][j + 2][g * 4 + e] = x[e];
+          }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- scan kernel
+// Phase 0: online softmax statistics of one token slot j over this tile's
+// 128 vocabulary rows held by the lane.  Template flags remove work that the
+// problem does not need.
+template <bool HAS_T, int FAM, bool T1, bool MASK>
+__device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][4], int j,
+                                          int vlane0, int64_t vlimit, const FusedParams& P) {
+  const float invT = P.invT;
+  float tms = -kInf, tmt = -kInf, tmu0 = -kInf, tmu1 = -kInf, tmu2 = -kInf;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
+      const float xs = acc[mb][j][r];
+      tms = fmaxf(tms, xs);
+      if (HAS_T) {
+        const float xt = acc[mb][j + 2][r];
+        tmt = fmaxf(tmt, xt);
+        if (FAM == FAM_POW) {
+          tmu0 = fmaxf(tmu0, P.pa[0] * xt + P.pb[0] * xs);
+          if (P.npow > 1) tmu1 = fmaxf(tmu1, P.pa[1] * xt + P.pb[1] * xs);
+          if (P.npow > 2) tmu2 = fmaxf(tmu2, P.pa[2] * xt + P.pb[2] * xs);
+        }
+      }
+    }
+  if (MASK && tms == -kInf) return;  // no valid vocabulary row in this lane
+
+  // rescale the running state to the new maxima
+  const float nms = fmaxf(S.ms, tms);
+  {
+    const float d = S.ms - nms;
+    const float cs = fexp(d);
+    const float csT = T1 ? cs : fexp(d * invT);
+    S.ss *= cs;
+    if (!T1) S.sst *= csT;
+    if (FAM == FAM_LIN) S.x[1] *= csT;
+    S.ms = nms;
+  }
+  float nmt = 0.f;
+  if (HAS_T) {
+    nmt = fmaxf(S.mt, tmt);
+    const float d = S.mt - nmt;
+    const float ct = fexp(d);
+    const float ctT = T1 ? ct : fexp(d * invT);
+    if (FAM == FAM_LIN) {
+      const float so = T1 ? S.st : S.stt;
+      S.x[0] *= ctT;
+      S.x[2] = (so == 0.f) ? 0.f : ctT * (S.x[2] + d * invT * so);
+    }
+    S.st *= ct;
+    if (!T1) S.stt *= ctT;
+    S.mt = nmt;
+  }
+  float nmu0 = 0.f, nmu1 = 0.f, nmu2 = 0.f;
+  if (FAM == FAM_POW) {
+    nmu0 = fmaxf(S.x[0], tmu0 * invT);
+    S.x[1] *= fexp(S.x[0] - nmu0);
+    S.x[0] = nmu0;
+    if (P.npow > 1) {
+      nmu1 = fmaxf(S.x[2], tmu1 * invT);
+      S.x[3] *= fexp(S.x[2] - nmu1);
+      S.x[2] = nmu1;
+    }
+    if (P.npow > 2) {
+      nmu2 = fmaxf(S.x[4], tmu2 * invT);
+      S.x[5] *= fexp(S.x[4] - nmu2);
+      S.x[4] = nmu2;
+    }
+  }
+
+  // accumulate this tile
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
+      const float xs = acc[mb][j][r];
+      const float es = fexp(xs - nms);
+      S.ss += es;
+      const float esT = T1 ? es : fexp((xs - nms) * invT);
+      if (!T1) S.sst += esT;
+      if (HAS_T) {
+        const float xt = acc[mb][j + 2][r];
+        const float et = fexp(xt - nmt);
+        S.st += et;
+        const float etT = T1 ? et : fexp((xt - nmt) * invT);
+        if (!T1) S.stt += etT;
+        if (FAM == FAM_LIN) {
+          const float zd = (xt - xs) * invT;
+          S.x[0] += etT * zd;
+          S.x[1] -= esT * zd;
+          S.x[2] += etT * ((xt - nmt) * invT);
+        }
+        if (FAM == FAM_POW) {
+          S.x[1] += fexp((P.pa[0] * xt + P.pb[0] * xs) * invT - nmu0);
+          if (P.npow > 1) S.x[3] += fexp((P.pa[1] * xt + P.pb[1] * xs) * invT - nmu1);
+          if (P.npow > 2) S.x[5] += fexp((P.pa[2] * xt + P.pb[2] * xs) * invT - nmu2);
+        }
+      }
+    }
+}
+
+// Phase 1 (two-pass divergences): sums of terms of the normalised
+// probabilities, given the row log-normalisers from phase 0.
+template <int DIV, bool MASK>
+__device__ __forceinline__ void rowsum_tile(RowState& S, const f32x16 (&acc)[4][4], int j,
+                                            int vlane0, int64_t vlimit, float lse_sT, float lse_tT,
+                                            const FusedParams& P) {
+  const float invT = P.invT;
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
+      const float lps = acc[mb][j][r] * invT - lse_sT;
+      const float lpt = acc[mb][j + 2][r] * invT - lse_tT;
+      const float ps = fexp(lps), pt = fexp(lpt);
+      if constexpr (DIV == DIV_JSD) {
+        const float lm = logaddexp(P.log_beta + lpt, P.log_1m_beta + lps);
+        s0 += pt * (lpt - lm);
+        s1 += ps * (lps - lm);
+      } else if constexpr (DIV == DIV_SKEW_F) {
+        const float lm = logaddexp(P.log_alpha + lpt, P.log_1m_alpha + lps);
+        s0 += pt * (lpt - lm);
+        s1 += ps * fexp(lpt - lm);
+      } else if constexpr (DIV == DIV_SKEW_R) {
+        const float lm = logaddexp(P.log_alpha + lps, P.log_1m_alpha + lpt);
+        s0 += ps * (lps - lm);
+        s1 += ps * fexp(lps - lm);
+      } else {  // TVD
+        s0 += fabsf(pt - ps);
+        s1 += (ps > pt) ? ps : ((ps < pt) ? -ps : 0.f);
+      }
+    }
+  S.x[0] += s0;
+  S.x[1] += s1;
+}
+
+// Exchange a RowState with lane l^32 of the same wave.
+__device__ __forceinline__ RowState shfl32(const RowState& s) {
+  RowState o;
+  o.ms = __shfl_xor(s.ms, 32); o.ss = __shfl_xor(s.ss, 32);
+  o.mt = __shfl_xor(s.mt, 32); o.st = __shfl_xor(s.st, 32);
+  o.sst = __shfl_xor(s.sst, 32); o.stt = __shfl_xor(s.stt, 32);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) o.x[i] = __shfl_xor(s.x[i], 32);
+  return o;
+}
+
+__device__ __forceinline__ void merge_any(RowState& a, const RowState& b, const FusedParams& P) {
+  if (P.phase == 1) {
+    a.x[0] += b.x[0];
+    a.x[1] += b.x[1];
+  } else {
+    state_merge(a, b, P.fam, P.t_is_one != 0, P.invT);
+  }
+}
+
+// Scan variants: which statistics a phase-0 tile accumulates.
+enum ScanVariant {
+  SV_STUDENT = 0,   // no teacher term
+  SV_TCE_T1 = 1,    // teacher softmax only (teacher CE / two-pass lse), T == 1
+  SV_TCE = 2,       // same, T != 1
+  SV_LIN_T1 = 3,    // forward/reverse/symmetric KL, soft CE, T == 1
+  SV_LIN = 4,       // same, T != 1
+  SV_POW = 5,       // power-sum divergences
+  SV_JSD = 6,       // phase 1 (second pass) of the two-pass divergences
+  SV_SKEW_F = 7,
+  SV_SKEW_R = 8,
+  SV_TVD = 9
+};
+
+template <int SV>
+__device__ __forceinline__ void scan_variant(RowState& S, const f32x16 (&acc)[4][4], int j, int vlane0,
+                                             int64_t vlimit, bool full, float lse_sT, float lse_tT,
+                                             const FusedParams& P) {
+  if constexpr (SV == SV_STUDENT) {
+    if (full) scan_tile<false, FAM_NONE, true, false>(S, acc, j, vlane0, vlimit, P);
+    else scan_tile<false, FAM_NONE, true, true>(S, acc, j, vlane0, vlimit, P);
+  } else if constexpr (SV == SV_TCE_T1) {
+    if (full) scan_tile<true, FAM_NONE, true, false>(S, acc, j, vlane0, vlimit, P);
+    else scan_tile<true, FAM_NONE, true, true>(S, acc, j, vlane0, vlimit, P);
+  } else if constexpr (SV == SV_TCE) {
+    if (full) scan_tile<true, FAM_NONE, false, false>(S, acc, j, vlane0, vlimit, P);
+    else scan_tile<true, FAM_NONE, false, true>(S, acc, j, vlane0, vlimit, P);
+  } else if constexpr (SV == SV_LIN_T1) {
+    if (full) scan_tile<true, FAM_LIN, true, false>(S, acc, j, vlane0, vlimit, P);
+    else scan_tile<true, FAM_LIN, true, true>(S, acc, j, vlane0, vlimit, P);
+  } else if constexpr (SV == SV_LIN) {
+    if (full) scan_tile<true, FAM_LIN, false, false>(S, acc, j, vlane0, vlimit, P);
+    else scan_tile<true, FAM_LIN, false, true>(S, acc, j, vlane0, vlimit, P);
+  } else if constexpr (SV == SV_POW) {
+    if (full) scan_tile<true, FAM_POW, false, false>(S, acc, j, vlane0, vlimit, P);
+    else scan_tile<true, FAM_POW, false, true>(S, acc, j, vlane0, vlimit, P);
+  } else {
+    constexpr int DIV = SV == SV_JSD ? DIV_JSD : SV == SV_SKEW_F ? DIV_SKEW_F : SV == SV_SKEW_R ? DIV_SKEW_R : DIV_TVD;
+    if (full) rowsum_tile<DIV, false>(S, acc, j, vlane0, vlimit, lse_sT, lse_tT, P);
+    else rowsum_tile<DIV, true>(S, acc, j, vlane0, vlimit, lse_sT, lse_tT, P);
+  }
+}
+
+template <class T, int SV>
+__global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  f32x16 acc[4][4];
+  constexpr bool kPhase1 = SV >= SV_JSD;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tt = blockIdx.x % P.n_ttiles;
+  const int vr = blockIdx.x / P.n_ttiles;
+  const int64_t t0 = (int64_t)tt * 128;
+  const int vt_begin = vr * P.tiles_per_range;
+  const int vt_end = min(vt_begin + P.tiles_per_range, P.n_vtiles);
+  RowState st[2];
+  state_init_fam(st[0], kPhase1 ? FAM_NONE : P.fam);
+  state_init_fam(st[1], kPhase1 ? FAM_NONE : P.fam);
+
+  int64_t tok[2];
+  float lse_sT[2] = {0.f, 0.f}, lse_tT[2] = {0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    tok[j] = t0 + wn * 64 + j * 32 + (lane & 31);
+    if (tok[j] < P.N) {
+      if (kPhase1) {
+        lse_sT[j] = P.rowp[1 * P.N + tok[j]];
+        lse_tT[j] = P.rowp[3 * P.N + tok[j]];
+      }
+    }
+  }
+
+  for (int vt = vt_begin; vt < vt_end; ++vt) {
+    const int64_t v0 = (int64_t)vt * 256;
+    // Opaque copy of the token base: keeps the compiler from hoisting every
+    // per-row operand address out of this loop (which costs ~250 VGPRs).
+    int64_t t0v = t0;
+    asm volatile("" : "+s"(t0v));
+    fused_logits<T>(acc, lds, P, v0, t0v);
+    const int vlane0 = wm * 128 + (lane >> 5) * 4;
+    const int64_t vlimit = P.V - v0;
+    const bool full = vlimit >= 256;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      scan_variant<SV>(st[j], acc, j, vlane0, vlimit, full, lse_sT[j], lse_tT[j], P);
+    }
+  }
+
+  // combine lane l with l^32, then the two waves sharing the tokens (wm 0/1)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const RowState o = shfl32(st[j]);
+    merge_any(st[j], o, P);
+  }
+  __syncthreads();
+  float* xch = reinterpret_cast<float*>(lds);  // [wn][j][kNStat][32]
+  if (wm == 1 && lane < 32) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float* d = xch + ((wn * 2 + j) * kNStat) * 32 + lane;
+      const float* s = reinterpret_cast<const float*>(&st[j]);
+#pragma unroll
+      for (int f = 0; f < kNStat; ++f) d[f * 32] = s[f];
+    }
+  }
+  __syncthreads();
+  if (wm == 0 && lane < 32) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      RowState o;
+      float* od = reinterpret_cast<float*>(&o);
+      const float* s = xch + ((wn * 2 + j) * kNStat) * 32 + lane;
+#pragma unroll
+      for (int f = 0; f < kNStat; ++f) od[f] = s[f * 32];
+      merge_any(st[j], o, P);
+      if (tok[j] < P.N) {
+        float* dst = P.partial + (int64_t)vr * kNStat * P.N + tok[j];
+        const float* sv = reinterpret_cast<const float*>(&st[j]);
+#pragma unroll
+        for (int f = 0; f < kNStat; ++f) dst[(int64_t)f * P.N] = sv[f];
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------- dlogits kernel
+template <class T, int DIV, bool T1>
+__device__ __forceinline__ void dl_tile(const f32x16 (&acc)[4][4], const FusedParams& P, int64_t v0,
+                                        int64_t t0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const float scale = P.grad_output[0] * P.mean_scale[0];
+  const float invT = P.invT;
+  const int64_t vend = min(P.V, P.vc0 + P.vcc);
+  T* dLT = static_cast<T*>(P.dLT);
+  T* dLNs = static_cast<T*>(P.dLNs);
+  T* dLNt = static_cast<T*>(P.dLNt);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t t = t0 + wn * 64 + j * 32 + (lane & 31);
+    if (t >= P.N) continue;
+    const int64_t y = P.labels[t];
+    const bool ignored = (y == P.ignore_index);
+    const int64_t yeff = (y >= 0 && y < P.V) ? y : 0;
+    const float lse_s = P.rowp[0 * P.N + t];
+    const float lse_sT = P.rowp[1 * P.N + t];
+    const float lse_t = P.rowp[2 * P.N + t];
+    const float lse_tT = P.rowp[3 * P.N + t];
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = P.rowp[(4 + i) * P.N + t];
+    const float sc_s = ignored ? 0.f : scale * P.w_s;
+    const float sc_t = ignored ? 0.f : scale * P.w_t;
+    const float sc_d = ignored ? 0.f : scale * P.w_kl * P.temperature;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t vg = v0 + wm * 128 + acc_row(mb, g * 4, lane);  // 4 consecutive rows
+        float gs[4], gt[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = g * 4 + e;
+          const int64_t v = vg + e;
+          const float xs = acc[mb][j][r];
+          const float onehot = (v == yeff) ? 1.f : 0.f;
+          const float ps1 = fexp(xs - lse_s);
+          float d = sc_s * (ps1 - onehot);
+          if (DIV >= 0) {
+            const float xt = acc[mb][j + 2][r];
+            const float lps = xs * invT - lse_sT;
+            const float lpt = xt * invT - lse_tT;
+            const float psT = T1 ? ps1 : fexp(lps);
+            const float ptT = fexp(lpt);
+            d += sc_d * div_grad<(DIV >= 0 ? DIV : 0)>(lps, lpt, psT, ptT, c, P.alpha, P.beta);
+          }
+          gs[e] = ignored ? 0.f : d;
+          if (P.tgrad) {
+            const float xt = acc[mb][j + 2][r];
+            gt[e] = ignored ? 0.f : sc_t * (fexp(xt - lse_t) - onehot);
+          } else {
+            gt[e] = 0.f;
+          }
+        }
+        const int64_t vl = vg - P.vc0;  // row inside the chunk
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (vg + e >= vend) continue;
+          if (P.w_dlt_s) dLT[(vl + e) * P.ldT + t] = from_f32<T>(gs[e]);
+          if (P.w_dlt_t) dLT[(vl + e) * P.ldT + P.tcol + t] = from_f32<T>(gt[e]);
+          if (P.w_dln_s) dLNs[t * P.ldN + vl + e] = from_f32<T>(gs[e]);
+          if (P.w_dln_t) dLNt[t * P.ldN + vl + e] = from_f32<T>(gt[e]);
+        }
+      }
+  }
+}
+
+template <class T, int DIV, bool T1>
+__global__ __launch_bounds__(kThreads) void k_dl(FusedParams P) {
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  f32x16 acc[4][4];
+  const int tt = blockIdx.x % P.n_ttiles;
+  const int vt = blockIdx.x / P.n_ttiles;
+  const int64_t t0 = (int64_t)tt * 128;
+  const int64_t v0 = P.vc0 + (int64_t)vt * 256;
+  fused_logits<T>(acc, lds, P, v0, t0);
+  dl_tile<T, DIV, T1>(acc, P, v0, t0);
+}
+
+// -------------------------------------------------------------- plain GEMM
+template <class T, int MODE>
+__device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[4][4], const GemmParams& P, int64_t m0,
+                                              int64_t n0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  // 32-bit offsets inside the tile; the tile base stays 64-bit.
+  T* C = static_cast<T*>(P.C) + m0 * P.ldc + n0;
+  float* C32 = P.C32 + m0 * P.ldc + n0;
+  const int ldc = (int)P.ldc;
+  const int mlim = (int)min<int64_t>(P.M - m0, 256), nlim = (int)min<int64_t>(P.N - n0, 256);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int n = acc_col0(nb, wn) + (lane & 31);
+      const int mrow0 = wm * 128 + mb * 32 + (lane >> 5) * 4;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = mrow0 + (r >> 2) * 8 + (r & 3);
+        if (m < mlim && n < nlim) {
+          const int o = m * ldc + n;
+          const float a = acc[mb][nb][r];
+          if (MODE == GEMM_STORE) C[o] = from_f32<T>(a);
+          else if (MODE == GEMM_ACC_FIRST) C32[o] = a;
+          else if (MODE == GEMM_ACC) C32[o] += a;
+          else C[o] = from_f32<T>(C32[o] + a);
+        }
+      }
+    }
+}
+
+template <class T>
+__global__ __launch_bounds__(kThreads) void k_gemm(GemmParams P) {
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  f32x16 acc[4][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tm = blockIdx.x % P.tiles_m;
+  const int tn = blockIdx.x / P.tiles_m;
+  const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
+  const T* A = static_cast<const T*>(P.A);
+  const T* B = static_cast<const T*>(P.B);
+  zero_acc(acc);
+  mainloop<T, true, true>(acc, lds, A + m0 * P.lda, P.lda, P.M - m0, B + n0 * P.ldb, P.ldb, P.N - n0,
+                          B + (n0 + 128) * P.ldb, P.ldb, P.N - n0 - 128, P.K);
+  switch (P.mode) {
+    case GEMM_STORE: gemm_epilogue<T, GEMM_STORE>(acc, P, m0, n0); break;
+    case GEMM_ACC_FIRST: gemm_epilogue<T, GEMM_ACC_FIRST>(acc, P, m0, n0); break;
+    case GEMM_ACC: gemm_epilogue<T, GEMM_ACC>(acc, P, m0, n0); break;
+    default: gemm_epilogue<T, GEMM_ACC_LAST>(acc, P, m0, n0); break;
+  }
+}
+
+// ---------------------------------------------------------------- transpose
+// out[c * ldo + r] = in[r * ldi + c] for r < R, c < C (64 x 64 LDS tiles).
+template <class T>
+__global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ in, int64_t ldi, T* __restrict__ out,
+                                                   int64_t ldo, int64_t R, int64_t C, int tiles_c) {
+  __shared__ T tile[64][65];
+  const int tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
+  const int64_t r0 = (int64_t)tr * 64, c0 = (int64_t)tc * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    if (r < R && c < C) tile[i][tx] = in[r * ldi + c];
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t c = c0 + i, r = r0 + tx;
+    if (r < R && c < C) out[c * ldo + r] = tile[tx][i];
+  }
+}
+
+// ------------------------------------------------------------ label logits
+// x_s[t, y_t] and x_t[t, y_t] (the logits at each row's label) as fp32 dot
+// products, one wave per row.  Labels outside [0, V) use class 0, as the
+// reference kernels do (ops/tied_teacher.py:42-44); ignored rows give 0.
+template <class T>
+__global__ __launch_bounds__(256) void k_label(LabelParams P) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= P.N) return;
+  const int64_t y = P.labels[t];
+  const int64_t yc = (y >= 0 && y < P.V) ? y : 0;
+  const bool ignored = (y == P.ignore_index);
+  float xs = 0.f, xt = 0.f;
+  if (!ignored) {
+    const T* a = static_cast<const T*>(P.hs) + t * P.H;
+    const T* b = static_cast<const T*>(P.W) + yc * P.H;
+    for (int64_t k = lane; k < P.H; k += 64) xs += to_f32(a[k]) * to_f32(b[k]);
+    if (P.tsrc == TSRC_SHARED || P.tsrc == TSRC_SEP) {
+      const T* c = static_cast<const T*>(P.ht) + t * P.Ht;
+      const T* d = static_cast<const T*>(P.tsrc == TSRC_SHARED ? P.W : P.Wt) + yc * P.Ht;
+      for (int64_t k = lane; k < P.Ht; k += 64) xt += to_f32(c[k]) * to_f32(d[k]);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    xs += __shfl_xor(xs, o);
+    xt += __shfl_xor(xt, o);
+  }
+  if (lane == 0) {
+    if (P.tsrc == TSRC_MEM && !ignored) {
+      const int64_t off = t * P.V + yc;
+      if (P.lt_dtype == DT_F32) xt = static_cast<const float*>(P.Lt)[off];
+      else if (P.lt_dtype == DT_BF16) xt = (float)static_cast<const bf16*>(P.Lt)[off];
+      else xt = (float)static_cast<const f16*>(P.Lt)[off];
+    }
+    P.out[t] = xs;
+    P.out[P.N + t] = xt;
+  }
+}
+
+// ------------------------------------------------------------- launchers
+// Scan variant for phase 0 (statistics) or phase 1 (two-pass row sums).
+inline int scan_variant_of(const FusedParams& P) {
+  if (P.phase == 1) {
+    switch (P.div) {
+      case DIV_JSD: return SV_JSD;
+      case DIV_SKEW_F: return SV_SKEW_F;
+      case DIV_SKEW_R: return SV_SKEW_R;
+      default: return SV_TVD;
+    }
+  }
+  if (P.tsrc == TSRC_NONE) return SV_STUDENT;
+  if (P.fam == FAM_LIN) return P.t_is_one ? SV_LIN_T1 : SV_LIN;
+  if (P.fam == FAM_POW) return SV_POW;
+  return P.t_is_one ? SV_TCE_T1 : SV_TCE;
+}
+
+template <class T>
+hipError_t launch_scan_t(const FusedParams& P, int grid, hipStream_t s);
+template <class T>
+hipError_t launch_dl_t(const FusedParams& P, int grid, hipStream_t s);
+
+#define ORDA_SCAN_CASE(T, SV) \
+  case SV: hipLaunchKernelGGL((k_scan<T, SV>), dim3(grid), dim3(kThreads), 0, s, P); break;
+#define ORDA_DL_CASE(T, D) \
+  case D: hipLaunchKernelGGL((k_dl<T, D, false>), dim3(grid), dim3(kThreads), 0, s, P); break;
+
+#define ORDA_INSTANTIATE_SCAN(T)                                                     \
+  template <> hipError_t launch_scan<T>(const FusedParams& P, int grid, hipStream_t s) { \
+    switch (scan_variant_of(P)) {                                                    \
+      ORDA_SCAN_CASE(T, SV_STUDENT)                                                  \
+      ORDA_SCAN_CASE(T, SV_TCE_T1)                                                   \
+      ORDA_SCAN_CASE(T, SV_TCE)                                                      \
+      ORDA_SCAN_CASE(T, SV_LIN_T1)                                                   \
+      ORDA_SCAN_CASE(T, SV_LIN)                                                      \
+      ORDA_SCAN_CASE(T, SV_POW)                                                      \
+      ORDA_SCAN_CASE(T, SV_JSD)                                                      \
+      ORDA_SCAN_CASE(T, SV_SKEW_F)                                                   \
+      ORDA_SCAN_CASE(T, SV_SKEW_R)                                                   \
+      ORDA_SCAN_CASE(T, SV_TVD)                                                      \
+      default: return hipErrorInvalidValue;                                          \
+    }                                                                                \
+    return hipGetLastError();                                                        \
+  }
+
+#define ORDA_INSTANTIATE_DL(T)                                                       \
+  template <> hipError_t launch_dl<T>(const FusedParams& P, int grid, hipStream_t s) {   \
+    const bool t1 = P.t_is_one != 0;                                                 \
+    switch (P.div) {                                                                 \
+      case -1: hipLaunchKernelGGL((k_dl<T, -1, true>), dim3(grid), dim3(kThreads), 0, s, P); break; \
+      case DIV_FKL:                                                                  \
+        if (t1) hipLaunchKernelGGL((k_dl<T, DIV_FKL, true>), dim3(grid), dim3(kThreads), 0, s, P); \
+        else hipLaunchKernelGGL((k_dl<T, DIV_FKL, false>), dim3(grid), dim3(kThreads), 0, s, P); \
+        break;                                                                       \
+      case DIV_SOFT:                                                                 \
+        if (t1) hipLaunchKernelGGL((k_dl<T, DIV_SOFT, true>), dim3(grid), dim3(kThreads), 0, s, P); \
+        else hipLaunchKernelGGL((k_dl<T, DIV_SOFT, false>), dim3(grid), dim3(kThreads), 0, s, P); \
+        break;                                                                       \
+      ORDA_DL_CASE(T, DIV_RKL)                                                       \
+      ORDA_DL_CASE(T, DIV_SYM)                                                       \
+      ORDA_DL_CASE(T, DIV_HELL)                                                      \
+      ORDA_DL_CASE(T, DIV_BHAT)                                                      \
+      ORDA_DL_CASE(T, DIV_RENYI)                                                     \
+      ORDA_DL_CASE(T, DIV_AMARI)                                                     \
+      ORDA_DL_CASE(T, DIV_CHI2)                                                      \
+      ORDA_DL_CASE(T, DIV_L2)                                                        \
+      ORDA_DL_CASE(T, DIV_AB)                                                        \
+      ORDA_DL_CASE(T, DIV_JSD)                                                       \
+      ORDA_DL_CASE(T, DIV_SKEW_F)                                                    \
+      ORDA_DL_CASE(T, DIV_SKEW_R)                                                    \
+      ORDA_DL_CASE(T, DIV_TVD)                                                       \
+      default: return hipErrorInvalidValue;                                          \
+    }                                                                                \
+    return hipGetLastError();                                                        \
+  }
+
+template <class T>
+hipError_t launch_gemm(const GemmParams& P, hipStream_t s) {
+  const int grid = P.tiles_m * P.tiles_n;
+  hipLaunchKernelGGL(k_gemm<T>, dim3(grid), dim3(kThreads), 0, s, P);
+  return hipGetLastError();
+}
+template <class T>
+hipError_t launch_transpose(const void* in, int64_t ldi, void* out, int64_t ldo, int64_t R, int64_t C,
+                            hipStream_t s) {
+  const int tiles_r = (int)((R + 63) / 64), tiles_c = (int)((C + 63) / 64);
+  hipLaunchKernelGGL(k_transpose<T>, dim3(tiles_r * tiles_c), dim3(256), 0, s, static_cast<const T*>(in), ldi,
+                     static_cast<T*>(out), ldo, R, C, tiles_c);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_label(const LabelParams& P, hipStream_t s) {
+  const int grid = (int)((P.N + 3) / 4);
+  hipLaunchKernelGGL(k_label<T>, dim3(grid), dim3(256), 0, s, P);
+  return hipGetLastError();
+}
+
+#define ORDA_INSTANTIATE_GEMM(T)                                                                     \
+  template hipError_t launch_gemm<T>(const GemmParams&, hipStream_t);                                \
+  template hipError_t launch_label<T>(const LabelParams&, hipStream_t);                              \
+  template hipError_t launch_transpose<T>(const void*, int64_t, void*, int64_t, int64_t, int64_t,    \
+                                          hipStream_t);
+
+}  // namespace orda

@@ -1,0 +1,118 @@
+// launch.hpp -- parameter blocks and launcher declarations shared between
+// the host entry points (abi.hip) and the per-dtype kernel objects.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace orda {
+
+enum DType { DT_BF16 = 0, DT_F16 = 1, DT_F32 = 2 };
+
+// Where a fused tile gets its teacher logits from.
+enum TeacherSource {
+  TSRC_NONE = 0,    // no teacher term (student CE only)
+  TSRC_SHARED = 1,  // teacher hidden x the student's W (tied mode)
+  TSRC_SEP = 2,     // teacher hidden x W_t (separate / precomputed hidden)
+  TSRC_MEM = 3      // precomputed logits [N x V]
+};
+
+enum GemmMode { GEMM_STORE = 0, GEMM_ACC_FIRST = 1, GEMM_ACC = 2, GEMM_ACC_LAST = 3 };
+
+struct FusedParams {
+  const void* W;
+  const void* hs;
+  const void* ht;
+  const void* Wt;
+  const void* Lt;
+  const int64_t* labels;
+  int64_t N, V, H, Ht, ignore_index;
+  int tsrc, lt_dtype;
+  int div;    // divergence code, -1 when the divergence is off
+  int fam;    // family of div (FAM_NONE when off)
+  int t_is_one;
+  int tgrad;  // dlogits of the teacher are needed (teacher CE gradients)
+  float invT, temperature, alpha, beta;
+  float log_alpha, log_1m_alpha, log_beta, log_1m_beta;
+  float pa[3], pb[3];
+  int npow;
+  // scan
+  int phase, n_ttiles, n_vranges, tiles_per_range, n_vtiles;
+  float* partial;     // [n_vranges][kNStat][N]
+  const float* rowp;  // [kNRowP][N]
+  // dlogits
+  int64_t vc0, vcc;
+  float w_s, w_t, w_kl;
+  const float* grad_output;
+  const float* mean_scale;
+  void* dLT;
+  int64_t ldT, tcol;
+  void* dLNs;
+  void* dLNt;
+  int64_t ldN;
+  int w_dlt_s, w_dlt_t, w_dln_s, w_dln_t;
+};
+
+struct GemmParams {
+  const void* A;
+  const void* B;
+  void* C;
+  float* C32;
+  int64_t M, N, K, lda, ldb, ldc;
+  int tiles_m, tiles_n, mode;
+};
+
+struct LabelParams {
+  const void* hs;
+  const void* W;
+  const void* ht;
+  const void* Wt;
+  const void* Lt;
+  const int64_t* labels;
+  int64_t N, V, H, Ht, ignore_index;
+  int tsrc, lt_dtype;
+  float* out;  // [2][N]
+};
+
+template <class T> hipError_t launch_scan(const FusedParams& P, int grid, hipStream_t s);
+template <class T> hipError_t launch_dl(const FusedParams& P, int grid, hipStream_t s);
+template <class T> hipError_t launch_gemm(const GemmParams& P, hipStream_t s);
+template <class T> hipError_t launch_label(const LabelParams& P, hipStream_t s);
+template <class T>
+hipError_t launch_transpose(const void* in, int64_t ldi, void* out, int64_t ldo, int64_t R, int64_t C,
+                            hipStream_t s);
+
+// dtype-independent kernels (rows.hip)
+struct MergeParams {
+  const float* partial;
+  int n_vranges;
+  int64_t N, V, ignore_index;
+  const int64_t* labels;
+  const float* label_x;
+  int phase, fam, div, t_is_one, has_t, teacher_ce, div_on;
+  float invT, temperature, alpha, beta;
+  float pa[3], pb[3];
+  int npow;
+  float* rowp;  // [kNRowP][N]
+  float* rowv;  // [3][N]: student CE, teacher CE, T^2 * divergence
+};
+hipError_t launch_merge(const MergeParams& P, hipStream_t s);
+
+struct FinalizeParams {
+  const float* rowv;
+  const int64_t* labels;
+  int64_t N, ignore_index;
+  int reduction_sum, teacher_ce, div_on;
+  float w_s, w_t, w_kl;
+  float* out_loss;
+  float* out_ce_s;
+  float* out_ce_t;
+  float* out_kl;
+  float* scal;  // [0] = mean_scale, [1] = count of non-ignored rows
+};
+hipError_t launch_finalize(const FinalizeParams& P, hipStream_t s);
+
+// out[r * ld + c] = 0 for r < R, c0 <= c < c1 (element size esize bytes)
+hipError_t launch_zero2d(void* out, int64_t ld, int64_t R, int64_t c0, int64_t c1, int esize, hipStream_t s);
+
+}  // namespace orda

@@ -1,0 +1,184 @@
+// rows.hip -- per-row merge of partial statistics, the loss reduction, and a
+// 2-D zero fill.  These are O(N) kernels; the O(N V H) work is elsewhere.
+#include "launch.hpp"
+#include "orda_core.hpp"
+
+namespace orda {
+
+// One thread per token: merge the per-vocabulary-range partial states in a
+// fixed order (bit-stable), then form the row losses and the parameters the
+// dlogits kernel needs.  The final combination runs in fp64 to limit the
+// cancellation in lse_s - lse_t + (cross term).
+__global__ __launch_bounds__(256) void k_merge(MergeParams P) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= P.N) return;
+  const int64_t N = P.N;
+  const int64_t y = P.labels[t];
+  const bool ignored = (y == P.ignore_index);
+  const double T = P.temperature, invT = P.invT;
+
+  if (P.phase == 1) {
+    double x0 = 0.0, x1 = 0.0;
+    for (int vr = 0; vr < P.n_vranges; ++vr) {
+      const float* s = P.partial + (int64_t)vr * kNStat * N + t;
+      x0 += s[6 * N];
+      x1 += s[7 * N];
+    }
+    double D = 0.0, c0 = 0.0, c1 = 0.0;
+    switch (P.div) {
+      case DIV_JSD: D = P.beta * x0 + (1.0 - P.beta) * x1; c1 = x1; break;
+      case DIV_SKEW_F: D = x0; c1 = x1; break;
+      case DIV_SKEW_R: D = x0; c0 = x0; c1 = x1; break;
+      default: D = 0.5 * x0; c1 = x1; break;  // TVD
+    }
+    P.rowp[4 * N + t] = (float)c0;
+    P.rowp[5 * N + t] = (float)c1;
+    P.rowv[2 * N + t] = ignored ? 0.f : (float)(T * T * D);
+    return;
+  }
+
+  RowState S;
+  {
+    const float* s = P.partial + t;
+    float* d = reinterpret_cast<float*>(&S);
+    for (int f = 0; f < kNStat; ++f) d[f] = s[(int64_t)f * N];
+  }
+  for (int vr = 1; vr < P.n_vranges; ++vr) {
+    RowState o;
+    const float* s = P.partial + (int64_t)vr * kNStat * N + t;
+    float* d = reinterpret_cast<float*>(&o);
+    for (int f = 0; f < kNStat; ++f) d[f] = s[(int64_t)f * N];
+    state_merge(S, o, P.fam, P.t_is_one != 0, P.invT);
+  }
+  const bool t1 = P.t_is_one != 0;
+  const double lse_s = (double)S.ms + log((double)S.ss);
+  const double lse_sT = t1 ? lse_s : (double)S.ms * invT + log((double)S.sst);
+  double lse_t = 0.0, lse_tT = 0.0;
+  if (P.has_t) {
+    lse_t = (double)S.mt + log((double)S.st);
+    lse_tT = t1 ? lse_t : (double)S.mt * invT + log((double)S.stt);
+  }
+  const double ce_s = ignored ? 0.0 : lse_s - (double)P.label_x[t];
+  const double ce_t = (P.teacher_ce && !ignored) ? lse_t - (double)P.label_x[N + t] : 0.0;
+
+  double D = 0.0, c[4] = {0.0, 0.0, 0.0, 0.0};
+  if (P.div_on && P.fam != FAM_TWO) {
+    const double sst = t1 ? S.ss : S.sst, stt = t1 ? S.st : S.stt;
+    if (P.fam == FAM_LIN) {
+      const double fkl = (double)S.x[0] / stt - lse_tT + lse_sT;
+      const double rkl = (double)S.x[1] / sst - lse_sT + lse_tT;
+      switch (P.div) {
+        case DIV_FKL: D = fkl; break;
+        case DIV_RKL: D = rkl; c[0] = rkl; break;
+        case DIV_SYM: D = fkl + rkl; c[0] = rkl; break;
+        default: {  // soft-target CE: lse_s^T - sum p_t z_s
+          const double pt_zt = (double)S.x[2] / stt + (double)S.mt * invT;
+          D = lse_sT - (pt_zt - (double)S.x[0] / stt);
+        } break;
+      }
+    } else {  // FAM_POW: log P_i = LSE(u_i) - a_i lse_t^T - b_i lse_s^T
+      double lp[3] = {0.0, 0.0, 0.0};
+      for (int i = 0; i < P.npow; ++i)
+        lp[i] = (double)S.x[2 * i] + log((double)S.x[2 * i + 1]) - (double)P.pa[i] * lse_tT -
+                (double)P.pb[i] * lse_sT;
+      const double a = P.alpha, b = P.beta;
+      switch (P.div) {
+        case DIV_HELL: D = 1.0 - exp(lp[0]); break;
+        case DIV_BHAT: D = -lp[0]; break;
+        case DIV_RENYI: D = lp[0] / (a - 1.0); break;
+        case DIV_AMARI: D = (1.0 - exp(lp[0])) / (a * (1.0 - a)); break;
+        case DIV_CHI2: D = exp(lp[0]) - 1.0; break;
+        case DIV_L2: D = exp(lp[0]) + exp(lp[1]) - 2.0 * exp(lp[2]); break;
+        default:  // AB
+          D = -(exp(lp[0]) - a / (a + b) * exp(lp[1]) - b / (a + b) * exp(lp[2])) / (a * b);
+          break;
+      }
+      // row constants: log P_i, ordered as the dlogits formulas expect
+      if (P.div == DIV_L2) { c[0] = lp[0]; c[1] = lp[1]; c[2] = lp[2]; }
+      else if (P.div == DIV_AB) { c[0] = lp[0]; c[1] = lp[1]; c[2] = lp[2]; }
+      else c[0] = lp[0];
+    }
+  }
+  P.rowp[0 * N + t] = (float)lse_s;
+  P.rowp[1 * N + t] = (float)lse_sT;
+  P.rowp[2 * N + t] = (float)lse_t;
+  P.rowp[3 * N + t] = (float)lse_tT;
+  for (int i = 0; i < 4; ++i) P.rowp[(4 + i) * N + t] = (float)c[i];
+  P.rowv[0 * N + t] = (float)ce_s;
+  P.rowv[1 * N + t] = (float)ce_t;
+  P.rowv[2 * N + t] = (P.div_on && !ignored) ? (float)(T * T * D) : 0.f;
+}
+
+// Single workgroup: fixed-order fp64 sums of the row losses, the count of
+// non-ignored labels, the mean scale and the weighted loss
+// (reference ops/tied_teacher.py:499-516).
+__global__ __launch_bounds__(1024) void k_finalize(FinalizeParams P) {
+  __shared__ double red[4][1024];
+  const int tid = threadIdx.x;
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, cnt = 0.0;
+  for (int64_t t = tid; t < P.N; t += 1024) {
+    s0 += (double)P.rowv[t];
+    s1 += (double)P.rowv[P.N + t];
+    s2 += (double)P.rowv[2 * P.N + t];
+    cnt += (P.labels[t] != P.ignore_index) ? 1.0 : 0.0;
+  }
+  red[0][tid] = s0; red[1][tid] = s1; red[2][tid] = s2; red[3][tid] = cnt;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if (tid < w) {
+      for (int i = 0; i < 4; ++i) red[i][tid] += red[i][tid + w];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const double count = red[3][0];
+    const double denom = count < 1.0 ? 1.0 : count;
+    double ce_s = red[0][0], ce_t = red[1][0], kl = red[2][0];
+    float mean_scale = 1.0f;
+    if (!P.reduction_sum) {
+      ce_s /= denom; ce_t /= denom; kl /= denom;
+      mean_scale = 1.0f / (float)denom;
+    }
+    if (!P.teacher_ce) ce_t = 0.0;
+    if (!P.div_on) kl = 0.0;
+    const double loss = (double)P.w_s * ce_s + (double)P.w_t * ce_t + (double)P.w_kl * kl;
+    *P.out_loss = (float)loss;
+    *P.out_ce_s = (float)ce_s;
+    *P.out_ce_t = (float)ce_t;
+    *P.out_kl = (float)kl;
+    P.scal[0] = mean_scale;
+    P.scal[1] = (float)count;
+  }
+}
+
+__global__ void k_zero2d(char* out, int64_t ld_bytes, int64_t R, int64_t c0_bytes, int64_t w_bytes) {
+  const int64_t total = R * w_bytes;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / w_bytes, c = i % w_bytes;
+    out[r * ld_bytes + c0_bytes + c] = 0;
+  }
+}
+
+hipError_t launch_merge(const MergeParams& P, hipStream_t s) {
+  const int grid = (int)((P.N + 255) / 256);
+  hipLaunchKernelGGL(k_merge, dim3(grid), dim3(256), 0, s, P);
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize(const FinalizeParams& P, hipStream_t s) {
+  hipLaunchKernelGGL(k_finalize, dim3(1), dim3(1024), 0, s, P);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero2d(void* out, int64_t ld, int64_t R, int64_t c0, int64_t c1, int esize, hipStream_t s) {
+  if (R <= 0 || c1 <= c0) return hipSuccess;
+  const int64_t total = R * (c1 - c0) * esize;
+  int grid = (int)((total + 255) / 256);
+  if (grid > 4096) grid = 4096;
+  hipLaunchKernelGGL(k_zero2d, dim3(grid), dim3(256), 0, s, static_cast<char*>(out), ld * esize, R,
+                     c0 * esize, (c1 - c0) * esize);
+  return hipGetLastError();
+}
+
+}  // namespace orda

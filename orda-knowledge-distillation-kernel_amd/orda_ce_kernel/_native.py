@@ -1,0 +1,182 @@
+"""ctypes binding of liborda_ce.so (the C ABI in include/orda_ce.h).
+
+The library is built in-tree by ``csrc/Makefile`` into ``_lib/liborda_ce.so``.
+``ORDA_CE_LIBRARY`` may point at another build.  Nothing here falls back to
+another implementation: if the library is missing, :func:`library` raises and
+the HIP path reports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+__all__ = [
+    "ABI_VERSION", "Problem", "Tensors", "library", "library_path", "forward", "backward",
+    "saved_bytes", "forward_workspace_bytes", "backward_workspace_bytes", "gemm_abt",
+    "MODE", "DTYPE", "FLAG",
+]
+
+ABI_VERSION = 1
+
+MODE = {"tied": 0, "separate": 1, "precomputed_logits": 2, "precomputed_hidden": 3}
+DTYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+FLAG = {
+    "need_grad_student_hidden": 1 << 0,
+    "need_grad_weight": 1 << 1,
+    "need_grad_teacher_hidden": 1 << 2,
+    "need_grad_teacher_weight": 1 << 3,
+    "compute_teacher_ce": 1 << 4,
+    "compute_divergence": 1 << 5,
+    "reduction_sum": 1 << 6,
+}
+
+
+class Problem(ctypes.Structure):
+    """orda_problem_t"""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("logits_dtype", ctypes.c_int32),
+        ("n_rows", ctypes.c_int64),
+        ("vocab", ctypes.c_int64),
+        ("hidden", ctypes.c_int64),
+        ("teacher_hidden", ctypes.c_int64),
+        ("ignore_index", ctypes.c_int64),
+        ("vocab_chunk", ctypes.c_int64),
+        ("flags", ctypes.c_uint32),
+        ("divergence", ctypes.c_int32),
+        ("temperature", ctypes.c_float),
+        ("student_ce_weight", ctypes.c_float),
+        ("teacher_ce_weight", ctypes.c_float),
+        ("kl_weight", ctypes.c_float),
+        ("div_alpha", ctypes.c_float),
+        ("div_beta", ctypes.c_float),
+    ]
+
+
+class Tensors(ctypes.Structure):
+    """orda_tensors_t"""
+
+    _fields_ = [
+        (name, ctypes.c_void_p)
+        for name in (
+            "student_hidden", "weight", "teacher_hidden", "teacher_weight", "teacher_logits", "labels",
+            "out_loss", "out_student_ce", "out_teacher_ce", "out_kl", "saved", "grad_output",
+            "grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight",
+        )
+    ]
+
+
+_LOCK = threading.Lock()
+_LIB = None
+
+
+def library_path() -> Path:
+    env = os.environ.get("ORDA_CE_LIBRARY")
+    if env:
+        return Path(env)
+    return Path(__file__).resolve().parent / "_lib" / "liborda_ce.so"
+
+
+def library() -> ctypes.CDLL:
+    """Load (once) and return liborda_ce.so; raise RuntimeError if missing."""
+    global _LIB
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        path = library_path()
+        if not path.exists():
+            raise RuntimeError(
+                f"liborda_ce.so not found at {path}; build it with `make -C csrc` "
+                "(or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(str(path))
+        P, T = ctypes.POINTER(Problem), ctypes.POINTER(Tensors)
+        lib.orda_abi_version.restype = ctypes.c_int
+        lib.orda_abi_version.argtypes = []
+        lib.orda_last_error.restype = ctypes.c_char_p
+        lib.orda_last_error.argtypes = []
+        for name in ("orda_saved_bytes", "orda_forward_workspace_bytes", "orda_backward_workspace_bytes"):
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_size_t
+            fn.argtypes = [P]
+        for name in ("orda_forward", "orda_backward"):
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [P, T, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.orda_gemm_abt.restype = ctypes.c_int
+        lib.orda_gemm_abt.argtypes = [
+            ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ]
+        version = lib.orda_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"liborda_ce.so ABI version {version}, expected {ABI_VERSION}")
+        _LIB = lib
+        return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = library().orda_last_error().decode("utf-8", "replace")
+        if rc == -1:
+            raise ValueError(f"{what}: {msg}")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def _size(fn_name: str, problem: Problem) -> int:
+    n = getattr(library(), fn_name)(ctypes.byref(problem))
+    if n == 0:
+        _check(-1, fn_name)
+    return int(n)
+
+
+def saved_bytes(problem: Problem) -> int:
+    return _size("orda_saved_bytes", problem)
+
+
+def forward_workspace_bytes(problem: Problem) -> int:
+    return _size("orda_forward_workspace_bytes", problem)
+
+
+def backward_workspace_bytes(problem: Problem) -> int:
+    return _size("orda_backward_workspace_bytes", problem)
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def forward(problem: Problem, tensors: Tensors, workspace: torch.Tensor) -> None:
+    rc = library().orda_forward(
+        ctypes.byref(problem), ctypes.byref(tensors), workspace.data_ptr(), workspace.numel(),
+        _stream(workspace.device),
+    )
+    _check(rc, "orda_forward")
+
+
+def backward(problem: Problem, tensors: Tensors, workspace: torch.Tensor | None, device: torch.device) -> None:
+    ptr = workspace.data_ptr() if workspace is not None else None
+    size = workspace.numel() if workspace is not None else 0
+    rc = library().orda_backward(ctypes.byref(problem), ctypes.byref(tensors), ptr, size, _stream(device))
+    _check(rc, "orda_backward")
+
+
+def gemm_abt(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """C = a @ b.T on the library's MFMA engine (a [M, K], b [N, K])."""
+    if a.dtype != b.dtype or a.dtype not in DTYPE:
+        raise ValueError("a and b must share a dtype among bf16, fp16, fp32")
+    a = a.contiguous()
+    b = b.contiguous()
+    M, K = a.shape
+    N = b.shape[0]
+    c = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    rc = library().orda_gemm_abt(DTYPE[a.dtype], M, N, K, a.data_ptr(), b.data_ptr(), c.data_ptr(), _stream(a.device))
+    _check(rc, "orda_gemm_abt")
+    return c

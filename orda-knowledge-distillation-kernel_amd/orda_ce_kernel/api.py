@@ -1,0 +1,400 @@
+"""Public API (reference ``api.py``): teacher descriptors, ``KernelConfig``,
+``DistillationLossOutput``, ``distillation_loss`` and ``DistillationLoss``.
+
+Backends
+--------
+``backend="auto"`` (default) runs the fused HIP kernels for HIP tensors and
+the unfused torch formulation for CPU tensors, as the reference does
+(``api.py:385-413``).  Unlike the reference, a HIP tensor never falls back
+silently: if ``liborda_ce.so`` cannot be loaded, ``auto`` raises.  With a
+``PrecomputedTeacher`` and ``teacher_ce_weight != 0`` the reference's
+``auto`` drops to torch; here the HIP path computes that case too.
+``backend="triton"`` is kept as the name of the kernel path (there is no
+Triton in this build; ``"hip"`` is an alias) and ``backend="torch"`` selects
+the unfused formulation explicitly.
+
+``divergence=`` (new, default ``"forward_kl"``) selects the distillation
+term; see :mod:`orda_ce_kernel.divergences`.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Literal, NamedTuple
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ._runtime import HAS_NATIVE, native_error
+from .divergences import Divergence, divergence_rows_torch, resolve_divergence
+from .utils.dispatcher import dynamic_chunk
+from .utils.resolver import DEFAULT_MAX_FUSED_SIZE, _is_auto_chunk_size, is_power_of_two
+
+Reduction = Literal["mean", "sum"]
+Profile = Literal["balanced", "debug"]
+Backend = Literal["auto", "triton", "hip", "torch"]
+
+__all__ = [
+    "DistillationLoss", "DistillationLossOutput", "KernelConfig", "PrecomputedTeacher", "SeparateTeacher",
+    "TiedTeacher", "distillation_loss",
+]
+
+
+# ── Teacher descriptors (reference api.py:21-52) ─────────────────────────────
+@dataclass(frozen=True)
+class TiedTeacher:
+    """Teacher hidden states that share the student's LM-head weight."""
+
+    hidden: torch.Tensor
+
+
+@dataclass(frozen=True)
+class SeparateTeacher:
+    """Teacher hidden states with the teacher's own LM-head weight."""
+
+    hidden: torch.Tensor
+    weight: torch.Tensor
+
+
+@dataclass(frozen=True)
+class PrecomputedTeacher:
+    """A frozen teacher: its logits, or its (hidden, weight) pair."""
+
+    logits: torch.Tensor | None = None
+    teacher_hidden: torch.Tensor | None = None
+    teacher_weight: torch.Tensor | None = None
+
+    def __post_init__(self):
+        with_logits = self.logits is not None
+        with_pair = self.teacher_hidden is not None or self.teacher_weight is not None
+        if with_logits and with_pair:
+            raise ValueError("PrecomputedTeacher: provide logits or (teacher_hidden, teacher_weight), not both")
+        if not with_logits and not with_pair:
+            raise ValueError("PrecomputedTeacher: must provide logits or (teacher_hidden, teacher_weight)")
+        if with_pair and (self.teacher_hidden is None or self.teacher_weight is None):
+            raise ValueError("PrecomputedTeacher: teacher_hidden and teacher_weight must both be provided")
+
+
+# ── Config and output types (reference api.py:56-76) ────────────────────────
+@dataclass(frozen=True)
+class KernelConfig:
+    """Tuning knobs.  ``chunk_size`` / ``num_chunks`` / ``max_chunks`` set the
+    backward staging chunks; ``max_fused_size`` is validated (power of two)
+    and otherwise unused; ``autotune`` is accepted and ignored (the gfx950
+    tile is fixed); gradients always accumulate in fp32, so
+    ``fp32_grad_weight_accumulation`` has nothing left to switch."""
+
+    fp32_grad_weight_accumulation: bool | None = None
+    chunk_size: int | Literal["auto", "dynamic"] | None = None
+    num_chunks: int | None = None
+    max_chunks: int | None = None
+    max_fused_size: int | None = None
+    kl_weight: float | None = None
+    kl_temperature: float | None = None
+    autotune: bool | None = None
+
+    @property
+    def effective_fp32_grad_weight_accumulation(self) -> bool:
+        return bool(self.fp32_grad_weight_accumulation)
+
+
+class DistillationLossOutput(NamedTuple):
+    loss: torch.Tensor
+    student_ce: torch.Tensor
+    teacher_ce: torch.Tensor
+    kl: torch.Tensor
+
+
+# ── Config resolution (reference api.py:80-141) ─────────────────────────────
+def _resolve_profile(profile: Profile) -> KernelConfig:
+    if profile not in ("balanced", "debug"):
+        raise ValueError(f"profile must be 'balanced' or 'debug', got {profile!r}")
+    return KernelConfig(
+        fp32_grad_weight_accumulation=(profile == "debug"),
+        max_fused_size=DEFAULT_MAX_FUSED_SIZE,
+        autotune=False,
+    )
+
+
+def _resolve_config(profile: Profile, config: KernelConfig | None) -> KernelConfig:
+    """Profile defaults overridden field by field by ``config``."""
+    base = _resolve_profile(profile)
+    if config is None:
+        return base
+    merged = {
+        name: getattr(base, name) if getattr(config, name) is None else getattr(config, name)
+        for name in KernelConfig.__dataclass_fields__
+    }
+    return KernelConfig(**merged)
+
+
+def _resolve_kl_config(config: KernelConfig, kl_weight: float, kl_temperature: float) -> tuple[float, float]:
+    weight = kl_weight if config.kl_weight is None else float(config.kl_weight)
+    temperature = kl_temperature if config.kl_temperature is None else float(config.kl_temperature)
+    return weight, temperature
+
+
+def _teacher_mode_and_tensors(teacher):
+    if isinstance(teacher, TiedTeacher):
+        return "tied", teacher.hidden, None, None
+    if isinstance(teacher, SeparateTeacher):
+        return "separate", teacher.hidden, teacher.weight, None
+    if isinstance(teacher, PrecomputedTeacher):
+        return "precomputed", teacher.teacher_hidden, teacher.teacher_weight, teacher.logits
+    raise TypeError("teacher must be TiedTeacher, SeparateTeacher, or PrecomputedTeacher")
+
+
+def _resolve_teacher_ce_weight(mode: str, teacher_ce_weight: float | None) -> float:
+    if teacher_ce_weight is not None:
+        return float(teacher_ce_weight)
+    return 1.0 if mode == "tied" else 0.0
+
+
+# ── Validation (reference api.py:145-265) ───────────────────────────────────
+def _validate_public_args(*, student_hidden, weight, labels, student_ce_weight, teacher_ce_weight, kl_weight,
+                          kl_temperature, reduction, backend, config) -> None:
+    if student_ce_weight < 0.0:
+        raise ValueError(f"student_ce_weight must be >= 0.0, got {student_ce_weight}")
+    if teacher_ce_weight is not None and teacher_ce_weight < 0.0:
+        raise ValueError(f"teacher_ce_weight must be >= 0.0, got {teacher_ce_weight}")
+    if kl_weight < 0.0:
+        raise ValueError(f"kl_weight must be >= 0.0, got {kl_weight}")
+    if kl_temperature <= 0.0:
+        raise ValueError(f"kl_temperature must be > 0.0, got {kl_temperature}")
+    if reduction not in ("mean", "sum"):
+        raise ValueError(f"reduction must be 'mean' or 'sum', got {reduction!r}")
+    if backend not in ("auto", "triton", "hip", "torch"):
+        raise ValueError(f"backend must be 'auto', 'triton', 'hip', or 'torch', got {backend!r}")
+    if student_hidden.ndim != 2:
+        raise ValueError(f"student_hidden must be 2D, got shape={tuple(student_hidden.shape)}")
+    BT, H = student_hidden.shape
+    if weight.ndim != 2 or weight.shape[1] != H:
+        raise ValueError(f"weight must have shape (vocab, {H}), got {tuple(weight.shape)}")
+    if labels.shape != (BT,):
+        raise ValueError(f"labels must have shape ({BT},), got {tuple(labels.shape)}")
+    if labels.dtype != torch.long:
+        raise ValueError(f"labels must have dtype torch.long, got {labels.dtype}")
+    if config.max_chunks is not None and config.max_chunks < 1:
+        raise ValueError(f"config.max_chunks must be >= 1, got {config.max_chunks}")
+    if config.num_chunks is not None and config.num_chunks < 1:
+        raise ValueError(f"config.num_chunks must be >= 1, got {config.num_chunks}")
+    if config.num_chunks is not None and not _is_auto_chunk_size(config.chunk_size):
+        raise ValueError("config.chunk_size and config.num_chunks are mutually exclusive")
+    if config.num_chunks is not None and config.max_chunks is not None:
+        if min(int(config.num_chunks), BT) > config.max_chunks:
+            raise ValueError(
+                f"config.num_chunks must be <= config.max_chunks, got "
+                f"num_chunks={config.num_chunks}, max_chunks={config.max_chunks}"
+            )
+    if config.max_fused_size < 1:
+        raise ValueError(f"config.max_fused_size must be >= 1, got {config.max_fused_size}")
+    if not is_power_of_two(int(config.max_fused_size)):
+        raise ValueError(f"config.max_fused_size must be a power of two, got {config.max_fused_size}")
+
+
+def _validate_teacher(*, mode, teacher_hidden, teacher_weight, teacher_logits, student_hidden, weight) -> None:
+    BT, H = student_hidden.shape
+    V = weight.shape[0]
+    if mode == "tied":
+        if teacher_hidden.shape != (BT, H):
+            raise ValueError(f"TiedTeacher.hidden must have shape {(BT, H)}, got {tuple(teacher_hidden.shape)}")
+        return
+    if mode == "separate":
+        if teacher_hidden.ndim != 2 or teacher_hidden.shape[0] != BT:
+            raise ValueError(
+                f"SeparateTeacher.hidden must have shape (BT, teacher_hidden_dim), got {tuple(teacher_hidden.shape)}"
+            )
+        if teacher_weight.shape != (V, teacher_hidden.shape[1]):
+            raise ValueError(
+                f"SeparateTeacher.weight must have shape {(V, teacher_hidden.shape[1])}, "
+                f"got {tuple(teacher_weight.shape)}"
+            )
+        return
+    if teacher_logits is not None:
+        if teacher_logits.shape != (BT, V):
+            raise ValueError(
+                f"PrecomputedTeacher.logits must have shape {(BT, V)}, got {tuple(teacher_logits.shape)}"
+            )
+        if teacher_logits.requires_grad:
+            raise ValueError(
+                "PrecomputedTeacher.logits must not require gradients; use SeparateTeacher "
+                "when the teacher path needs gradients"
+            )
+        return
+    if teacher_hidden is None or teacher_weight is None:
+        raise ValueError("PrecomputedTeacher requires logits or (teacher_hidden, teacher_weight)")
+    if teacher_hidden.ndim != 2 or teacher_hidden.shape[0] != BT:
+        raise ValueError(
+            f"PrecomputedTeacher.teacher_hidden must have shape (BT, D_t), got {tuple(teacher_hidden.shape)}"
+        )
+    if teacher_weight.shape != (V, teacher_hidden.shape[1]):
+        raise ValueError(
+            f"PrecomputedTeacher.teacher_weight must have shape {(V, teacher_hidden.shape[1])}, "
+            f"got {tuple(teacher_weight.shape)}"
+        )
+    if teacher_hidden.requires_grad or teacher_weight.requires_grad:
+        raise ValueError("PrecomputedTeacher.teacher_hidden and teacher_weight must not require gradients")
+
+
+# ── Unfused torch formulation (reference api.py:274-335) ────────────────────
+def _torch_reference(*, student_hidden, weight, labels, teacher, student_ce_weight, teacher_ce_weight, kl_weight,
+                     kl_temperature, ignore_index, reduction, divergence: Divergence | None = None):
+    """Materialises full logits and lets autograd differentiate.  Used for
+    ``backend="torch"`` and CPU tensors; the divergence term is computed even
+    when ``kl_weight == 0`` (reported, not weighted), as in the reference."""
+    div = resolve_divergence(divergence)
+    mode, t_hidden, t_weight, t_logits = _teacher_mode_and_tensors(teacher)
+    logits_s = student_hidden @ weight.t()
+    if mode == "tied":
+        logits_t = t_hidden @ weight.t()
+    elif mode == "separate":
+        logits_t = t_hidden @ t_weight.t()
+    elif t_logits is not None:
+        logits_t = t_logits.detach()
+    else:
+        logits_t = (t_hidden @ t_weight.t()).detach()
+
+    ce_s_rows = F.cross_entropy(logits_s, labels, ignore_index=ignore_index, reduction="none")
+    ce_t_rows = F.cross_entropy(logits_t, labels, ignore_index=ignore_index, reduction="none")
+    keep = labels != ignore_index
+    denom = keep.sum().clamp(min=1)
+
+    T = float(kl_temperature)
+    log_p_s = F.log_softmax(logits_s / T, dim=-1)
+    log_p_t = F.log_softmax(logits_t.detach() / T, dim=-1)
+    d_rows = (divergence_rows_torch(log_p_s, log_p_t, div) * (T * T)).masked_fill(~keep, 0.0)
+
+    if reduction == "mean":
+        student_ce, teacher_ce_all, kl = ce_s_rows.sum() / denom, ce_t_rows.sum() / denom, d_rows.sum() / denom
+    else:
+        student_ce, teacher_ce_all, kl = ce_s_rows.sum(), ce_t_rows.sum(), d_rows.sum()
+    teacher_ce = teacher_ce_all if teacher_ce_weight != 0.0 else student_ce.new_zeros(())
+    loss = student_ce_weight * student_ce + teacher_ce_weight * teacher_ce + kl_weight * kl
+    return DistillationLossOutput(loss, student_ce.detach(), teacher_ce.detach(), kl.detach())
+
+
+def _supports_native(student_hidden: torch.Tensor) -> bool:
+    return bool(HAS_NATIVE and student_hidden.device.type == "cuda")
+
+
+# ── Functional API (reference api.py:339-437) ───────────────────────────────
+@torch._dynamo.disable
+def distillation_loss(
+    student_hidden: torch.Tensor,
+    weight: torch.Tensor,
+    labels: torch.Tensor,
+    teacher: TiedTeacher | SeparateTeacher | PrecomputedTeacher,
+    *,
+    student_ce_weight: float = 1.0,
+    teacher_ce_weight: float | None = None,
+    kl_weight: float = 0.0,
+    kl_temperature: float = 1.0,
+    ignore_index: int = -100,
+    reduction: Reduction = "mean",
+    profile: Profile = "balanced",
+    backend: Backend = "auto",
+    config: KernelConfig | None = None,
+    divergence: str | Divergence = "forward_kl",
+) -> DistillationLossOutput:
+    """Fused LM-head CE + distillation loss.
+
+    ``loss = student_ce_weight * CE(student) + teacher_ce_weight * CE(teacher)
+    + kl_weight * T^2 * D(teacher || student)`` over non-ignored rows, mean or
+    sum.  ``teacher_ce_weight`` defaults to 1.0 for a tied teacher and 0.0
+    otherwise.  Only ``loss`` carries gradients.
+    """
+    resolved = _resolve_config(profile, config)
+    kl_w, kl_t = _resolve_kl_config(resolved, kl_weight, kl_temperature)
+    _validate_public_args(
+        student_hidden=student_hidden, weight=weight, labels=labels, student_ce_weight=student_ce_weight,
+        teacher_ce_weight=teacher_ce_weight, kl_weight=kl_w, kl_temperature=kl_t, reduction=reduction,
+        backend=backend, config=resolved,
+    )
+    div = resolve_divergence(divergence)
+    mode, t_hidden, t_weight, t_logits = _teacher_mode_and_tensors(teacher)
+    _validate_teacher(
+        mode=mode, teacher_hidden=t_hidden, teacher_weight=t_weight, teacher_logits=t_logits,
+        student_hidden=student_hidden, weight=weight,
+    )
+    w_t = _resolve_teacher_ce_weight(mode, teacher_ce_weight)
+    on_device = student_hidden.device.type == "cuda"
+
+    if backend == "triton" and mode == "precomputed" and w_t != 0.0:
+        raise ValueError("backend='triton' with PrecomputedTeacher requires teacher_ce_weight=0.0")
+    if backend == "torch" or (backend == "auto" and not on_device):
+        return _torch_reference(
+            student_hidden=student_hidden, weight=weight, labels=labels, teacher=teacher,
+            student_ce_weight=student_ce_weight, teacher_ce_weight=w_t, kl_weight=kl_w, kl_temperature=kl_t,
+            ignore_index=ignore_index, reduction=reduction, divergence=div,
+        )
+    if not _supports_native(student_hidden):
+        raise RuntimeError(
+            f"backend={backend!r} requires the HIP extension liborda_ce.so and CUDA/HIP tensors "
+            f"(device={student_hidden.device}, library: {native_error() or 'loaded'}); use backend='auto' "
+            "or backend='torch' for fallback execution"
+        )
+
+    common = dict(
+        student_ce_weight=student_ce_weight, ignore_index=ignore_index, reduction=reduction,
+        chunk_size=resolved.chunk_size, num_chunks=resolved.num_chunks,
+        use_fp32_accum=resolved.effective_fp32_grad_weight_accumulation, kl_weight=kl_w, kl_temperature=kl_t,
+        max_chunks=resolved.max_chunks, max_fused_size=resolved.max_fused_size, autotune=resolved.autotune,
+        teacher_ce_weight=w_t, validate_labels=profile == "debug", divergence=div,
+    )
+    if mode == "precomputed" and w_t != 0.0:
+        from .ops.precomputed_teacher import precomputed_distillation_loss_with_teacher_ce
+        from .utils.resolver import resolve_chunk_size
+
+        cs, _ = resolve_chunk_size(
+            student_hidden.shape[0], resolved.chunk_size, V=weight.shape[0], max_chunks=resolved.max_chunks,
+            num_chunks=resolved.num_chunks,
+        )
+        common.pop("num_chunks")
+        common["chunk_size"] = cs
+        out = precomputed_distillation_loss_with_teacher_ce(
+            student_hidden, weight, t_logits, labels, teacher_hidden=t_hidden, teacher_weight=t_weight, **common
+        )
+        return DistillationLossOutput(*out)
+    out = dynamic_chunk(
+        student_hidden, t_hidden, weight, labels, teacher_mode=mode, teacher_weight=t_weight,
+        logits_teacher=t_logits, **common,
+    )
+    return DistillationLossOutput(*out)
+
+
+# ── Module wrapper (reference api.py:441-486) ───────────────────────────────
+class DistillationLoss(nn.Module):
+    def __init__(
+        self,
+        *,
+        student_ce_weight: float = 1.0,
+        teacher_ce_weight: float | None = None,
+        kl_weight: float = 0.0,
+        kl_temperature: float = 1.0,
+        ignore_index: int = -100,
+        reduction: Reduction = "mean",
+        profile: Profile = "balanced",
+        backend: Backend = "auto",
+        config: KernelConfig | None = None,
+        divergence: str | Divergence = "forward_kl",
+    ) -> None:
+        super().__init__()
+        self.student_ce_weight = student_ce_weight
+        self.teacher_ce_weight = teacher_ce_weight
+        self.kl_weight = kl_weight
+        self.kl_temperature = kl_temperature
+        self.ignore_index = ignore_index
+        self.reduction = reduction
+        self.profile = profile
+        self.backend = backend
+        self.config = config
+        self.divergence = divergence
+
+    def forward(self, student_hidden, weight, labels, teacher) -> DistillationLossOutput:
+        return distillation_loss(
+            student_hidden, weight, labels, teacher,
+            student_ce_weight=self.student_ce_weight, teacher_ce_weight=self.teacher_ce_weight,
+            kl_weight=self.kl_weight, kl_temperature=self.kl_temperature, ignore_index=self.ignore_index,
+            reduction=self.reduction, profile=self.profile, backend=self.backend, config=self.config,
+            divergence=self.divergence,
+        )

@@ -1,0 +1,238 @@
+"""Host side of the fused HIP path, shared by the four autograd Functions.
+
+Forward runs ``orda_forward``: the logits GEMMs with an online-softmax
+epilogue (no ``[N x V]`` tensor), per-row statistics and the loss scalars.
+Backward runs ``orda_backward``: it recomputes logits per vocabulary chunk,
+forms dlogits already scaled by ``grad_output * mean_scale`` and feeds the
+gradient GEMMs (fp32 accumulation).  The reference instead computes the
+gradients inside forward and scales them in backward
+(``ops/tied_teacher.py:468-495,531-564``); the results are the same, this
+order just never holds gradients that are not asked for.
+
+PyTorch allocates every buffer (outputs, the saved statistics, workspaces),
+so an out-of-memory error is a ``torch.cuda.OutOfMemoryError`` that the
+dispatcher's retry understands.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .. import _native
+from .._runtime import HAS_NATIVE, native_error
+from ..divergences import Divergence, resolve_divergence
+
+__all__ = ["FusedCall", "cast_to", "fused_forward", "fused_backward", "vocab_chunk_for", "require_native"]
+
+
+def require_native(entry: str) -> None:
+    """Raise RuntimeError when the HIP library cannot be used."""
+    if not HAS_NATIVE:
+        raise RuntimeError(
+            f"{entry} requires the HIP extension liborda_ce.so and HIP tensors "
+            f"({native_error()}). Use distillation_loss(..., backend='auto' or 'torch') for fallback execution."
+        )
+
+
+def vocab_chunk_for(BT: int, V: int, chunk_size, max_chunks) -> int:
+    """Vocabulary columns per backward chunk.
+
+    The reference splits the tokens into ``num_chunks`` chunks of logits
+    (``utils/resolver.py:28-62``); this build splits the vocabulary into the
+    same number of chunks, so the staging memory scales the same way with the
+    chunk settings and the OOM retry (which doubles ``num_chunks``) halves it.
+    """
+    from ..utils.resolver import resolve_chunk_size
+
+    _, num_chunks = resolve_chunk_size(BT, chunk_size, V=V, max_chunks=max_chunks)
+    return -(-int(V) // int(num_chunks))
+
+
+def _kelems(dtype: torch.dtype) -> int:
+    return 4 if dtype == torch.float32 else 8
+
+
+def _pad_cols(x: torch.Tensor, mult: int) -> torch.Tensor:
+    """Zero-pad the last dimension to a multiple of ``mult`` (zero columns do
+    not change any dot product) and make the base 16-byte aligned."""
+    pad = (-x.shape[-1]) % mult
+    if pad:
+        x = F.pad(x, (0, pad))
+    if x.data_ptr() % 16 != 0:
+        x = x.clone()
+    return x
+
+
+def _ptr(x: torch.Tensor | None):
+    return None if x is None else x.data_ptr()
+
+
+@dataclass
+class FusedCall:
+    """Everything one fused loss evaluation needs (built by the Functions)."""
+
+    mode: str                         # tied / separate / precomputed_logits / precomputed_hidden
+    student_hidden: torch.Tensor
+    weight: torch.Tensor
+    labels: torch.Tensor
+    teacher_hidden: torch.Tensor | None
+    teacher_weight: torch.Tensor | None
+    teacher_logits: torch.Tensor | None
+    student_ce_weight: float
+    teacher_ce_weight: float
+    kl_weight: float
+    kl_temperature: float
+    ignore_index: int
+    reduction: str
+    vocab_chunk: int
+    divergence: Divergence
+    compute_teacher_ce: bool
+    need_grad_student_hidden: bool
+    need_grad_weight: bool
+    need_grad_teacher_hidden: bool = False
+    need_grad_teacher_weight: bool = False
+
+
+def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None) -> _native.Problem:
+    flags = 0
+    if call.need_grad_student_hidden:
+        flags |= _native.FLAG["need_grad_student_hidden"]
+    if call.need_grad_weight:
+        flags |= _native.FLAG["need_grad_weight"]
+    if call.need_grad_teacher_hidden:
+        flags |= _native.FLAG["need_grad_teacher_hidden"]
+    if call.need_grad_teacher_weight:
+        flags |= _native.FLAG["need_grad_teacher_weight"]
+    if call.compute_teacher_ce:
+        flags |= _native.FLAG["compute_teacher_ce"]
+    if float(call.kl_weight) != 0.0:
+        flags |= _native.FLAG["compute_divergence"]
+    if call.reduction == "sum":
+        flags |= _native.FLAG["reduction_sum"]
+    div = call.divergence
+    p = _native.Problem()
+    p.abi_version = _native.ABI_VERSION
+    p.mode = _native.MODE[call.mode]
+    p.dtype = _native.DTYPE[call.student_hidden.dtype]
+    p.logits_dtype = _native.DTYPE[logits_dtype] if logits_dtype is not None else 0
+    p.n_rows = call.student_hidden.shape[0]
+    p.vocab = call.weight.shape[0]
+    p.hidden = H
+    p.teacher_hidden = Ht
+    p.ignore_index = int(call.ignore_index)
+    p.vocab_chunk = int(call.vocab_chunk)
+    p.flags = flags
+    p.divergence = div.code
+    p.temperature = float(call.kl_temperature)
+    p.student_ce_weight = float(call.student_ce_weight)
+    p.teacher_ce_weight = float(call.teacher_ce_weight) if call.compute_teacher_ce else 0.0
+    p.kl_weight = float(call.kl_weight)
+    p.div_alpha = float(div.alpha) if div.alpha is not None else 0.0
+    p.div_beta = float(div.beta) if div.beta is not None else 0.0
+    return p
+
+
+def fused_forward(ctx, call: FusedCall):
+    """Run the fused forward; stash what backward needs on ``ctx``.
+
+    Inputs must already be contiguous and in the compute dtype (the
+    Functions do that, as the reference does at ``ops/tied_teacher.py:334-344``).
+    Returns ``(loss, student_ce, teacher_ce, kl)`` as fp32 0-dim tensors.
+    """
+    require_native("the fused HIP path")
+    dev = call.student_hidden.device
+    if dev.type != "cuda":
+        raise ValueError(f"tensors must be CUDA/HIP tensors, got device={dev}")
+    call.divergence = resolve_divergence(call.divergence)
+    mult = _kelems(call.student_hidden.dtype)
+    H = call.student_hidden.shape[1]
+    hs = _pad_cols(call.student_hidden, mult)
+    w = _pad_cols(call.weight, mult)
+    ht = wt = lt = None
+    Ht = H
+    if call.mode == "tied":
+        ht = _pad_cols(call.teacher_hidden, mult)
+    elif call.mode in ("separate", "precomputed_hidden"):
+        Ht = call.teacher_hidden.shape[1]
+        ht = _pad_cols(call.teacher_hidden, mult)
+        wt = _pad_cols(call.teacher_weight, mult)
+    elif call.mode == "precomputed_logits":
+        lt = call.teacher_logits.contiguous()
+        if lt.dtype not in _native.DTYPE:
+            lt = lt.float()
+    labels = call.labels.contiguous()
+    Hp = hs.shape[1]
+    Htp = ht.shape[1] if (ht is not None and call.mode != "tied") else Hp
+    problem = _problem(call, Hp, Htp, lt.dtype if lt is not None else None)
+
+    saved = torch.empty(_native.saved_bytes(problem), dtype=torch.uint8, device=dev)
+    ws = torch.empty(_native.forward_workspace_bytes(problem), dtype=torch.uint8, device=dev)
+    outs = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(4)]
+    t = _native.Tensors()
+    t.student_hidden, t.weight, t.labels = _ptr(hs), _ptr(w), _ptr(labels)
+    t.teacher_hidden, t.teacher_weight, t.teacher_logits = _ptr(ht), _ptr(wt), _ptr(lt)
+    t.out_loss, t.out_student_ce, t.out_teacher_ce, t.out_kl = (o.data_ptr() for o in outs)
+    t.saved = saved.data_ptr()
+    _native.forward(problem, t, ws)
+    del ws
+
+    ctx.orda_problem = problem
+    ctx.orda_shapes = (H, Ht)
+    ctx.orda_mode = call.mode
+    ctx.save_for_backward(hs, w, ht, wt, lt, labels, saved)
+    return tuple(outs)
+
+
+def fused_backward(ctx, grad_output: torch.Tensor):
+    """Gradients ``(d_student_hidden, d_weight, d_teacher_hidden,
+    d_teacher_weight)`` in the compute dtype, unpadded; None where not needed."""
+    hs, w, ht, wt, lt, labels, saved = ctx.saved_tensors
+    problem = ctx.orda_problem
+    H, Ht = ctx.orda_shapes
+    flags = problem.flags
+    dev = hs.device
+    need = lambda name: bool(flags & _native.FLAG[name])  # noqa: E731
+    g_hs = torch.empty_like(hs) if need("need_grad_student_hidden") else None
+    g_w = torch.empty_like(w) if need("need_grad_weight") else None
+    g_ht = torch.empty_like(ht) if (need("need_grad_teacher_hidden") and ht is not None) else None
+    g_wt = torch.empty_like(wt) if (need("need_grad_teacher_weight") and wt is not None) else None
+    go = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()
+    ws_bytes = _native.backward_workspace_bytes(problem)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    t = _native.Tensors()
+    t.student_hidden, t.weight, t.labels = _ptr(hs), _ptr(w), _ptr(labels)
+    t.teacher_hidden, t.teacher_weight, t.teacher_logits = _ptr(ht), _ptr(wt), _ptr(lt)
+    t.saved = saved.data_ptr()
+    t.grad_output = go.data_ptr()
+    t.grad_student_hidden, t.grad_weight = _ptr(g_hs), _ptr(g_w)
+    t.grad_teacher_hidden, t.grad_teacher_weight = _ptr(g_ht), _ptr(g_wt)
+    _native.backward(problem, t, ws, dev)
+    del ws
+    if g_hs is not None and g_hs.shape[1] != H:
+        g_hs = g_hs[:, :H]
+    if g_w is not None and g_w.shape[1] != H:
+        g_w = g_w[:, :H]
+    ht_cols = H if ctx.orda_mode == "tied" else Ht
+    if g_ht is not None and g_ht.shape[1] != ht_cols:
+        g_ht = g_ht[:, :ht_cols]
+    if g_wt is not None and g_wt.shape[1] != Ht:
+        g_wt = g_wt[:, :Ht]
+    return g_hs, g_w, g_ht, g_wt
+
+
+def cast_to(grad: torch.Tensor | None, dtype: torch.dtype) -> torch.Tensor | None:
+    """Gradient in the dtype of the original input (the reference casts
+    grad_W to the weight dtype, ``ops/tied_teacher.py:545``)."""
+    if grad is None:
+        return None
+    return grad if grad.dtype == dtype else grad.to(dtype)
+
+
+def finite_or_raise(value: float, name: str) -> float:
+    value = float(value)
+    if math.isnan(value):
+        raise ValueError(f"{name} must not be NaN")
+    return value

@@ -1,0 +1,264 @@
+"""GPU parity: the HIP path (through the C ABI) against the float64 oracle.
+
+Inputs are generated on the CPU with a seeded generator, rounded to the
+compute dtype, and the oracle sees exactly those rounded values.  Tolerances
+loss components within 1e-3 relative (plus a small
+absolute floor for values near 0); gradients within atol/rtol 1e-2 of the
+float64 oracle for 16-bit inputs, 1e-4 for float32 inputs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.orda_oracle import distillation_loss_oracle
+
+pytestmark = pytest.mark.gpu
+
+DIVS = [
+    "forward_kl", "reverse_kl", "symmetric_kl", "soft_target_ce", "hellinger", "bhattacharyya", "renyi",
+    "amari_alpha", "chi_squared", "squared_l2", "ab", "jsd", "skew_forward_kl", "skew_reverse_kl", "tvd",
+]
+
+
+def _orda():
+    import orda_ce_kernel
+
+    assert orda_ce_kernel.is_available(), "liborda_ce.so must load on a HIP device"
+    return orda_ce_kernel
+
+
+def _make(seed, N, H, V, dtype, *, Ht=None, ignore_frac=0.05, h_std=1.0, w_std=0.02, t_noise=None):
+    g = torch.Generator().manual_seed(seed)
+    hs = torch.randn(N, H, generator=g) * h_std
+    if t_noise is not None:
+        ht = hs + t_noise * torch.randn(N, H, generator=g)
+    else:
+        ht = torch.randn(N, Ht or H, generator=g) * h_std
+    W = torch.randn(V, H, generator=g) * w_std
+    Wt = torch.randn(V, Ht or H, generator=g) * w_std
+    y = torch.randint(0, V, (N,), generator=g)
+    n_ign = int(round(ignore_frac * N))
+    if n_ign:
+        y[torch.randperm(N, generator=g)[:n_ign]] = -100
+    cast = lambda x: x.to(dtype)  # noqa: E731
+    return cast(hs), cast(ht), cast(W), cast(Wt), y
+
+
+def _np(x):
+    return x.detach().double().cpu().numpy()
+
+
+def _close_scalar(actual, expected, name, rtol=1e-3, atol=1e-5):
+    a = float(actual)
+    assert np.isfinite(a), f"{name} is not finite: {a}"
+    assert abs(a - expected) <= atol + rtol * abs(expected), f"{name}: got {a:.9g}, expected {expected:.9g}"
+
+
+def _close_grad(actual, expected, name, tol):
+    a = actual.detach().double().cpu().numpy()
+    assert np.all(np.isfinite(a)), f"{name} has non-finite values"
+    err = np.abs(a - expected)
+    bound = tol + tol * np.abs(expected)
+    worst = float((err - bound).max())
+    assert worst <= 0, f"{name}: max |err| {err.max():.3e} exceeds atol/rtol {tol:g}"
+
+
+def _grad_tol(dtype):
+    return 1e-4 if dtype == torch.float32 else 1e-2
+
+
+def _run(mode, dtype, *, N=96, H=64, V=1000, Ht=None, seed=0, reduction="mean", w_s=1.0, w_t=None, kl_w=0.5,
+         T=1.0, div="forward_kl", config=None, ignore_frac=0.05, grad_teacher=True, grad_output=1.0):
+    o = _orda()
+    hs, ht, W, Wt, y = _make(seed, N, H, V, dtype, Ht=Ht, ignore_frac=ignore_frac)
+    dev = "cuda"
+    hs_d = hs.to(dev).requires_grad_(True)
+    W_d = W.to(dev).requires_grad_(True)
+    y_d = y.to(dev)
+    kw = {}
+    if mode == "tied":
+        ht_d = ht.to(dev).requires_grad_(grad_teacher)
+        teacher = o.TiedTeacher(ht_d)
+        kw = dict(teacher_hidden=_np(ht))
+    elif mode == "separate":
+        ht_d = ht.to(dev).requires_grad_(grad_teacher)
+        Wt_d = Wt.to(dev).requires_grad_(grad_teacher)
+        teacher = o.SeparateTeacher(ht_d, Wt_d)
+        kw = dict(teacher_hidden=_np(ht), teacher_weight=_np(Wt))
+    elif mode == "precomputed_logits":
+        lt = (ht.float() @ Wt.float().t()).to(dtype)
+        teacher = o.PrecomputedTeacher(logits=lt.to(dev))
+        kw = dict(teacher_logits=_np(lt))
+    else:
+        teacher = o.PrecomputedTeacher(teacher_hidden=ht.to(dev), teacher_weight=Wt.to(dev))
+        kw = dict(teacher_hidden=_np(ht), teacher_weight=_np(Wt))
+    out = o.distillation_loss(
+        hs_d, W_d, y_d, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t, kl_weight=kl_w,
+        kl_temperature=T, reduction=reduction, backend="triton", config=config, divergence=div,
+    )
+    (out.loss * grad_output).backward()
+    omode = "precomputed" if mode.startswith("precomputed") else mode
+    ref = distillation_loss_oracle(
+        omode, _np(hs), _np(W), y.numpy(), student_ce_weight=w_s, teacher_ce_weight=w_t, kl_weight=kl_w,
+        kl_temperature=T, reduction=reduction, divergence=div, grad_output=grad_output,
+        teacher_grads=(w_t or 0.0) > 0 or mode == "tied", **kw,
+    )
+    torch.cuda.synchronize()
+    return out, ref, hs_d, W_d, teacher
+
+
+def _check(out, ref, hs_d, W_d, dtype, rtol=1e-3):
+    for name in ("loss", "student_ce", "teacher_ce", "kl"):
+        _close_scalar(getattr(out, name), ref[name], name, rtol=rtol)
+    tol = _grad_tol(dtype)
+    _close_grad(hs_d.grad, ref["grad_student_hidden"], "grad_student_hidden", tol)
+    _close_grad(W_d.grad, ref["grad_weight"], "grad_weight", tol)
+
+
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_tied_matches_oracle(dtype, reduction):
+    out, ref, hs, W, teacher = _run("tied", dtype, reduction=reduction, T=1.7, kl_w=0.35, w_s=0.8, w_t=0.25)
+    _check(out, ref, hs, W, dtype)
+    _close_grad(teacher.hidden.grad, ref["grad_teacher_hidden"], "grad_teacher_hidden", _grad_tol(dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("full", [False, True], ids=["student", "full"])
+def test_separate_matches_oracle(dtype, full):
+    out, ref, hs, W, teacher = _run("separate", dtype, Ht=96, T=2.0, w_t=1.0 if full else None, grad_teacher=full)
+    _check(out, ref, hs, W, dtype)
+    if full:
+        tol = _grad_tol(dtype)
+        _close_grad(teacher.hidden.grad, ref["grad_teacher_hidden"], "grad_teacher_hidden", tol)
+        _close_grad(teacher.weight.grad, ref["grad_teacher_weight"], "grad_teacher_weight", tol)
+    else:
+        assert teacher.hidden.grad is None and teacher.weight.grad is None
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("source", ["precomputed_logits", "precomputed_hidden"])
+def test_precomputed_matches_oracle(dtype, source):
+    out, ref, hs, W, _ = _run(source, dtype, Ht=48, T=4.0)
+    _check(out, ref, hs, W, dtype)
+
+
+@pytest.mark.parametrize("div", DIVS)
+@pytest.mark.parametrize("T", [1.0, 2.0])
+def test_every_divergence_matches_oracle_fp32(div, T):
+    out, ref, hs, W, _ = _run("tied", torch.float32, div=div, T=T, kl_w=0.7, N=64, V=700, H=32)
+    _check(out, ref, hs, W, torch.float32)
+
+
+@pytest.mark.parametrize("div", DIVS)
+def test_every_divergence_matches_oracle_bf16_precomputed(div):
+    out, ref, hs, W, _ = _run("precomputed_logits", torch.bfloat16, div=div, T=4.0, kl_w=1.0, N=64, V=700, H=64)
+    _check(out, ref, hs, W, torch.bfloat16)
+
+
+def test_config1_cpu_plumbing_shape_on_gpu():
+    """fp32, N=512, H=256, V=4096, tied, T=2, alpha 0.5."""
+    for w_t in (None, 0.0):
+        out, ref, hs, W, teacher = _run("tied", torch.float32, N=512, H=256, V=4096, T=2.0, w_s=0.5, kl_w=0.5,
+                                        w_t=w_t, seed=1001)
+        _check(out, ref, hs, W, torch.float32)
+
+
+def test_multi_chunk_backward_accumulates():
+    from orda_ce_kernel import KernelConfig
+
+    for cfg in (KernelConfig(num_chunks=4), KernelConfig(chunk_size=7)):
+        out, ref, hs, W, teacher = _run("tied", torch.bfloat16, V=1500, N=64, config=cfg, T=1.3)
+        _check(out, ref, hs, W, torch.bfloat16)
+        _close_grad(teacher.hidden.grad, ref["grad_teacher_hidden"], "grad_teacher_hidden", 1e-2)
+
+
+def test_ragged_shapes_and_padding():
+    # N not a multiple of 8, H not a multiple of 8 (host pads), V tiny and ragged
+    for N, H, V in ((9, 36, 17), (130, 40, 257), (1, 8, 5)):
+        out, ref, hs, W, _ = _run("tied", torch.bfloat16, N=N, H=H, V=V, T=1.4, ignore_frac=0.0)
+        _check(out, ref, hs, W, torch.bfloat16)
+
+
+def test_grad_output_scaling():
+    out, ref, hs, W, _ = _run("tied", torch.bfloat16, grad_output=3.5, reduction="sum")
+    _check(out, ref, hs, W, torch.bfloat16)
+
+
+def test_all_ignored_gives_exact_zeros():
+    o = _orda()
+    hs, ht, W, _, _ = _make(7, 16, 32, 300, torch.bfloat16)
+    hs, ht, W = (x.cuda().requires_grad_(True) for x in (hs, ht, W))
+    y = torch.full((16,), -100, dtype=torch.long, device="cuda")
+    out = o.distillation_loss(hs, W, y, o.TiedTeacher(ht), kl_weight=0.5, kl_temperature=1.7, backend="triton")
+    out.loss.backward()
+    for t in out:
+        assert torch.equal(t, torch.zeros_like(t))
+    for t in (hs.grad, ht.grad, W.grad):
+        assert torch.count_nonzero(t) == 0
+
+
+def test_kl_weight_zero_reports_exact_zero_kl():
+    out, ref, hs, W, _ = _run("separate", torch.float16, kl_w=0.0, Ht=48)
+    assert float(out.kl) == 0.0
+    _check(out, ref, hs, W, torch.float16)
+
+
+def test_teacher_ce_zero_keeps_teacher_grad_zero():
+    out, ref, hs, W, teacher = _run("tied", torch.float16, w_t=0.0, T=1.4)
+    assert torch.count_nonzero(teacher.hidden.grad) == 0
+    assert float(out.teacher_ce) == 0.0
+
+
+def test_out_of_range_label_counts_as_class_zero():
+    """Reference kernel quirk (ops/tied_teacher.py:42-44): without label
+    validation an out-of-range label is treated as class 0."""
+    o = _orda()
+    hs, ht, W, _, y = _make(3, 24, 32, 300, torch.float32, ignore_frac=0.0)
+    y[5] = 1000
+    hs_d, ht_d, W_d = (x.cuda().requires_grad_(True) for x in (hs, ht, W))
+    out = o.distillation_loss(hs_d, W_d, y.cuda(), o.TiedTeacher(ht_d), kl_weight=0.3, backend="triton")
+    out.loss.backward()
+    ref = distillation_loss_oracle("tied", _np(hs), _np(W), y.numpy(), teacher_hidden=_np(ht), kl_weight=0.3)
+    _check(out, ref, hs_d, W_d, torch.float32)
+
+
+def test_loss_is_bit_stable_across_runs():
+    o = _orda()
+    hs, ht, W, _, y = _make(11, 200, 128, 3000, torch.bfloat16)
+    args = (hs.cuda(), W.cuda(), y.cuda(), o.TiedTeacher(ht.cuda()))
+    a = o.distillation_loss(*args, kl_weight=1.0, backend="triton")
+    b = o.distillation_loss(*args, kl_weight=1.0, backend="triton")
+    for x, z in zip(a, b):
+        assert torch.equal(x, z)
+
+
+def test_identical_teacher_gives_zero_divergence():
+    o = _orda()
+    hs, _, W, _, y = _make(5, 64, 64, 900, torch.float32)
+    for div in DIVS:
+        if div == "soft_target_ce":  # cross-entropy: equals T^2 H(p_t) at p_s = p_t, not 0
+            continue
+        out = o.distillation_loss(hs.cuda(), W.cuda(), y.cuda(), o.TiedTeacher(hs.cuda()), kl_weight=1.0,
+                                  kl_temperature=1.3, backend="triton", divergence=div)
+        assert abs(float(out.kl)) < 2e-5, (div, float(out.kl))
+
+
+def test_gemm_engine_matches_torch():
+    from orda_ce_kernel import _native
+
+    g = torch.Generator().manual_seed(0)
+    for dtype in DTYPES:
+        for M, N, K in ((300, 270, 64), (256, 256, 512), (17, 513, 72), (1, 1, 8)):
+            a = torch.randn(M, K, generator=g).to(dtype)
+            b = torch.randn(N, K, generator=g).to(dtype)
+            c = _native.gemm_abt(a.cuda(), b.cuda()).float().cpu()
+            ref = a.double() @ b.double().t()
+            tol = 1e-4 if dtype == torch.float32 else 2e-2
+            err = (c.double() - ref).abs().max().item()
+            assert err <= tol * max(1.0, ref.abs().max().item()), (dtype, M, N, K, err)
