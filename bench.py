@@ -1,0 +1,304 @@
+#!/usr/bin/env python
+"""Benchmark: fused CE + distillation loss, forward + backward, on one MI355X.
+
+Default workload is BASELINE config 2 (tied teacher, bf16, N=8192 tokens
+(B=4 x T=2048), hidden 4096, vocab 128256, forward KL, T=1, kl_weight 1,
+student and teacher CE weight 1, gradients for student hidden and W; the
+teacher hidden is frozen).  A step is ``loss = distillation_loss(...);
+loss.backward()`` on inputs resident in HBM.  Prints ONE JSON line.
+
+Extra fields beyond the driver contract:
+  roofline      dominant kernel class: algorithmic flops per launch / mean
+                launch time (hipEvents recorded by the library on its launch
+                stream during the timed steps) against 2.5 PFLOP/s bf16
+  step_roofline whole step: algorithmic flops (5 x 2NVH at config 2) / step time
+  kernels       per kernel class: launches, ms per step, executed and
+                algorithmic TFLOP/s
+  peak_extra_hbm_gb  max_memory_allocated - memory_allocated before a step
+                (gradients count), the reference's own method
+  cpu_baseline  the oracle's unfused PyTorch restatement (fp32) on the
+                host cores, on a bounded token sample of the same workload
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "orda-knowledge-distillation-kernel_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "fwd+bwd tokens/s, CE+KL distill, h4096 V128256 bf16; peak extra HBM GB"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (mode, N, H, Ht, V, dtype, divergence, T, w_s, w_t, kl_w, ignore_frac)
+    "c1": ("tied", 512, 256, 256, 4096, "float32", "forward_kl", 2.0, 0.5, None, 0.5, 0.05),
+    "c2": ("tied", 8192, 4096, 4096, 128256, "bfloat16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
+    "c3": ("separate", 8192, 2048, 4096, 128256, "bfloat16", "reverse_kl", 2.0, 1.0, None, 1.0, 0.05),
+    "c3jsd": ("separate", 8192, 2048, 4096, 128256, "bfloat16", "jsd", 2.0, 1.0, None, 1.0, 0.05),
+    "c4": ("precomputed", 8192, 4096, 4096, 128256, "bfloat16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
+    "c5": ("tied", 32768, 5120, 5120, 152064, "bfloat16", "forward_kl", 1.0, 0.7, None, 0.3, 0.20),
+}
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(cfg, device, seed):
+    import torch
+
+    mode, N, H, Ht, V, dtype_name, *_rest, ignore_frac = cfg
+    dtype = getattr(torch, dtype_name)
+    g = torch.Generator(device=device).manual_seed(seed)
+    hs = torch.randn(N, H, generator=g, device=device).to(dtype)
+    if mode == "tied":
+        ht = torch.randn(N, H, generator=g, device=device).to(dtype)
+        Wt = None
+    else:
+        ht = torch.randn(N, Ht, generator=g, device=device).to(dtype)
+        Wt = (0.02 * torch.randn(V, Ht, generator=g, device=device)).to(dtype)
+    W = (0.02 * torch.randn(V, H, generator=g, device=device)).to(dtype)
+    y = torch.randint(0, V, (N,), generator=g, device=device)
+    n_ign = int(round(ignore_frac * N))
+    y[torch.randperm(N, generator=g, device=device)[:n_ign]] = -100
+    lt = None
+    if mode == "precomputed":
+        # teacher log-probs of N(0, 3) logits, stored bf16 (config 4)
+        lt = torch.empty(N, V, dtype=dtype, device=device)
+        for s in range(0, N, 1024):
+            e = min(N, s + 1024)
+            lt[s:e] = torch.log_softmax(3.0 * torch.randn(e - s, V, generator=g, device=device), -1).to(dtype)
+    return hs, ht, W, Wt, lt, y
+
+
+def algorithmic_flops(cfg) -> float:
+    """GEMM flops the reference's algorithm needs per step (no recompute):
+    forward one 2NVH per logits distribution; backward one per requested
+    grad_hidden and one per dlogits source feeding grad_W."""
+    mode, N, H, Ht, V = cfg[:5]
+    w_t = cfg[9]
+    G = lambda h: 2.0 * N * V * h  # noqa: E731
+    if mode == "tied":
+        teacher_ce = (1.0 if w_t is None else w_t) != 0.0
+        return G(H) * (2 + 1 + (2 if teacher_ce else 1))
+    if mode == "separate":
+        return G(Ht) + 3 * G(H)
+    return 3 * G(H)
+
+
+def run_gpu(cfg, steps, warmup, seed, timing):
+    import torch
+
+    import orda_ce_kernel as orda
+    from orda_ce_kernel import _native
+
+    mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, _ = cfg
+    device = "cuda"
+    hs, ht, W, Wt, lt, y = make_inputs(cfg, device, seed)
+    hs.requires_grad_(True)
+    W.requires_grad_(True)
+    if mode == "tied":
+        teacher = orda.TiedTeacher(ht)
+    elif mode == "separate":
+        teacher = orda.SeparateTeacher(ht, Wt)
+    else:
+        teacher = orda.PrecomputedTeacher(logits=lt)
+
+    def step():
+        out = orda.distillation_loss(hs, W, y, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t,
+                                     kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div)
+        out.loss.backward()
+        hs.grad = None
+        W.grad = None
+        return out
+
+    _log(f"[bench] warmup {warmup} step(s)")
+    for _ in range(max(warmup, 1)):
+        out = step()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    out = step()
+    torch.cuda.synchronize()
+    peak_extra = torch.cuda.max_memory_allocated() - base
+    loss_val = float(out.loss)
+    _log(f"[bench] loss={loss_val:.6f} peak extra {peak_extra / 1e9:.3f} GB; timing {steps} steps")
+
+    if timing:
+        _native.timing_enable(True)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern = _native.timing_collect() if timing else None
+    if timing:
+        _native.timing_enable(False)
+    ms_step = start.elapsed_time(stop) / steps
+    _log(f"[bench] {ms_step:.3f} ms/step (wall {wall * 1e3 / steps:.3f})")
+    return ms_step, peak_extra, loss_val, kern
+
+
+def kernel_report(kern, steps, peak_tflops):
+    rows = {}
+    for name, k in kern.items():
+        if k["launches"] == 0:
+            continue
+        sec = k["ms"] / 1e3
+        rows[name] = {
+            "launches_per_step": k["launches"] / steps,
+            "ms_per_step": k["ms"] / steps,
+            "mean_launch_ms": k["ms"] / k["launches"],
+            "executed_tflops": (k["executed_flops"] / sec / 1e12) if sec > 0 else 0.0,
+            "algorithmic_tflops": (k["algorithmic_flops"] / sec / 1e12) if sec > 0 else 0.0,
+            "executed_mfma_frac": (k["executed_flops"] / sec / 1e12 / peak_tflops) if sec > 0 else 0.0,
+        }
+    return rows
+
+
+def cpu_baseline(cfg, seed, budget_s):
+    """Time the oracle's unfused torch restatement (fp32) on a token sample."""
+    import torch
+
+    from oracle.torch_unfused import tied_forward_kl_loss
+
+    mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, _ = cfg
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    hs, ht, W, _, _, y = make_inputs(cfg, "cuda", seed)
+    Wc = W.float().cpu()
+    hs_c, ht_c, y_c = hs.float().cpu(), ht.float().cpu(), y.cpu()
+    del hs, ht, W
+    w_t_eff = 1.0 if w_t is None else w_t
+
+    Wc.requires_grad_(True)
+
+    def run(n):
+        a = hs_c[:n].clone().requires_grad_(True)
+        Wc.grad = None
+        t0 = time.perf_counter()
+        loss, *_ = tied_forward_kl_loss(a, ht_c[:n], Wc, y_c[:n], student_ce_weight=w_s,
+                                        teacher_ce_weight=w_t_eff, kl_weight=kl_w, kl_temperature=T)
+        loss.backward()
+        return time.perf_counter() - t0
+
+    run(16)  # warm up allocator and thread pool
+    probe = 64
+    t_probe = run(probe)
+    per_tok = t_probe / probe
+    n = int(max(probe, min(N, (budget_s / 3.0) / per_tok)))
+    n = max(probe, (n // 64) * 64)
+    times = [run(n) for _ in range(2)]
+    t = statistics.median(times)
+    cpu_name = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": n / t,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{n} of {N} tokens of the same workload (full V={V}, H={H}), fp32 unfused torch restatement "
+                   f"of the reference loss (oracle/torch_unfused.py), fwd+bwd, median of {len(times)} runs; "
+                   f"os.cpu_count()={os.cpu_count()}, {cpu_name}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--seed", type=int, default=1002)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-timing", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    cfg = CONFIGS[args.config]
+    mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, ignore_frac = cfg
+    ms_step, peak_extra, loss_val, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, not args.no_timing)
+    peak = PEAK_FP32_TFLOPS if dtype_name == "float32" else PEAK_BF16_TFLOPS
+    alg = algorithmic_flops(cfg)
+    step_tflops = alg / (ms_step / 1e3) / 1e12
+
+    result = {
+        "metric": METRIC,
+        "value": N / (ms_step / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"bfloat16": "bf16", "float32": "f32", "float16": "f16"}[dtype_name],
+        "data": "synthetic (seeded randn hidden/weights, uniform labels with ignore_index; no checkpoint)",
+        "config": {
+            "workload": f"{args.config}: {mode} teacher, N={N} tokens, hidden={H}"
+                        + (f", teacher hidden={Ht}" if mode != "tied" else "")
+                        + f", vocab={V}, {div}, T={T}, fwd+bwd (grad hidden + grad W)",
+            "tokens": N, "hidden": H, "vocab": V, "teacher": mode, "divergence": div, "temperature": T,
+            "student_ce_weight": w_s, "teacher_ce_weight": w_t, "kl_weight": kl_w, "ignore_frac": ignore_frac,
+        },
+        "peak_extra_hbm_gb": peak_extra / 1e9,
+        "loss": loss_val,
+        "step_roofline": {
+            "bound": "mfma", "achieved": step_tflops, "peak": peak, "unit": "TFLOP/s", "frac": step_tflops / peak,
+            "algorithmic_tflop_per_step": alg / 1e12,
+        },
+    }
+    if kern is not None:
+        rows = kernel_report(kern, args.steps, peak)
+        result["kernels"] = rows
+        # dominant kernel class by time among those that carry algorithmic flops
+        dominant = max((r for r in rows if rows[r]["algorithmic_tflops"] > 0), key=lambda r: rows[r]["ms_per_step"])
+        k = kern[dominant]
+        mean_ms = k["ms"] / k["launches"]
+        alg_per_launch = k["algorithmic_flops"] / k["launches"]
+        achieved = alg_per_launch / (mean_ms / 1e3) / 1e12
+        result["roofline"] = {
+            "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
+            "traffic": None, "kernel": dominant, "mean_launch_ms": mean_ms,
+            "algorithmic_tflop_per_launch": alg_per_launch / 1e12,
+        }
+    if not args.no_cpu_baseline and mode == "tied":
+        _log("[bench] CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(cfg, args.seed, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

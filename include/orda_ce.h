@@ -175,6 +175,35 @@ int orda_backward(const orda_problem_t* p, const orda_tensors_t* t,
 int orda_gemm_abt(int32_t dtype, int64_t M, int64_t N, int64_t K,
                   const void* A, const void* B, void* C, void* stream);
 
+/* Per-kernel-class timing, for benchmarks.  No counterpart in the reference,
+ * whose benchmarks bracket whole steps with torch.cuda.Event
+ * (test/benchmark/src/_train.py:410-419); this hook brackets each launch
+ * inside the library with hipEvents on the launch stream.  Off by default;
+ * the state is process-wide (backward may run on another host thread). */
+enum orda_kernel_class {
+  ORDA_K_SCAN = 0,      /* forward logits GEMM + online-softmax statistics */
+  ORDA_K_ROWS = 1,      /* label logits, per-row merge, loss reduction     */
+  ORDA_K_DLOGITS = 2,   /* backward logits recompute + dlogits epilogue    */
+  ORDA_K_GEMM_W = 3,    /* grad_weight GEMMs                               */
+  ORDA_K_GEMM_H = 4,    /* grad_hidden GEMMs                               */
+  ORDA_K_AUX = 5,       /* transposes and fills                            */
+  ORDA_K_COUNT = 6
+};
+
+typedef struct orda_timing {
+  int32_t launches[ORDA_K_COUNT];
+  double milliseconds[ORDA_K_COUNT];    /* summed kernel time per class   */
+  double algorithmic_flops[ORDA_K_COUNT]; /* GEMM flops that count (no recompute) */
+  double executed_flops[ORDA_K_COUNT];  /* GEMM flops issued to MFMA     */
+} orda_timing_t;
+
+/* Start (enable != 0) or stop recording; starting clears previous records. */
+int orda_timing_enable(int enable);
+
+/* Wait for the recorded events, fill *out with the sums since the last
+ * enable/collect, and clear the records. */
+int orda_timing_collect(orda_timing_t* out);
+
 #ifdef __cplusplus
 }
 #endif

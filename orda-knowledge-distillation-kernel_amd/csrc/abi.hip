@@ -5,6 +5,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <vector>
+#include <atomic>
+#include <mutex>
 
 #include "../../include/orda_ce.h"
 #include "launch.hpp"
@@ -214,6 +217,52 @@ inline char* aligned_base(void* ws) {
 
 inline bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
+// ------------------------------------------------------------ timing hook
+struct TimedLaunch {
+  hipEvent_t start, stop;
+  int kind;
+  double alg, exe;
+};
+// Process-wide (autograd runs backward on its own device thread).
+std::mutex g_timing_mu;
+std::atomic<bool> g_timing{false};
+std::vector<TimedLaunch> g_launches;
+std::vector<hipEvent_t> g_event_pool;
+
+// Caller holds g_timing_mu.
+hipEvent_t pooled_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// Brackets one launch with events on its stream when timing is enabled.
+struct Timed {
+  bool on;
+  TimedLaunch rec;
+  hipStream_t s;
+  Timed(int kind, hipStream_t stream, double alg, double exe) : on(g_timing.load()), s(stream) {
+    if (!on) return;
+    {
+      std::lock_guard<std::mutex> lk(g_timing_mu);
+      rec = TimedLaunch{pooled_event(), pooled_event(), kind, alg, exe};
+    }
+    if (!rec.start || !rec.stop) { on = false; return; }
+    hipEventRecord(rec.start, s);
+  }
+  ~Timed() {
+    if (!on) return;
+    hipEventRecord(rec.stop, s);
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    g_launches.push_back(rec);
+  }
+};
+
 #define ORDA_CHECK_LAUNCH(expr)                                                        \
   do {                                                                                 \
     hipError_t e_ = (expr);                                                            \
@@ -233,7 +282,7 @@ int run_forward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t
   L.Lt = t->teacher_logits; L.labels = t->labels;
   L.N = pl.N; L.V = pl.V; L.H = pl.H; L.Ht = pl.Ht; L.ignore_index = p->ignore_index;
   L.tsrc = pl.tsrc; L.lt_dtype = p->logits_dtype; L.out = labelx;
-  ORDA_CHECK_LAUNCH(launch_label<T>(L, s));
+  { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_label<T>(L, s)); }
 
   FusedParams F{};
   F.W = t->weight; F.hs = t->student_hidden; F.ht = t->teacher_hidden; F.Wt = t->teacher_weight;
@@ -251,7 +300,9 @@ int run_forward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t
   F.tiles_per_range = pl.tiles_per_range; F.n_vtiles = pl.n_vtiles;
   F.partial = partial; F.rowp = rowp;
   const int grid = pl.n_ttiles * pl.n_vranges;
-  ORDA_CHECK_LAUNCH(launch_scan<T>(F, grid, s));
+  const double scan_flops = 2.0 * (double)pl.N * (double)pl.V *
+                            ((double)pl.H + ((pl.tsrc == TSRC_SHARED || pl.tsrc == TSRC_SEP) ? (double)pl.Ht : 0.0));
+  { Timed tm_(ORDA_K_SCAN, s, scan_flops, scan_flops); ORDA_CHECK_LAUNCH(launch_scan<T>(F, grid, s)); }
 
   MergeParams M{};
   M.partial = partial; M.n_vranges = pl.n_vranges; M.N = pl.N; M.V = pl.V; M.ignore_index = p->ignore_index;
@@ -260,13 +311,13 @@ int run_forward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t
   M.invT = F.invT; M.temperature = p->temperature; M.alpha = p->div_alpha; M.beta = p->div_beta;
   for (int i = 0; i < 3; ++i) { M.pa[i] = pl.pa[i]; M.pb[i] = pl.pb[i]; }
   M.npow = pl.npow; M.rowp = rowp; M.rowv = rowv;
-  ORDA_CHECK_LAUNCH(launch_merge(M, s));
+  { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
 
   if (pl.two_pass) {
     F.phase = 1;
-    ORDA_CHECK_LAUNCH(launch_scan<T>(F, grid, s));
+    { Timed tm_(ORDA_K_SCAN, s, 0.0, scan_flops); ORDA_CHECK_LAUNCH(launch_scan<T>(F, grid, s)); }
     M.phase = 1;
-    ORDA_CHECK_LAUNCH(launch_merge(M, s));
+    { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
   }
 
   FinalizeParams Z{};
@@ -276,18 +327,19 @@ int run_forward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t
   Z.w_s = p->student_ce_weight; Z.w_t = p->teacher_ce_weight; Z.w_kl = p->kl_weight;
   Z.out_loss = t->out_loss; Z.out_ce_s = t->out_student_ce; Z.out_ce_t = t->out_teacher_ce; Z.out_kl = t->out_kl;
   Z.scal = scal;
-  ORDA_CHECK_LAUNCH(launch_finalize(Z, s));
+  { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_finalize(Z, s)); }
   return ORDA_OK;
 }
 
 template <class T>
 int gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, float* C32, int64_t ldc, int64_t M,
-         int64_t N, int64_t K, int mode, hipStream_t s) {
+         int64_t N, int64_t K, int mode, hipStream_t s, int kind = ORDA_K_AUX, double alg = 0.0) {
   GemmParams G{};
   G.A = A; G.B = B; G.C = C; G.C32 = C32;
   G.M = M; G.N = N; G.K = K; G.lda = lda; G.ldb = ldb; G.ldc = ldc;
   G.tiles_m = (int)cdiv(M, 256); G.tiles_n = (int)cdiv(N, 256); G.mode = mode;
   if ((int64_t)G.tiles_m * G.tiles_n > 0x7fffffffll) return fail(ORDA_EINVAL, "gemm grid too large");
+  Timed tm_(kind, s, alg, 2.0 * (double)M * (double)N * (double)K);
   ORDA_CHECK_LAUNCH(launch_gemm<T>(G, s));
   return ORDA_OK;
 }
@@ -318,7 +370,7 @@ int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* 
   // Tied mode with teacher CE off: the teacher hidden gradient is zero
   // (reference ops/tied_teacher.py:478-479).
   if (tied && pl.need_gt && !pl.w_dln_t)
-    ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, H, N, 0, H, eb, s));
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, H, N, 0, H, eb, s)); }
 
   const bool any = pl.w_dlt_s || pl.w_dlt_t || pl.w_dln_s || pl.w_dln_t;
   if (!any) return ORDA_OK;
@@ -326,20 +378,20 @@ int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* 
   // Transposed hidden states for the grad_W GEMMs (K = tokens), with zeroed
   // padding columns so K can be rounded up to a multiple of 8.
   if (pl.need_gw) {
-    ORDA_CHECK_LAUNCH(launch_zero2d(hT, pl.ldh, H, N, NP, eb, s));
-    ORDA_CHECK_LAUNCH(launch_transpose<T>(t->student_hidden, H, hT, pl.ldh, N, H, s));
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(hT, pl.ldh, H, N, NP, eb, s)); }
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_transpose<T>(t->student_hidden, H, hT, pl.ldh, N, H, s)); }
     if (tied && pl.w_dlt_t) {
-      ORDA_CHECK_LAUNCH(launch_zero2d(hT, pl.ldh, H, NP + N, 2 * NP, eb, s));
-      ORDA_CHECK_LAUNCH(launch_transpose<T>(t->teacher_hidden, H, hT + NP * eb, pl.ldh, N, H, s));
+      { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(hT, pl.ldh, H, NP + N, 2 * NP, eb, s)); }
+      { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_transpose<T>(t->teacher_hidden, H, hT + NP * eb, pl.ldh, N, H, s)); }
     }
   }
   if (sep && pl.w_dlt_t) {
-    ORDA_CHECK_LAUNCH(launch_zero2d(htT, NP, Ht, N, NP, eb, s));
-    ORDA_CHECK_LAUNCH(launch_transpose<T>(t->teacher_hidden, Ht, htT, NP, N, Ht, s));
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(htT, NP, Ht, N, NP, eb, s)); }
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_transpose<T>(t->teacher_hidden, Ht, htT, NP, N, Ht, s)); }
   }
   // padding columns of the staged dlogits (never written by the dL kernel)
-  if (pl.w_dlt_s || pl.w_dlt_t) ORDA_CHECK_LAUNCH(launch_zero2d(dLT, pl.ldT, pl.Vc, N, NP, eb, s));
-  if (pl.w_dlt_t) ORDA_CHECK_LAUNCH(launch_zero2d(dLT, pl.ldT, pl.Vc, NP + N, 2 * NP, eb, s));
+  if (pl.w_dlt_s || pl.w_dlt_t) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(dLT, pl.ldT, pl.Vc, N, NP, eb, s)); }
+  if (pl.w_dlt_t) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(dLT, pl.ldT, pl.Vc, NP + N, 2 * NP, eb, s)); }
 
   FusedParams F{};
   F.W = t->weight; F.hs = t->student_hidden; F.ht = t->teacher_hidden; F.Wt = t->teacher_weight;
@@ -367,41 +419,49 @@ int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* 
                       : c == pl.nchunks - 1 ? GEMM_ACC_LAST : GEMM_ACC;
     const bool needWT = pl.need_gs || (tied && pl.w_dln_t);
     if (needWT) {
-      ORDA_CHECK_LAUNCH(launch_transpose<T>(static_cast<const char*>(t->weight) + vc0 * H * eb, H, WT, pl.Vc, vcc, H, s));
-      if (vck > vcc) ORDA_CHECK_LAUNCH(launch_zero2d(WT, pl.Vc, H, vcc, vck, eb, s));
+      { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_transpose<T>(static_cast<const char*>(t->weight) + vc0 * H * eb, H, WT, pl.Vc, vcc, H, s)); }
+      if (vck > vcc) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(WT, pl.Vc, H, vcc, vck, eb, s)); }
     }
     if (sep && pl.w_dln_t) {
-      ORDA_CHECK_LAUNCH(launch_transpose<T>(static_cast<const char*>(t->teacher_weight) + vc0 * Ht * eb, Ht, WtT, pl.Vc, vcc, Ht, s));
-      if (vck > vcc) ORDA_CHECK_LAUNCH(launch_zero2d(WtT, pl.Vc, Ht, vcc, vck, eb, s));
+      { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_transpose<T>(static_cast<const char*>(t->teacher_weight) + vc0 * Ht * eb, Ht, WtT, pl.Vc, vcc, Ht, s)); }
+      if (vck > vcc) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(WtT, pl.Vc, Ht, vcc, vck, eb, s)); }
     }
     if (vck > vcc) {
-      if (pl.w_dln_s) ORDA_CHECK_LAUNCH(launch_zero2d(dLNs, pl.Vc, N, vcc, vck, eb, s));
-      if (pl.w_dln_t) ORDA_CHECK_LAUNCH(launch_zero2d(dLNt, pl.Vc, N, vcc, vck, eb, s));
+      if (pl.w_dln_s) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(dLNs, pl.Vc, N, vcc, vck, eb, s)); }
+      if (pl.w_dln_t) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(dLNt, pl.Vc, N, vcc, vck, eb, s)); }
     }
     F.vc0 = vc0; F.vcc = vcc;
     const int grid = (int)(cdiv(vcc, 256) * pl.n_ttiles);
-    ORDA_CHECK_LAUNCH(launch_dl<T>(F, grid, s));
+    {
+      const double kt = (pl.bwd_tsrc == TSRC_SHARED || pl.bwd_tsrc == TSRC_SEP) ? (double)Ht : 0.0;
+      Timed tm_(ORDA_K_DLOGITS, s, 0.0, 2.0 * (double)N * (double)vcc * ((double)H + kt));
+      ORDA_CHECK_LAUNCH(launch_dl<T>(F, grid, s));
+    }
 
     if (pl.need_gw) {
+      const double kv = (tied && pl.w_dlt_t) ? 2.0 * (double)N : (double)N;
       ORDA_TRY(gemm<T>(dLT, pl.ldT, hT, pl.ldh, static_cast<char*>(t->grad_weight) + vc0 * H * eb, nullptr, H, vcc,
-                       H, Kw, GEMM_STORE, s));
+                       H, Kw, GEMM_STORE, s, ORDA_K_GEMM_W, 2.0 * (double)vcc * (double)H * kv));
     }
     if (sep && pl.need_gwt && pl.w_dlt_t) {
       ORDA_TRY(gemm<T>(dLT + NP * eb, pl.ldT, htT, NP, static_cast<char*>(t->grad_teacher_weight) + vc0 * Ht * eb,
-                       nullptr, Ht, vcc, Ht, NP, GEMM_STORE, s));
+                       nullptr, Ht, vcc, Ht, NP, GEMM_STORE, s, ORDA_K_GEMM_W,
+                       2.0 * (double)vcc * (double)Ht * (double)N));
     }
     if (pl.need_gs) {
-      ORDA_TRY(gemm<T>(dLNs, pl.Vc, WT, pl.Vc, t->grad_student_hidden, g32s, H, N, H, vck, gmode, s));
+      ORDA_TRY(gemm<T>(dLNs, pl.Vc, WT, pl.Vc, t->grad_student_hidden, g32s, H, N, H, vck, gmode, s, ORDA_K_GEMM_H,
+                       2.0 * (double)N * (double)H * (double)vcc));
     }
     if (pl.w_dln_t) {
-      ORDA_TRY(gemm<T>(dLNt, pl.Vc, tied ? WT : WtT, pl.Vc, t->grad_teacher_hidden, g32t, Ht, N, Ht, vck, gmode, s));
+      ORDA_TRY(gemm<T>(dLNt, pl.Vc, tied ? WT : WtT, pl.Vc, t->grad_teacher_hidden, g32t, Ht, N, Ht, vck, gmode, s,
+                       ORDA_K_GEMM_H, 2.0 * (double)N * (double)Ht * (double)vcc));
     }
   }
   // separate mode, teacher weight grad requested but teacher CE off: zero
   if (sep && pl.need_gwt && !pl.w_dlt_t)
-    ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_weight, Ht, pl.V, 0, Ht, eb, s));
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_weight, Ht, pl.V, 0, Ht, eb, s)); }
   if (sep && pl.need_gt && !pl.w_dln_t)
-    ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, Ht, N, 0, Ht, eb, s));
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, Ht, N, 0, Ht, eb, s)); }
   return ORDA_OK;
 }
 
@@ -502,6 +562,38 @@ int orda_gemm_abt(int32_t dtype, int64_t M, int64_t N, int64_t K, const void* A,
     case ORDA_F16: return gemm<f16>(A, K, B, K, C, nullptr, N, M, N, K, GEMM_STORE, s);
     default: return gemm<float>(A, K, B, K, C, nullptr, N, M, N, K, GEMM_STORE, s);
   }
+}
+
+int orda_timing_enable(int enable) {
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  g_timing = enable != 0;
+  if (enable) {
+    for (auto& r : g_launches) { g_event_pool.push_back(r.start); g_event_pool.push_back(r.stop); }
+    g_launches.clear();
+  }
+  return ORDA_OK;
+}
+
+int orda_timing_collect(orda_timing_t* out) {
+  g_err.clear();
+  if (!out) return fail(ORDA_EINVAL, "out is NULL");
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  *out = orda_timing_t{};
+  for (auto& r : g_launches) {
+    if (hipEventSynchronize(r.stop) != hipSuccess) return fail(ORDA_ELAUNCH, "hipEventSynchronize failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) return fail(ORDA_ELAUNCH, "hipEventElapsedTime failed");
+    if (r.kind >= 0 && r.kind < ORDA_K_COUNT) {
+      out->launches[r.kind] += 1;
+      out->milliseconds[r.kind] += ms;
+      out->algorithmic_flops[r.kind] += r.alg;
+      out->executed_flops[r.kind] += r.exe;
+    }
+    g_event_pool.push_back(r.start);
+    g_event_pool.push_back(r.stop);
+  }
+  g_launches.clear();
+  return ORDA_OK;
 }
 
 }  // extern "C"

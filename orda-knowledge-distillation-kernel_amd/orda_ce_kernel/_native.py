@@ -17,7 +17,7 @@ import torch
 __all__ = [
     "ABI_VERSION", "Problem", "Tensors", "library", "library_path", "forward", "backward",
     "saved_bytes", "forward_workspace_bytes", "backward_workspace_bytes", "gemm_abt",
-    "MODE", "DTYPE", "FLAG",
+    "MODE", "DTYPE", "FLAG", "KERNEL_CLASSES", "timing_enable", "timing_collect",
 ]
 
 ABI_VERSION = 1
@@ -57,6 +57,20 @@ class Problem(ctypes.Structure):
         ("kl_weight", ctypes.c_float),
         ("div_alpha", ctypes.c_float),
         ("div_beta", ctypes.c_float),
+    ]
+
+
+KERNEL_CLASSES = ("scan", "rows", "dlogits", "gemm_w", "gemm_h", "aux")
+
+
+class Timing(ctypes.Structure):
+    """orda_timing_t"""
+
+    _fields_ = [
+        ("launches", ctypes.c_int32 * 6),
+        ("milliseconds", ctypes.c_double * 6),
+        ("algorithmic_flops", ctypes.c_double * 6),
+        ("executed_flops", ctypes.c_double * 6),
     ]
 
 
@@ -115,6 +129,10 @@ def library() -> ctypes.CDLL:
             ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
         ]
+        lib.orda_timing_enable.restype = ctypes.c_int
+        lib.orda_timing_enable.argtypes = [ctypes.c_int]
+        lib.orda_timing_collect.restype = ctypes.c_int
+        lib.orda_timing_collect.argtypes = [ctypes.POINTER(Timing)]
         version = lib.orda_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"liborda_ce.so ABI version {version}, expected {ABI_VERSION}")
@@ -180,3 +198,24 @@ def gemm_abt(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     rc = library().orda_gemm_abt(DTYPE[a.dtype], M, N, K, a.data_ptr(), b.data_ptr(), c.data_ptr(), _stream(a.device))
     _check(rc, "orda_gemm_abt")
     return c
+
+
+def timing_enable(enable: bool = True) -> None:
+    """Start/stop per-launch hipEvent timing inside the library (this thread)."""
+    library().orda_timing_enable(1 if enable else 0)
+
+
+def timing_collect() -> dict:
+    """Per kernel class: launches, ms, algorithmic and executed GEMM flops
+    since the last enable/collect (waits for the recorded events)."""
+    t = Timing()
+    _check(library().orda_timing_collect(ctypes.byref(t)), "orda_timing_collect")
+    return {
+        name: {
+            "launches": int(t.launches[i]),
+            "ms": float(t.milliseconds[i]),
+            "algorithmic_flops": float(t.algorithmic_flops[i]),
+            "executed_flops": float(t.executed_flops[i]),
+        }
+        for i, name in enumerate(KERNEL_CLASSES)
+    }
