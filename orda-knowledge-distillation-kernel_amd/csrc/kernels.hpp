@@ -1,5 +1,5 @@
-// kernels.hpp -- kernel templates of liborda_ce.so, instantiated once per
-// element type by kernels_{bf16,f16,f32}.hip.
+// kernels.hpp -- kernel templates of liborda_ce.so, instantiated per element
+// type by k_{scan,dl,gemm}_{bf16,f16,f32}.hip.
 #pragma once
 
 #include "launch.hpp"
@@ -50,12 +50,12 @@ __device__ __forceinline__ float div_grad(float lps, float lpt, float psT, float
 }
 
 // ------------------------------------------------------------- shared GEMMs
-// Runs the logits GEMM of one fused tile: acc[.][0..1] = student logits
-// (W rows v0.. x hs rows t0..), acc[.][2..3] = teacher logits of the same
-// tokens (tied: same W, teacher hidden; separate: W_t x teacher hidden;
-// precomputed logits: loaded from memory).
+// Logits of one fused tile (256 vocabulary rows x 128 tokens): acc[.][0] =
+// student logits (W rows v0.. x hs rows t0..), acc[.][1] = teacher logits of
+// the same tokens (tied: same W x teacher hidden; separate: W_t x teacher
+// hidden; precomputed logits: loaded from memory).
 template <class T>
-__device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][4], char* lds, const FusedParams& P,
+__device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][2], char* lds, const FusedParams& P,
                                              int64_t v0, int64_t t0) {
   zero_acc(acc);
   const T* W = static_cast<const T*>(P.W);
@@ -74,13 +74,11 @@ __device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][4], char* lds, con
       mainloop<T, false, true>(acc, lds, Wt + v0 * P.Ht, P.Ht, arows, nullptr, 0, 0,
                                ht + t0 * P.Ht, P.Ht, brows, P.Ht);
     } else if (P.tsrc == TSRC_MEM) {
-      // Teacher logits [N x V] from memory into the unused teacher half.
-      const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-      const int wm = wave >> 1, wn = wave & 1;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t t = t0 + wn * 64 + j * 32 + (lane & 31);
-        if (t >= P.N) continue;
+      // Teacher logits [N x V] from memory into the unused teacher block.
+      const int lane = threadIdx.x & 63;
+      const int wm = wave_m(), wn = wave_n();
+      const int64_t t = t0 + wn * 32 + (lane & 31);
+      if (t < P.N) {
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
@@ -102,7 +100,7 @@ __device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][4], char* lds, con
               for (int e = 0; e < 4; ++e) x[e] = (v + e < P.V) ? (float)src[e] : 0.f;
             }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[mb][j + 2][g * 4 + e] = x[e];
+            for (int e = 0; e < 4; ++e) acc[mb][1][g * 4 + e] = x[e];
           }
       }
     }
@@ -110,12 +108,12 @@ __device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][4], char* lds, con
 }
 
 // ------------------------------------------------------------- scan kernel
-// Phase 0: online softmax statistics of one token slot j over this tile's
-// 128 vocabulary rows held by the lane.  Template flags remove work that the
-// problem does not need.
+// Phase 0: online softmax statistics of this lane's token over its 64
+// vocabulary rows of the tile.  Template flags remove work that the problem
+// does not need.
 template <bool HAS_T, int FAM, bool T1, bool MASK>
-__device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][4], int j,
-                                          int vlane0, int64_t vlimit, const FusedParams& P) {
+__device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][2], int vlane0, int64_t vlimit,
+                                          const FusedParams& P) {
   const float invT = P.invT;
   float tms = -kInf, tmt = -kInf, tmu0 = -kInf, tmu1 = -kInf, tmu2 = -kInf;
 #pragma unroll
@@ -123,10 +121,10 @@ __device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][4]
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
-      const float xs = acc[mb][j][r];
+      const float xs = acc[mb][0][r];
       tms = fmaxf(tms, xs);
       if (HAS_T) {
-        const float xt = acc[mb][j + 2][r];
+        const float xt = acc[mb][1][r];
         tmt = fmaxf(tmt, xt);
         if (FAM == FAM_POW) {
           tmu0 = fmaxf(tmu0, P.pa[0] * xt + P.pb[0] * xs);
@@ -186,13 +184,13 @@ __device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][4]
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
-      const float xs = acc[mb][j][r];
+      const float xs = acc[mb][0][r];
       const float es = fexp(xs - nms);
       S.ss += es;
       const float esT = T1 ? es : fexp((xs - nms) * invT);
       if (!T1) S.sst += esT;
       if (HAS_T) {
-        const float xt = acc[mb][j + 2][r];
+        const float xt = acc[mb][1][r];
         const float et = fexp(xt - nmt);
         S.st += et;
         const float etT = T1 ? et : fexp((xt - nmt) * invT);
@@ -215,9 +213,8 @@ __device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][4]
 // Phase 1 (two-pass divergences): sums of terms of the normalised
 // probabilities, given the row log-normalisers from phase 0.
 template <int DIV, bool MASK>
-__device__ __forceinline__ void rowsum_tile(RowState& S, const f32x16 (&acc)[4][4], int j,
-                                            int vlane0, int64_t vlimit, float lse_sT, float lse_tT,
-                                            const FusedParams& P) {
+__device__ __forceinline__ void rowsum_tile(RowState& S, const f32x16 (&acc)[4][2], int vlane0, int64_t vlimit,
+                                            float lse_sT, float lse_tT, const FusedParams& P) {
   const float invT = P.invT;
   float s0 = 0.f, s1 = 0.f;
 #pragma unroll
@@ -225,8 +222,8 @@ __device__ __forceinline__ void rowsum_tile(RowState& S, const f32x16 (&acc)[4][
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
-      const float lps = acc[mb][j][r] * invT - lse_sT;
-      const float lpt = acc[mb][j + 2][r] * invT - lse_tT;
+      const float lps = acc[mb][0][r] * invT - lse_sT;
+      const float lpt = acc[mb][1][r] * invT - lse_tT;
       const float ps = fexp(lps), pt = fexp(lpt);
       if constexpr (DIV == DIV_JSD) {
         const float lm = logaddexp(P.log_beta + lpt, P.log_1m_beta + lps);
@@ -260,8 +257,9 @@ __device__ __forceinline__ RowState shfl32(const RowState& s) {
   return o;
 }
 
+template <bool PHASE1>
 __device__ __forceinline__ void merge_any(RowState& a, const RowState& b, const FusedParams& P) {
-  if (P.phase == 1) {
+  if (PHASE1) {
     a.x[0] += b.x[0];
     a.x[1] += b.x[1];
   } else {
@@ -284,194 +282,176 @@ enum ScanVariant {
 };
 
 template <int SV>
-__device__ __forceinline__ void scan_variant(RowState& S, const f32x16 (&acc)[4][4], int j, int vlane0,
-                                             int64_t vlimit, bool full, float lse_sT, float lse_tT,
-                                             const FusedParams& P) {
+__device__ __forceinline__ void scan_variant(RowState& S, const f32x16 (&acc)[4][2], int vlane0, int64_t vlimit,
+                                             bool full, float lse_sT, float lse_tT, const FusedParams& P) {
   if constexpr (SV == SV_STUDENT) {
-    if (full) scan_tile<false, FAM_NONE, true, false>(S, acc, j, vlane0, vlimit, P);
-    else scan_tile<false, FAM_NONE, true, true>(S, acc, j, vlane0, vlimit, P);
+    if (full) scan_tile<false, FAM_NONE, true, false>(S, acc, vlane0, vlimit, P);
+    else scan_tile<false, FAM_NONE, true, true>(S, acc, vlane0, vlimit, P);
   } else if constexpr (SV == SV_TCE_T1) {
-    if (full) scan_tile<true, FAM_NONE, true, false>(S, acc, j, vlane0, vlimit, P);
-    else scan_tile<true, FAM_NONE, true, true>(S, acc, j, vlane0, vlimit, P);
+    if (full) scan_tile<true, FAM_NONE, true, false>(S, acc, vlane0, vlimit, P);
+    else scan_tile<true, FAM_NONE, true, true>(S, acc, vlane0, vlimit, P);
   } else if constexpr (SV == SV_TCE) {
-    if (full) scan_tile<true, FAM_NONE, false, false>(S, acc, j, vlane0, vlimit, P);
-    else scan_tile<true, FAM_NONE, false, true>(S, acc, j, vlane0, vlimit, P);
+    if (full) scan_tile<true, FAM_NONE, false, false>(S, acc, vlane0, vlimit, P);
+    else scan_tile<true, FAM_NONE, false, true>(S, acc, vlane0, vlimit, P);
   } else if constexpr (SV == SV_LIN_T1) {
-    if (full) scan_tile<true, FAM_LIN, true, false>(S, acc, j, vlane0, vlimit, P);
-    else scan_tile<true, FAM_LIN, true, true>(S, acc, j, vlane0, vlimit, P);
+    if (full) scan_tile<true, FAM_LIN, true, false>(S, acc, vlane0, vlimit, P);
+    else scan_tile<true, FAM_LIN, true, true>(S, acc, vlane0, vlimit, P);
   } else if constexpr (SV == SV_LIN) {
-    if (full) scan_tile<true, FAM_LIN, false, false>(S, acc, j, vlane0, vlimit, P);
-    else scan_tile<true, FAM_LIN, false, true>(S, acc, j, vlane0, vlimit, P);
+    if (full) scan_tile<true, FAM_LIN, false, false>(S, acc, vlane0, vlimit, P);
+    else scan_tile<true, FAM_LIN, false, true>(S, acc, vlane0, vlimit, P);
   } else if constexpr (SV == SV_POW) {
-    if (full) scan_tile<true, FAM_POW, false, false>(S, acc, j, vlane0, vlimit, P);
-    else scan_tile<true, FAM_POW, false, true>(S, acc, j, vlane0, vlimit, P);
+    if (full) scan_tile<true, FAM_POW, false, false>(S, acc, vlane0, vlimit, P);
+    else scan_tile<true, FAM_POW, false, true>(S, acc, vlane0, vlimit, P);
   } else {
     constexpr int DIV = SV == SV_JSD ? DIV_JSD : SV == SV_SKEW_F ? DIV_SKEW_F : SV == SV_SKEW_R ? DIV_SKEW_R : DIV_TVD;
-    if (full) rowsum_tile<DIV, false>(S, acc, j, vlane0, vlimit, lse_sT, lse_tT, P);
-    else rowsum_tile<DIV, true>(S, acc, j, vlane0, vlimit, lse_sT, lse_tT, P);
+    if (full) rowsum_tile<DIV, false>(S, acc, vlane0, vlimit, lse_sT, lse_tT, P);
+    else rowsum_tile<DIV, true>(S, acc, vlane0, vlimit, lse_sT, lse_tT, P);
   }
 }
 
+// One workgroup: 128 tokens x a contiguous range of 256-row vocabulary
+// tiles; writes one partial RowState per (range, token).
 template <class T, int SV>
 __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
   constexpr bool kPhase1 = SV >= SV_JSD;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int tt = blockIdx.x % P.n_ttiles;
-  const int vr = blockIdx.x / P.n_ttiles;
+  const int lane = threadIdx.x & 63;
+  const int wm = wave_m(), wn = wave_n();
+  const int t = xcd_order(blockIdx.x, gridDim.x);
+  const int tt = t % P.n_ttiles;
+  const int vr = t / P.n_ttiles;
   const int64_t t0 = (int64_t)tt * 128;
   const int vt_begin = vr * P.tiles_per_range;
   const int vt_end = min(vt_begin + P.tiles_per_range, P.n_vtiles);
-  RowState st[2];
-  state_init_fam(st[0], kPhase1 ? FAM_NONE : P.fam);
-  state_init_fam(st[1], kPhase1 ? FAM_NONE : P.fam);
 
-  int64_t tok[2];
-  float lse_sT[2] = {0.f, 0.f}, lse_tT[2] = {0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    tok[j] = t0 + wn * 64 + j * 32 + (lane & 31);
-    if (tok[j] < P.N) {
-      if (kPhase1) {
-        lse_sT[j] = P.rowp[1 * P.N + tok[j]];
-        lse_tT[j] = P.rowp[3 * P.N + tok[j]];
-      }
-    }
+  RowState st;
+  state_init_fam(st, kPhase1 ? FAM_NONE : P.fam);
+  const int64_t tok = t0 + wn * 32 + (lane & 31);
+  float lse_sT = 0.f, lse_tT = 0.f;
+  if (kPhase1 && tok < P.N) {
+    lse_sT = P.rowp[1 * P.N + tok];
+    lse_tT = P.rowp[3 * P.N + tok];
   }
 
   for (int vt = vt_begin; vt < vt_end; ++vt) {
     const int64_t v0 = (int64_t)vt * 256;
     // Opaque copy of the token base: keeps the compiler from hoisting every
-    // per-row operand address out of this loop (which costs ~250 VGPRs).
+    // per-row operand address out of this loop.
     int64_t t0v = t0;
     asm volatile("" : "+s"(t0v));
     fused_logits<T>(acc, lds, P, v0, t0v);
     const int vlane0 = wm * 128 + (lane >> 5) * 4;
     const int64_t vlimit = P.V - v0;
-    const bool full = vlimit >= 256;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      scan_variant<SV>(st[j], acc, j, vlane0, vlimit, full, lse_sT[j], lse_tT[j], P);
-    }
+    scan_variant<SV>(st, acc, vlane0, vlimit, vlimit >= 256, lse_sT, lse_tT, P);
   }
 
   // combine lane l with l^32, then the two waves sharing the tokens (wm 0/1)
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const RowState o = shfl32(st[j]);
-    merge_any(st[j], o, P);
+  {
+    const RowState o = shfl32(st);
+    merge_any<kPhase1>(st, o, P);
   }
   __syncthreads();
-  float* xch = reinterpret_cast<float*>(lds);  // [wn][j][kNStat][32]
+  float* xch = reinterpret_cast<float*>(lds);  // [wn][kNStat][32]
   if (wm == 1 && lane < 32) {
+    float* d = xch + (wn * kNStat) * 32 + lane;
+    const float* s = reinterpret_cast<const float*>(&st);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float* d = xch + ((wn * 2 + j) * kNStat) * 32 + lane;
-      const float* s = reinterpret_cast<const float*>(&st[j]);
-#pragma unroll
-      for (int f = 0; f < kNStat; ++f) d[f * 32] = s[f];
-    }
+    for (int f = 0; f < kNStat; ++f) d[f * 32] = s[f];
   }
   __syncthreads();
   if (wm == 0 && lane < 32) {
+    RowState o;
+    float* od = reinterpret_cast<float*>(&o);
+    const float* s = xch + (wn * kNStat) * 32 + lane;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      RowState o;
-      float* od = reinterpret_cast<float*>(&o);
-      const float* s = xch + ((wn * 2 + j) * kNStat) * 32 + lane;
+    for (int f = 0; f < kNStat; ++f) od[f] = s[f * 32];
+    merge_any<kPhase1>(st, o, P);
+    if (tok < P.N) {
+      float* dst = P.partial + (int64_t)vr * kNStat * P.N + tok;
+      const float* sv = reinterpret_cast<const float*>(&st);
 #pragma unroll
-      for (int f = 0; f < kNStat; ++f) od[f] = s[f * 32];
-      merge_any(st[j], o, P);
-      if (tok[j] < P.N) {
-        float* dst = P.partial + (int64_t)vr * kNStat * P.N + tok[j];
-        const float* sv = reinterpret_cast<const float*>(&st[j]);
-#pragma unroll
-        for (int f = 0; f < kNStat; ++f) dst[(int64_t)f * P.N] = sv[f];
-      }
+      for (int f = 0; f < kNStat; ++f) dst[(int64_t)f * P.N] = sv[f];
     }
   }
 }
 
 // ----------------------------------------------------------- dlogits kernel
 template <class T, int DIV, bool T1>
-__device__ __forceinline__ void dl_tile(const f32x16 (&acc)[4][4], const FusedParams& P, int64_t v0,
+__device__ __forceinline__ void dl_tile(const f32x16 (&acc)[4][2], const FusedParams& P, int64_t v0,
                                         int64_t t0) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int lane = threadIdx.x & 63;
+  const int wm = wave_m(), wn = wave_n();
+  const int64_t t = t0 + wn * 32 + (lane & 31);
+  if (t >= P.N) return;
   const float scale = P.grad_output[0] * P.mean_scale[0];
   const float invT = P.invT;
   const int64_t vend = min(P.V, P.vc0 + P.vcc);
   T* dLT = static_cast<T*>(P.dLT);
   T* dLNs = static_cast<T*>(P.dLNs);
   T* dLNt = static_cast<T*>(P.dLNt);
+  const int64_t y = P.labels[t];
+  const bool ignored = (y == P.ignore_index);
+  const int64_t yeff = (y >= 0 && y < P.V) ? y : 0;
+  const float lse_s = P.rowp[0 * P.N + t];
+  const float lse_sT = P.rowp[1 * P.N + t];
+  const float lse_t = P.rowp[2 * P.N + t];
+  const float lse_tT = P.rowp[3 * P.N + t];
+  float c[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t t = t0 + wn * 64 + j * 32 + (lane & 31);
-    if (t >= P.N) continue;
-    const int64_t y = P.labels[t];
-    const bool ignored = (y == P.ignore_index);
-    const int64_t yeff = (y >= 0 && y < P.V) ? y : 0;
-    const float lse_s = P.rowp[0 * P.N + t];
-    const float lse_sT = P.rowp[1 * P.N + t];
-    const float lse_t = P.rowp[2 * P.N + t];
-    const float lse_tT = P.rowp[3 * P.N + t];
-    float c[4];
+  for (int i = 0; i < 4; ++i) c[i] = P.rowp[(4 + i) * P.N + t];
+  const float sc_s = ignored ? 0.f : scale * P.w_s;
+  const float sc_t = ignored ? 0.f : scale * P.w_t;
+  const float sc_d = ignored ? 0.f : scale * P.w_kl * P.temperature;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = P.rowp[(4 + i) * P.N + t];
-    const float sc_s = ignored ? 0.f : scale * P.w_s;
-    const float sc_t = ignored ? 0.f : scale * P.w_t;
-    const float sc_d = ignored ? 0.f : scale * P.w_kl * P.temperature;
+  for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int g = 0; g < 4; ++g) {
+      const int64_t vg = v0 + wm * 128 + acc_row(mb, g * 4, lane);  // 4 consecutive rows
+      float gs[4], gt[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t vg = v0 + wm * 128 + acc_row(mb, g * 4, lane);  // 4 consecutive rows
-        float gs[4], gt[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = g * 4 + e;
-          const int64_t v = vg + e;
-          const float xs = acc[mb][j][r];
-          const float onehot = (v == yeff) ? 1.f : 0.f;
-          const float ps1 = fexp(xs - lse_s);
-          float d = sc_s * (ps1 - onehot);
-          if (DIV >= 0) {
-            const float xt = acc[mb][j + 2][r];
-            const float lps = xs * invT - lse_sT;
-            const float lpt = xt * invT - lse_tT;
-            const float psT = T1 ? ps1 : fexp(lps);
-            const float ptT = fexp(lpt);
-            d += sc_d * div_grad<(DIV >= 0 ? DIV : 0)>(lps, lpt, psT, ptT, c, P.alpha, P.beta);
-          }
-          gs[e] = ignored ? 0.f : d;
-          if (P.tgrad) {
-            const float xt = acc[mb][j + 2][r];
-            gt[e] = ignored ? 0.f : sc_t * (fexp(xt - lse_t) - onehot);
-          } else {
-            gt[e] = 0.f;
-          }
+      for (int e = 0; e < 4; ++e) {
+        const int r = g * 4 + e;
+        const int64_t v = vg + e;
+        const float xs = acc[mb][0][r];
+        const float onehot = (v == yeff) ? 1.f : 0.f;
+        const float ps1 = fexp(xs - lse_s);
+        float d = sc_s * (ps1 - onehot);
+        if (DIV >= 0) {
+          const float xt = acc[mb][1][r];
+          const float lps = xs * invT - lse_sT;
+          const float lpt = xt * invT - lse_tT;
+          const float psT = T1 ? ps1 : fexp(lps);
+          const float ptT = fexp(lpt);
+          d += sc_d * div_grad<(DIV >= 0 ? DIV : 0)>(lps, lpt, psT, ptT, c, P.alpha, P.beta);
         }
-        const int64_t vl = vg - P.vc0;  // row inside the chunk
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (vg + e >= vend) continue;
-          if (P.w_dlt_s) dLT[(vl + e) * P.ldT + t] = from_f32<T>(gs[e]);
-          if (P.w_dlt_t) dLT[(vl + e) * P.ldT + P.tcol + t] = from_f32<T>(gt[e]);
-          if (P.w_dln_s) dLNs[t * P.ldN + vl + e] = from_f32<T>(gs[e]);
-          if (P.w_dln_t) dLNt[t * P.ldN + vl + e] = from_f32<T>(gt[e]);
+        gs[e] = ignored ? 0.f : d;
+        if (P.tgrad) {
+          const float xt = acc[mb][1][r];
+          gt[e] = ignored ? 0.f : sc_t * (fexp(xt - lse_t) - onehot);
+        } else {
+          gt[e] = 0.f;
         }
       }
-  }
+      const int64_t vl = vg - P.vc0;  // row inside the chunk
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (vg + e >= vend) continue;
+        if (P.w_dlt_s) dLT[(vl + e) * P.ldT + t] = from_f32<T>(gs[e]);
+        if (P.w_dlt_t) dLT[(vl + e) * P.ldT + P.tcol + t] = from_f32<T>(gt[e]);
+        if (P.w_dln_s) dLNs[t * P.ldN + vl + e] = from_f32<T>(gs[e]);
+        if (P.w_dln_t) dLNt[t * P.ldN + vl + e] = from_f32<T>(gt[e]);
+      }
+    }
 }
 
 template <class T, int DIV, bool T1>
 __global__ __launch_bounds__(kThreads) void k_dl(FusedParams P) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
-  f32x16 acc[4][4];
-  const int tt = blockIdx.x % P.n_ttiles;
-  const int vt = blockIdx.x / P.n_ttiles;
+  f32x16 acc[4][2];
+  const int b = xcd_order(blockIdx.x, gridDim.x);
+  const int tt = b % P.n_ttiles;
+  const int vt = b / P.n_ttiles;
   const int64_t t0 = (int64_t)tt * 128;
   const int64_t v0 = P.vc0 + (int64_t)vt * 256;
   fused_logits<T>(acc, lds, P, v0, t0);
@@ -480,10 +460,10 @@ __global__ __launch_bounds__(kThreads) void k_dl(FusedParams P) {
 
 // -------------------------------------------------------------- plain GEMM
 template <class T, int MODE>
-__device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[4][4], const GemmParams& P, int64_t m0,
+__device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[4][2], const GemmParams& P, int64_t m0,
                                               int64_t n0) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int lane = threadIdx.x & 63;
+  const int wm = wave_m(), wn = wave_n();
   // 32-bit offsets inside the tile; the tile base stays 64-bit.
   T* C = static_cast<T*>(P.C) + m0 * P.ldc + n0;
   float* C32 = P.C32 + m0 * P.ldc + n0;
@@ -492,7 +472,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[4][4], const G
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+    for (int nb = 0; nb < 2; ++nb) {
       const int n = acc_col0(nb, wn) + (lane & 31);
       const int mrow0 = wm * 128 + mb * 32 + (lane >> 5) * 4;
 #pragma unroll
@@ -510,14 +490,21 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16 (&acc)[4][4], const G
     }
 }
 
+// C[M x N] (= or +=) A[M x K] * B[N x K]^T.  Epilogue modes: STORE writes C
+// in T; ACC_FIRST/ACC write the fp32 accumulator C32; ACC_LAST adds C32 and
+// writes C in T.  Tiles are visited in bands of 8 tile rows, XCD by XCD.
 template <class T>
 __global__ __launch_bounds__(kThreads) void k_gemm(GemmParams P) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
-  f32x16 acc[4][4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int tm = blockIdx.x % P.tiles_m;
-  const int tn = blockIdx.x / P.tiles_m;
+  f32x16 acc[4][2];
+  const int t = xcd_order(blockIdx.x, gridDim.x);
+  constexpr int G = 8;
+  const int band = t / (G * P.tiles_n);
+  const int first_m = band * G;
+  const int gm = min(P.tiles_m - first_m, G);
+  const int rem = t % (G * P.tiles_n);
+  const int tm = first_m + rem % gm;
+  const int tn = rem / gm;
   const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
   const T* A = static_cast<const T*>(P.A);
   const T* B = static_cast<const T*>(P.B);

@@ -1,6 +1,7 @@
 // orda_core.hpp -- device building blocks shared by every kernel of
 // liborda_ce.so: element traits, the LDS-staged MFMA main loop (CDNA4,
-// gfx950), and the per-row softmax / divergence statistics.
+// gfx950), the XCD-aware workgroup order, and the per-row softmax /
+// divergence statistics.
 //
 // Orientation.  Every GEMM here computes C = A * B^T with both operands
 // K-contiguous (row-major [rows x K]).  In the fused loss kernels A is the
@@ -9,6 +10,13 @@
 // rows per 32x32 block.  Per-token softmax reductions over the vocabulary
 // are therefore in-lane, plus one exchange between lane l and lane l^32 and
 // one between the two waves that split a tile's 256 vocabulary rows.
+//
+// Workgroup tile: 256 A rows x 256 B rows, 8 waves (2 per SIMD) arranged
+// 2 (A) x 4 (B); each wave owns 128 A rows x 64 B rows = 4 x 2 MFMA blocks
+// of 32x32.  B rows come in two 128-row halves; a wave's block 0 is in half 0
+// and block 1 in half 1 at the same offset, so for the loss kernels (half 0 =
+// student tokens, half 1 = teacher rows of the same tokens) a lane holds the
+// student and teacher logits of one token.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,10 +30,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;          // 4 waves of 64
-constexpr int kTileA = 256;            // A rows per workgroup tile
-constexpr int kTileB = 256;            // B rows per workgroup tile (2 halves)
-constexpr int kRowBytes = 128;         // bytes of K staged per row per step
+constexpr int kThreads = 512;            // 8 waves of 64, 2 per SIMD
+constexpr int kRowBytes = 128;           // bytes of K staged per row per step
 constexpr int kLdsRow = kRowBytes + 16;  // padded LDS row: conflict-free b128 reads
 constexpr int kLdsTile = 256 * kLdsRow;  // one operand tile
 constexpr int kLdsBytes = 4 * kLdsTile;  // double-buffered A and B: 144 KiB
@@ -75,28 +81,38 @@ template <> struct Traits<float> {
 template <class T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
 template <class T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
 
+// Wave coordinates inside the workgroup tile.
+__device__ __forceinline__ int wave_m() { return (threadIdx.x >> 6) >> 2; }  // 0..1
+__device__ __forceinline__ int wave_n() { return (threadIdx.x >> 6) & 3; }   // 0..3
+
 // Row (within the wave's 128-row A slice) held by accumulator register r of
 // 32x32 block mb for this lane: 8*(r/4) + 4*(lane/32) + r%4 (+ 32*mb).
 __device__ __forceinline__ int acc_row(int mb, int r, int lane) {
   return mb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
 }
-// First B row of accumulator block nb inside the 256-row B tile for wave
-// column wn: blocks 0,1 come from half 0, blocks 2,3 from half 1, at the
-// same offsets, so block nb and nb+2 hold the same token of the two halves.
-__device__ __forceinline__ int acc_col0(int nb, int wn) {
-  return (nb >> 1) * 128 + wn * 64 + (nb & 1) * 32;
+// First B row of accumulator block nb (0: half 0, 1: half 1) for wave column wn.
+__device__ __forceinline__ int acc_col0(int nb, int wn) { return nb * 128 + wn * 32; }
+
+// XCD-aware order.  Workgroup b is dispatched to XCD b % 8; renumber so each
+// XCD receives one contiguous run of the logical tile sequence (its L2 then
+// sees neighbouring tiles that share operand rows).  Bijective for any count.
+__device__ __forceinline__ int xcd_order(int b, int total) {
+  const int per = total / 8, extra = total % 8;
+  const int x = b % 8, local = b / 8;
+  return x * per + min(x, extra) + local;
 }
 
 // ------------------------------------------------- global -> LDS staging
 // A ROWS x 128-byte slab of a row-major [rows x K] operand.  Thread i moves
-// 16-byte chunk (i % 8) of rows i/8, i/8 + 32, ...: each row segment is one
+// 16-byte chunk (i % 8) of rows i/8, i/8 + 64, ...: each row segment is one
 // fully used 128-byte line.  Rows >= rows_valid and columns >= K read as 0.
 // Contract (checked by the host): the operand base and leading dimension
 // are 16-byte aligned and K is a multiple of 16 / sizeof(T), so a chunk is
 // either wholly inside or wholly outside [0, K).
 template <class T, int ROWS>
 struct Stage {
-  static constexpr int kLoads = ROWS / 32;
+  static constexpr int kRowsPerPass = kThreads / 8;
+  static constexpr int kLoads = ROWS / kRowsPerPass;
   static constexpr int kElems = 16 / sizeof(T);
   uint4 v[kLoads];
 
@@ -106,16 +122,17 @@ struct Stage {
     const T* p = base + (int64_t)(tid >> 3) * ld + kc;
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
-      const int r = (tid >> 3) + 32 * j;
-      v[j] = (r < rows_valid && kc < K) ? *reinterpret_cast<const uint4*>(p + (int64_t)(32 * j) * ld)
-                                        : make_uint4(0u, 0u, 0u, 0u);
+      const int r = (tid >> 3) + kRowsPerPass * j;
+      v[j] = (r < rows_valid && kc < K)
+                 ? *reinterpret_cast<const uint4*>(p + (int64_t)(kRowsPerPass * j) * ld)
+                 : make_uint4(0u, 0u, 0u, 0u);
     }
   }
   __device__ __forceinline__ void store(char* lds) const {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
-      const int r = (tid >> 3) + 32 * j;
+      const int r = (tid >> 3) + kRowsPerPass * j;
       *reinterpret_cast<uint4*>(lds + r * kLdsRow + (tid & 7) * 16) = v[j];
     }
   }
@@ -135,30 +152,33 @@ __device__ __forceinline__ typename Traits<T>::Frag frag(const char* tile, int r
   }
 }
 
-__device__ __forceinline__ void zero_acc(f32x16 (&acc)[4][4]) {
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[4][2]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 }
 
-// acc[mb][nb] += A[wm*128 + mb*32 .. +32, :] * Bhalf[...]^T over K.
+// acc[mb][nb] += A[wm*128 + mb*32 .. +32, :] * Bhalf_nb[wn*32 .. +32, :]^T over K.
 // H0/H1 select which 128-row halves of the B tile take part.  A points at the
 // tile's first row with a_rows valid rows from there (likewise B0, B1).
-// Double-buffered LDS with register prefetch: one barrier per K step.
+// Double-buffered LDS with register prefetch of the next K step (written to
+// LDS halfway through the current one) and MFMA fragments read one K
+// sub-step ahead; one barrier per K step.
 template <class T, bool H0, bool H1>
-__device__ __forceinline__ void mainloop(f32x16 (&acc)[4][4], char* lds,
+__device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], char* lds,
                                          const T* A, int64_t lda, int64_t a_rows,
                                          const T* B0, int64_t ldb0, int64_t b0_rows,
                                          const T* B1, int64_t ldb1, int64_t b1_rows,
                                          int64_t K) {
   using Tr = Traits<T>;
+  using Frag = typename Tr::Frag;
   constexpr int BK = Tr::kBK;
   constexpr int KS = BK / Tr::kKStep;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  constexpr int kStoreAt = KS / 2 - 1;
+  const int wm = wave_m(), wn = wave_n();
   Stage<T, 256> ga;
   Stage<T, 128> gb0, gb1;
   const int nk = (int)((K + BK - 1) / BK);
@@ -186,28 +206,32 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][4], char* lds,
       if (H0) gb0.load(B0, ldb0, b0_rows, k0, K);
       if (H1) gb1.load(B1, ldb1, b1_rows, k0, K);
     }
+    Frag a[2][4], b[2][2];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) a[0][mb] = frag<T>(as, wm * 128 + mb * 32, 0);
+    if (H0) b[0][0] = frag<T>(bs, acc_col0(0, wn), 0);
+    if (H1) b[0][1] = frag<T>(bs, acc_col0(1, wn), 0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      typename Tr::Frag a[4], b[4];
+      const int cur = ks & 1;
+      if (ks + 1 < KS) {
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) a[mb] = frag<T>(as, wm * 128 + mb * 32, ks);
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        if ((nb < 2 && H0) || (nb >= 2 && H1)) b[nb] = frag<T>(bs, acc_col0(nb, wn), ks);
+        for (int mb = 0; mb < 4; ++mb) a[cur ^ 1][mb] = frag<T>(as, wm * 128 + mb * 32, ks + 1);
+        if (H0) b[cur ^ 1][0] = frag<T>(bs, acc_col0(0, wn), ks + 1);
+        if (H1) b[cur ^ 1][1] = frag<T>(bs, acc_col0(1, wn), ks + 1);
       }
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          if ((nb < 2 && H0) || (nb >= 2 && H1)) acc[mb][nb] = Tr::mma(a[mb], b[nb], acc[mb][nb]);
-        }
-    }
-    if (more) {
-      char* an = (kt & 1) ? abuf0 : abuf1;
-      char* bn = (kt & 1) ? bbuf0 : bbuf1;
-      ga.store(an);
-      if (H0) gb0.store(bn);
-      if (H1) gb1.store(bn + 128 * kLdsRow);
+      for (int mb = 0; mb < 4; ++mb) {
+        if (H0) acc[mb][0] = Tr::mma(a[cur][mb], b[cur][0], acc[mb][0]);
+        if (H1) acc[mb][1] = Tr::mma(a[cur][mb], b[cur][1], acc[mb][1]);
+      }
+      if (ks == kStoreAt && more) {
+        char* an = (kt & 1) ? abuf0 : abuf1;
+        char* bn = (kt & 1) ? bbuf0 : bbuf1;
+        ga.store(an);
+        if (H0) gb0.store(bn);
+        if (H1) gb1.store(bn + 128 * kLdsRow);
+      }
     }
     __syncthreads();
   }
