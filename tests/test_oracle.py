@@ -1,0 +1,335 @@
+"""Pins of the CPU oracle (oracle/orda_oracle.py) -- CPU only.
+
+Each check reaches the oracle's numbers by an independent route, chosen so
+that a plausible mistake (a dropped term, a wrong sign or index, a swapped
+operand) fails:
+
+* torch float64 autograd through F.cross_entropy / F.log_softmax / F.kl_div,
+  the formulation of the reference's own test oracle
+  (test/utils/reference.py:60-93), on the reference's CPU test cases
+  (test/correctness/test_torch_backend_cpu.py, seeds 101-106);
+* scipy.stats.entropy and scipy.spatial.distance.jensenshannon for the
+  divergence values;
+* closed-form identities between divergences;
+* central finite differences of the oracle's own loss for every gradient;
+* invariants: all-ignored rows give exact zeros, D(p || p) = 0, a per-row
+  logit shift changes nothing, sum = mean * count.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from scipy.spatial.distance import jensenshannon
+from scipy.stats import entropy
+
+from oracle.orda_oracle import DIVERGENCE_DEFS, distillation_loss_oracle, divergence_value_and_grad
+
+DIVS = sorted(DIVERGENCE_DEFS)
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _inputs(seed, N=9, H=7, V=17, Ht=None, ignore_every=4):
+    r = _rng(seed)
+    hs = r.standard_normal((N, H)) * 0.5
+    ht = r.standard_normal((N, Ht or H)) * 0.5
+    W = r.standard_normal((V, H)) * 0.5
+    Wt = r.standard_normal((V, Ht or H)) * 0.5
+    y = r.integers(0, V, N)
+    if ignore_every:
+        y[::ignore_every] = -100
+    return hs, ht, W, Wt, y
+
+
+def _torch_ref(mode, hs, W, y, *, ht=None, Wt=None, lt=None, w_s, w_t, kl_w, T, reduction):
+    """float64 autograd of the reference test oracle's formulation."""
+    hs_t = torch.tensor(hs, requires_grad=True)
+    W_t = torch.tensor(W, requires_grad=True)
+    y_t = torch.tensor(y)
+    logits_s = hs_t @ W_t.t()
+    extra = {}
+    if mode == "tied":
+        ht_t = torch.tensor(ht, requires_grad=True)
+        logits_t = ht_t @ W_t.t()
+        extra["ht"] = ht_t
+    elif mode == "separate":
+        ht_t = torch.tensor(ht, requires_grad=True)
+        wt_t = torch.tensor(Wt, requires_grad=True)
+        logits_t = ht_t @ wt_t.t()
+        extra["ht"], extra["wt"] = ht_t, wt_t
+    else:
+        logits_t = torch.tensor(lt)
+    ce_s = F.cross_entropy(logits_s, y_t, ignore_index=-100, reduction="none")
+    ce_t = F.cross_entropy(logits_t, y_t, ignore_index=-100, reduction="none")
+    mask = y_t != -100
+    denom = max(int(mask.sum()), 1)
+    kl = F.kl_div(F.log_softmax(logits_s / T, -1), F.softmax(logits_t.detach() / T, -1), reduction="none").sum(-1)
+    kl = (kl * T * T).masked_fill(~mask, 0.0)
+    if reduction == "mean":
+        s, t, k = ce_s.sum() / denom, ce_t.sum() / denom, kl.sum() / denom
+    else:
+        s, t, k = ce_s.sum(), ce_t.sum(), kl.sum()
+    t = t if w_t != 0.0 else t.new_zeros(())
+    loss = w_s * s + w_t * t + kl_w * k
+    loss.backward()
+    out = {"loss": loss.item(), "student_ce": s.item(), "teacher_ce": t.item(), "kl": k.item(),
+           "grad_student_hidden": hs_t.grad.numpy(), "grad_weight": W_t.grad.numpy()}
+    if "ht" in extra and extra["ht"].grad is not None:
+        out["grad_teacher_hidden"] = extra["ht"].grad.numpy()
+    if "wt" in extra and extra["wt"].grad is not None:
+        out["grad_teacher_weight"] = extra["wt"].grad.numpy()
+    return out
+
+
+def _assert_match(a, b, keys, tol=1e-9):
+    for k in keys:
+        np.testing.assert_allclose(a[k], b[k], rtol=tol, atol=tol, err_msg=k)
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_tied_matches_torch_float64_reference(reduction):
+    hs, ht, W, _, y = _inputs(101)
+    kw = dict(w_s=0.8, w_t=0.25, kl_w=0.35, T=1.4, reduction=reduction)
+    ref = _torch_ref("tied", hs, W, y, ht=ht, **kw)
+    got = distillation_loss_oracle("tied", hs, W, y, teacher_hidden=ht, student_ce_weight=0.8, teacher_ce_weight=0.25,
+                                   kl_weight=0.35, kl_temperature=1.4, reduction=reduction)
+    _assert_match(got, ref, ["loss", "student_ce", "teacher_ce", "kl", "grad_student_hidden", "grad_weight",
+                             "grad_teacher_hidden"])
+
+
+def test_separate_full_matches_torch_float64_reference():
+    hs, ht, W, Wt, y = _inputs(103, N=10, H=6, V=19, Ht=8)
+    ref = _torch_ref("separate", hs, W, y, ht=ht, Wt=Wt, w_s=1.0, w_t=1.0, kl_w=0.4, T=1.6, reduction="mean")
+    got = distillation_loss_oracle("separate", hs, W, y, teacher_hidden=ht, teacher_weight=Wt, teacher_ce_weight=1.0,
+                                   kl_weight=0.4, kl_temperature=1.6)
+    _assert_match(got, ref, ["loss", "student_ce", "teacher_ce", "kl", "grad_student_hidden", "grad_weight",
+                             "grad_teacher_hidden", "grad_teacher_weight"])
+
+
+def test_separate_student_only_matches_torch_float64_reference():
+    hs, ht, W, Wt, y = _inputs(102, N=10, H=6, V=19, Ht=8)
+    ref = _torch_ref("separate", hs, W, y, ht=ht, Wt=Wt, w_s=1.0, w_t=0.0, kl_w=0.4, T=1.6, reduction="mean")
+    got = distillation_loss_oracle("separate", hs, W, y, teacher_hidden=ht, teacher_weight=Wt, kl_weight=0.4,
+                                   kl_temperature=1.6, teacher_grads=False)
+    assert got["teacher_ce"] == 0.0
+    _assert_match(got, ref, ["loss", "student_ce", "kl", "grad_student_hidden", "grad_weight"])
+
+
+def test_precomputed_logits_matches_torch_float64_reference():
+    hs, _, W, _, y = _inputs(104, N=11, H=7, V=23)
+    lt = _rng(5).standard_normal((11, 23)) * 0.3
+    ref = _torch_ref("precomputed", hs, W, y, lt=lt, w_s=1.0, w_t=0.0, kl_w=0.3, T=1.5, reduction="mean")
+    got = distillation_loss_oracle("precomputed", hs, W, y, teacher_logits=lt, kl_weight=0.3, kl_temperature=1.5)
+    _assert_match(got, ref, ["loss", "student_ce", "kl", "grad_student_hidden", "grad_weight"])
+
+
+def test_precomputed_hidden_equals_precomputed_logits():
+    hs, ht, W, Wt, y = _inputs(105, N=11, H=7, V=23, Ht=9)
+    a = distillation_loss_oracle("precomputed", hs, W, y, teacher_hidden=ht, teacher_weight=Wt, kl_weight=0.3,
+                                 kl_temperature=1.5)
+    b = distillation_loss_oracle("precomputed", hs, W, y, teacher_logits=ht @ Wt.T, kl_weight=0.3,
+                                 kl_temperature=1.5)
+    _assert_match(a, b, ["loss", "kl", "grad_student_hidden", "grad_weight"], tol=1e-12)
+
+
+def test_all_ignored_rows_give_exact_zeros():
+    hs, ht, W, _, _ = _inputs(106, N=8, H=6, V=13)
+    y = np.full(8, -100)
+    out = distillation_loss_oracle("tied", hs, W, y, teacher_hidden=ht, kl_weight=0.5, kl_temperature=1.7)
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        assert out[k] == 0.0
+    for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden"):
+        assert not np.any(out[k])
+
+
+def test_sum_equals_mean_times_count():
+    hs, ht, W, _, y = _inputs(7, N=12, V=30)
+    kw = dict(teacher_hidden=ht, kl_weight=0.6, kl_temperature=2.0, divergence="jsd")
+    m = distillation_loss_oracle("tied", hs, W, y, reduction="mean", **kw)
+    s = distillation_loss_oracle("tied", hs, W, y, reduction="sum", **kw)
+    for k in ("loss", "student_ce", "teacher_ce", "kl"):
+        assert np.isclose(s[k], m[k] * m["count"], rtol=1e-12)
+
+
+def test_kernel_semantics_zero_kl_when_weight_zero():
+    hs, ht, W, _, y = _inputs(8)
+    k = distillation_loss_oracle("tied", hs, W, y, teacher_hidden=ht, kl_weight=0.0)
+    t = distillation_loss_oracle("tied", hs, W, y, teacher_hidden=ht, kl_weight=0.0, kernel_semantics=False)
+    assert k["kl"] == 0.0 and t["kl"] > 0.0
+    assert k["loss"] == t["loss"]
+
+
+def test_out_of_range_label_is_class_zero():
+    hs, ht, W, _, y = _inputs(9, ignore_every=0)
+    y2 = y.copy()
+    y2[3] = 10_000
+    y3 = y.copy()
+    y3[3] = 0
+    a = distillation_loss_oracle("tied", hs, W, y2, teacher_hidden=ht, kl_weight=0.2)
+    b = distillation_loss_oracle("tied", hs, W, y3, teacher_hidden=ht, kl_weight=0.2)
+    _assert_match(a, b, ["loss", "grad_student_hidden", "grad_weight"], tol=0)
+
+
+# ---------------------------------------------------------------- divergences
+def _probs(seed, rows=5, V=12, scale=1.5):
+    r = _rng(seed)
+    return r.standard_normal((rows, V)) * scale, r.standard_normal((rows, V)) * scale
+
+
+def _softmax(z):
+    e = np.exp(z - z.max(-1, keepdims=True))
+    return e / e.sum(-1, keepdims=True)
+
+
+def test_kl_values_match_scipy_entropy():
+    zt, zs = _probs(1)
+    pt, ps = _softmax(zt), _softmax(zs)
+    f, _ = divergence_value_and_grad(zt, zs, "forward_kl")
+    r, _ = divergence_value_and_grad(zt, zs, "reverse_kl")
+    s, _ = divergence_value_and_grad(zt, zs, "symmetric_kl")
+    c, _ = divergence_value_and_grad(zt, zs, "soft_target_ce")
+    for i in range(zt.shape[0]):
+        assert np.isclose(f[i], entropy(pt[i], ps[i]), rtol=1e-12)
+        assert np.isclose(r[i], entropy(ps[i], pt[i]), rtol=1e-12)
+        assert np.isclose(s[i], entropy(pt[i], ps[i]) + entropy(ps[i], pt[i]), rtol=1e-12)
+        assert np.isclose(c[i], entropy(pt[i], ps[i]) + entropy(pt[i]), rtol=1e-12)
+
+
+def test_jsd_matches_scipy_jensenshannon():
+    zt, zs = _probs(2)
+    pt, ps = _softmax(zt), _softmax(zs)
+    v, _ = divergence_value_and_grad(zt, zs, "jsd", beta=0.5)
+    for i in range(zt.shape[0]):
+        assert np.isclose(v[i], jensenshannon(pt[i], ps[i]) ** 2, rtol=1e-10)
+
+
+def test_tvd_matches_l1_definition_and_pinsker():
+    zt, zs = _probs(3)
+    pt, ps = _softmax(zt), _softmax(zs)
+    v, _ = divergence_value_and_grad(zt, zs, "tvd")
+    f, _ = divergence_value_and_grad(zt, zs, "forward_kl")
+    for i in range(zt.shape[0]):
+        assert np.isclose(v[i], np.max([np.sum(np.maximum(pt[i] - ps[i], 0)), 0.0]), rtol=1e-12)  # TV = sum (p-q)_+
+        assert v[i] <= np.sqrt(f[i] / 2) + 1e-12  # Pinsker
+
+
+def test_power_family_identities():
+    zt, zs = _probs(4)
+    pt, ps = _softmax(zt), _softmax(zs)
+    hel, _ = divergence_value_and_grad(zt, zs, "hellinger")
+    bha, _ = divergence_value_and_grad(zt, zs, "bhattacharyya")
+    ren, _ = divergence_value_and_grad(zt, zs, "renyi", alpha=0.5)
+    ama, _ = divergence_value_and_grad(zt, zs, "amari_alpha", alpha=0.5)
+    ab, _ = divergence_value_and_grad(zt, zs, "ab", alpha=0.5, beta=0.5)
+    ab2, _ = divergence_value_and_grad(zt, zs, "ab", alpha=0.3, beta=0.7)
+    am3, _ = divergence_value_and_grad(zt, zs, "amari_alpha", alpha=0.3)
+    chi, _ = divergence_value_and_grad(zt, zs, "chi_squared")
+    l2, _ = divergence_value_and_grad(zt, zs, "squared_l2")
+    fkl, _ = divergence_value_and_grad(zt, zs, "forward_kl")
+    ren1, _ = divergence_value_and_grad(zt, zs, "renyi", alpha=1.0 - 1e-6)
+    bc = np.sum(np.sqrt(pt * ps), -1)
+    np.testing.assert_allclose(hel, 1 - bc, rtol=1e-12)
+    np.testing.assert_allclose(bha, -np.log(bc), rtol=1e-12)
+    np.testing.assert_allclose(ren, 2 * bha, rtol=1e-12)          # Renyi(1/2) = 2 Bhattacharyya
+    np.testing.assert_allclose(ama, 4 * hel, rtol=1e-12)          # Amari(1/2) = 4 H^2
+    np.testing.assert_allclose(ab, 4 * hel, rtol=1e-12)           # AB(1/2,1/2) = 4 H^2
+    np.testing.assert_allclose(ab2, am3, rtol=1e-10)              # AB(a, 1-a) = Amari(a)
+    np.testing.assert_allclose(ren1, fkl, rtol=1e-4)              # Renyi -> KL as alpha -> 1
+    np.testing.assert_allclose(chi, np.sum((pt - ps) ** 2 / ps, -1), rtol=1e-12)
+    np.testing.assert_allclose(l2, np.sum((pt - ps) ** 2, -1), rtol=1e-12)
+
+
+def test_skew_divergences_reduce_to_kl_at_alpha_zero():
+    zt, zs = _probs(5)
+    f, gf = divergence_value_and_grad(zt, zs, "forward_kl")
+    r, gr = divergence_value_and_grad(zt, zs, "reverse_kl")
+    sf, gsf = divergence_value_and_grad(zt, zs, "skew_forward_kl", alpha=0.0)
+    sr, gsr = divergence_value_and_grad(zt, zs, "skew_reverse_kl", alpha=0.0)
+    np.testing.assert_allclose(sf, f, rtol=1e-12)
+    np.testing.assert_allclose(sr, r, rtol=1e-12)
+    np.testing.assert_allclose(gsf, gf, rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(gsr, gr, rtol=1e-10, atol=1e-14)
+
+
+@pytest.mark.parametrize("name", DIVS)
+def test_divergence_is_zero_at_equal_distributions(name):
+    zt, _ = _probs(6)
+    v, g = divergence_value_and_grad(zt, zt + 0.7, name)  # shifted logits: same distribution
+    if name == "soft_target_ce":
+        np.testing.assert_allclose(v, [entropy(p) for p in _softmax(zt)], rtol=1e-12)
+    else:
+        np.testing.assert_allclose(v, 0.0, atol=1e-12)
+        if name != "tvd":  # |.| has no gradient at 0
+            np.testing.assert_allclose(g, 0.0, atol=1e-12)
+
+
+@pytest.mark.parametrize("name", DIVS)
+def test_divergence_gradient_matches_finite_differences(name):
+    zt, zs = _probs(7, rows=2, V=7)
+    _, g = divergence_value_and_grad(zt, zs, name)
+    eps = 1e-6
+    num = np.zeros_like(zs)
+    for i in range(zs.shape[0]):
+        for j in range(zs.shape[1]):
+            zp, zm = zs.copy(), zs.copy()
+            zp[i, j] += eps
+            zm[i, j] -= eps
+            vp, _ = divergence_value_and_grad(zt, zp, name)
+            vm, _ = divergence_value_and_grad(zt, zm, name)
+            num[i, j] = (vp[i] - vm[i]) / (2 * eps)
+    np.testing.assert_allclose(g, num, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("name", DIVS)
+def test_divergence_gradient_matches_torch_autograd(name):
+    from orda_ce_kernel.divergences import divergence_rows_torch, resolve_divergence
+
+    zt, zs = _probs(8, rows=3, V=9)
+    _, g = divergence_value_and_grad(zt, zs, name)
+    zs_t = torch.tensor(zs, requires_grad=True)
+    v = divergence_rows_torch(torch.log_softmax(zs_t, -1), torch.log_softmax(torch.tensor(zt), -1),
+                              resolve_divergence(name))
+    v.sum().backward()
+    np.testing.assert_allclose(zs_t.grad.numpy(), g, rtol=1e-9, atol=1e-12)
+
+
+def _fd(fn, arr, eps=1e-6):
+    num = np.zeros_like(arr)
+    for idx in np.ndindex(arr.shape):
+        orig = arr[idx]
+        arr[idx] = orig + eps
+        lp = fn()
+        arr[idx] = orig - eps
+        lm = fn()
+        arr[idx] = orig
+        num[idx] = (lp - lm) / (2 * eps)
+    return num
+
+
+def test_loss_gradient_matches_finite_differences_with_temperature():
+    """The teacher distribution is detached in the divergence (reference
+    api.py:319), so finite differences through the teacher path are taken
+    with the divergence off, and the divergence's W gradient is checked with
+    the teacher logits held fixed (precomputed mode)."""
+    hs, ht, W, _, y = _inputs(11, N=4, H=3, V=6)
+    kw = dict(teacher_hidden=ht, kl_weight=0.7, kl_temperature=2.5, divergence="jsd", teacher_ce_weight=0.3)
+    out = distillation_loss_oracle("tied", hs, W, y, **kw)
+    num = _fd(lambda: distillation_loss_oracle("tied", hs, W, y, **kw)["loss"], hs)
+    np.testing.assert_allclose(out["grad_student_hidden"], num, rtol=1e-5, atol=1e-8)
+
+    kw_ce = dict(kw, kl_weight=0.0)
+    out_ce = distillation_loss_oracle("tied", hs, W, y, **kw_ce)
+    for arr, key in ((ht, "grad_teacher_hidden"), (W, "grad_weight")):
+        num = _fd(lambda: distillation_loss_oracle("tied", hs, W, y, **kw_ce)["loss"], arr)
+        np.testing.assert_allclose(out_ce[key], num, rtol=1e-5, atol=1e-8, err_msg=key)
+    assert np.allclose(out["grad_teacher_hidden"], out_ce["grad_teacher_hidden"])
+
+    lt = ht @ W.T
+    kw_p = dict(teacher_logits=lt, kl_weight=0.7, kl_temperature=2.5, divergence="jsd")
+    out_p = distillation_loss_oracle("precomputed", hs, W, y, **kw_p)
+    num = _fd(lambda: distillation_loss_oracle("precomputed", hs, W, y, **kw_p)["loss"], W)
+    np.testing.assert_allclose(out_p["grad_weight"], num, rtol=1e-5, atol=1e-8)
