@@ -318,9 +318,8 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
   constexpr bool kPhase1 = SV >= SV_JSD;
   const int lane = threadIdx.x & 63;
   const int wm = wave_m(), wn = wave_n();
-  const int t = xcd_order(blockIdx.x, gridDim.x);
-  const int tt = t % P.n_ttiles;
-  const int vr = t / P.n_ttiles;
+  int tt, vr;
+  grouped_tile<4>(xcd_order(blockIdx.x, gridDim.x), P.n_ttiles, P.n_vranges, tt, vr);
   const int64_t t0 = (int64_t)tt * 128;
   const int vt_begin = vr * P.tiles_per_range;
   const int vt_end = min(vt_begin + P.tiles_per_range, P.n_vtiles);
@@ -377,29 +376,53 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
 }
 
 // ----------------------------------------------------------- dlogits kernel
+// Store 4 consecutive elements (one 8-byte or 16-byte store when full; p is
+// then aligned by construction), else the first n.
+template <class T>
+__device__ __forceinline__ void store4(T* p, const float (&x)[4], bool full, int n) {
+  if (full) {
+    if constexpr (sizeof(T) == 2) {
+      union { T e[4]; uint2 u; } v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v.e[i] = from_f32<T>(x[i]);
+      *reinterpret_cast<uint2*>(p) = v.u;
+    } else {
+      *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < n) p[i] = from_f32<T>(x[i]);
+  }
+}
+
 template <class T, int DIV, bool T1>
 __device__ __forceinline__ void dl_tile(const f32x16 (&acc)[4][2], const FusedParams& P, int64_t v0,
                                         int64_t t0) {
   const int lane = threadIdx.x & 63;
   const int wm = wave_m(), wn = wave_n();
   const int64_t t = t0 + wn * 32 + (lane & 31);
-  if (t >= P.N) return;
+  // lanes past the last token stay active (the quad transpose below needs
+  // every lane of a quad); they read token 0's row data, produce zeros and
+  // store nothing
+  const bool tok_ok = t < P.N;
+  const int64_t tr = tok_ok ? t : 0;
   const float scale = P.grad_output[0] * P.mean_scale[0];
   const float invT = P.invT;
   const int64_t vend = min(P.V, P.vc0 + P.vcc);
   T* dLT = static_cast<T*>(P.dLT);
   T* dLNs = static_cast<T*>(P.dLNs);
   T* dLNt = static_cast<T*>(P.dLNt);
-  const int64_t y = P.labels[t];
-  const bool ignored = (y == P.ignore_index);
+  const int64_t y = P.labels[tr];
+  const bool ignored = !tok_ok || (y == P.ignore_index);
   const int64_t yeff = (y >= 0 && y < P.V) ? y : 0;
-  const float lse_s = P.rowp[0 * P.N + t];
-  const float lse_sT = P.rowp[1 * P.N + t];
-  const float lse_t = P.rowp[2 * P.N + t];
-  const float lse_tT = P.rowp[3 * P.N + t];
+  const float lse_s = P.rowp[0 * P.N + tr];
+  const float lse_sT = P.rowp[1 * P.N + tr];
+  const float lse_t = P.rowp[2 * P.N + tr];
+  const float lse_tT = P.rowp[3 * P.N + tr];
   float c[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) c[i] = P.rowp[(4 + i) * P.N + t];
+  for (int i = 0; i < 4; ++i) c[i] = P.rowp[(4 + i) * P.N + tr];
   const float sc_s = ignored ? 0.f : scale * P.w_s;
   const float sc_t = ignored ? 0.f : scale * P.w_t;
   const float sc_d = ignored ? 0.f : scale * P.w_kl * P.temperature;
@@ -434,13 +457,27 @@ __device__ __forceinline__ void dl_tile(const f32x16 (&acc)[4][2], const FusedPa
         }
       }
       const int64_t vl = vg - P.vc0;  // row inside the chunk
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (vg + e >= vend) continue;
-        if (P.w_dlt_s) dLT[(vl + e) * P.ldT + t] = from_f32<T>(gs[e]);
-        if (P.w_dlt_t) dLT[(vl + e) * P.ldT + P.tcol + t] = from_f32<T>(gt[e]);
-        if (P.w_dln_s) dLNs[t * P.ldN + vl + e] = from_f32<T>(gs[e]);
-        if (P.w_dln_t) dLNt[t * P.ldN + vl + e] = from_f32<T>(gt[e]);
+      const bool rows_full = vg + 3 < vend;
+      // token-major staging: this lane's 4 consecutive rows are contiguous
+      if (P.w_dln_s && tok_ok) store4(dLNs + t * P.ldN + vl, gs, rows_full, (int)(vend - vg));
+      if (P.w_dln_t && tok_ok) store4(dLNt + t * P.ldN + vl, gt, rows_full, (int)(vend - vg));
+      // row-major staging: transpose inside the lane quad so each lane
+      // holds 4 consecutive tokens of one row
+      if (P.w_dlt_s || P.w_dlt_t) {
+        const int q = lane & 3;
+        const int64_t tb = t - q;  // first token of the quad
+        const int ntok = (int)min<int64_t>(P.N - tb, 4);
+        const bool row_ok = vg + q < vend;
+        if (P.w_dlt_s) {
+          float o[4];
+          quad_transpose(gs, o);
+          if (row_ok) store4(dLT + (vl + q) * P.ldT + tb, o, ntok == 4, ntok);
+        }
+        if (P.w_dlt_t) {
+          float o[4];
+          quad_transpose(gt, o);
+          if (row_ok) store4(dLT + (vl + q) * P.ldT + P.tcol + tb, o, ntok == 4, ntok);
+        }
       }
     }
 }
@@ -449,9 +486,8 @@ template <class T, int DIV, bool T1>
 __global__ __launch_bounds__(kThreads) void k_dl(FusedParams P) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   f32x16 acc[4][2];
-  const int b = xcd_order(blockIdx.x, gridDim.x);
-  const int tt = b % P.n_ttiles;
-  const int vt = b / P.n_ttiles;
+  int tt, vt;
+  grouped_tile<4>(xcd_order(blockIdx.x, gridDim.x), P.n_ttiles, gridDim.x / P.n_ttiles, tt, vt);
   const int64_t t0 = (int64_t)tt * 128;
   const int64_t v0 = P.vc0 + (int64_t)vt * 256;
   fused_logits<T>(acc, lds, P, v0, t0);

@@ -102,6 +102,46 @@ __device__ __forceinline__ int xcd_order(int b, int total) {
   return x * per + min(x, extra) + local;
 }
 
+// Grouped 2-D order of a (rows x cols) tile grid: groups of G columns are
+// walked column-fastest, so consecutive indices form G x (32 / G) blocks
+// and the ~32 workgroups an XCD runs at once share both operands' tiles.
+template <int G>
+__device__ __forceinline__ void grouped_tile(int t, int rows, int cols, int& row, int& col) {
+  const int group = t / (G * rows);
+  const int first = group * G;
+  const int width = min(cols - first, G);
+  const int rem = t % (G * rows);
+  col = first + rem % width;
+  row = rem / width;
+}
+
+// Value of v held by lane (q - j) mod 4 of this lane's quad (DPP quad_perm).
+template <int J>
+__device__ __forceinline__ float quad_rot(float v) {
+  constexpr int ctrl = J == 1 ? 0x93 : J == 2 ? 0x4E : 0x39;  // perm[q] = (q - J) & 3
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+// 4 x 4 transpose inside a lane quad: lane q holds x[e] = M[q][e]; on return
+// out[k] = M[k][q].
+__device__ __forceinline__ void quad_transpose(const float (&x)[4], float (&out)[4]) {
+  const int q = threadIdx.x & 3;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) out[k] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int si = (q + j) & 3;
+    const float send = si == 0 ? x[0] : si == 1 ? x[1] : si == 2 ? x[2] : x[3];
+    float recv = send;
+    if (j == 1) recv = quad_rot<1>(send);
+    if (j == 2) recv = quad_rot<2>(send);
+    if (j == 3) recv = quad_rot<3>(send);
+    const int di = (q - j) & 3;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[k] = (di == k) ? recv : out[k];
+  }
+}
+
 // ------------------------------------------------- global -> LDS staging
 // A ROWS x 128-byte slab of a row-major [rows x K] operand.  Thread i moves
 // 16-byte chunk (i % 8) of rows i/8, i/8 + 64, ...: each row segment is one
