@@ -225,6 +225,44 @@ def cpu_baseline(cfg, seed, budget_s):
     }
 
 
+KERNEL_OF_CLASS = {"scan": "k_scan", "dlogits": "k_dl", "gemm_w": "k_gemm", "gemm_h": "k_gemm"}
+
+
+def profiled_traffic(config: str, kernel_class: str):
+    """HBM bytes per launch of ``kernel_class`` at ``config`` from the
+    committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/*_pmc_traffic.md,
+    its fenced json line), or None when no summary covers it."""
+    kernel = KERNEL_OF_CLASS.get(kernel_class)
+    for md in sorted((ROOT / "profiles").glob("*_pmc_traffic.md")):
+        for line in md.read_text().splitlines():
+            line = line.strip()
+            if not (line.startswith("{") and "traffic_bytes_per_launch" in line):
+                continue
+            rec = json.loads(line)
+            if rec.get("workload") == config and rec.get("kernel") == kernel:
+                return float(rec["traffic_bytes_per_launch"]), md.name
+    return None, None
+
+
+def copy_calibration(mib: int) -> int:
+    """Three device copies of ``mib`` MiB each through an elementwise kernel
+    (dst = src * 1, fp32; a blit could go to the DMA engines and show no
+    dispatch): its HBM traffic is known exactly, mib MiB read + mib MiB
+    written per launch."""
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    n = mib << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 3}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -235,7 +273,12 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run 3 plain device copies of MIB MiB (the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box has one GPU); "
@@ -288,11 +331,14 @@ def main() -> int:
         mean_ms = k["ms"] / k["launches"]
         alg_per_launch = k["algorithmic_flops"] / k["launches"]
         achieved = alg_per_launch / (mean_ms / 1e3) / 1e12
+        traffic, source = profiled_traffic(args.config, dominant)
         result["roofline"] = {
             "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
-            "traffic": None, "kernel": dominant, "mean_launch_ms": mean_ms,
+            "traffic": traffic, "kernel": dominant, "mean_launch_ms": mean_ms,
             "algorithmic_tflop_per_launch": alg_per_launch / 1e12,
         }
+        if traffic is not None:
+            result["roofline"]["traffic_source"] = f"profiles/{source} (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)"
     if not args.no_cpu_baseline and mode == "tied":
         _log("[bench] CPU baseline")
         result["cpu_baseline"] = cpu_baseline(cfg, args.seed, args.cpu_budget)
