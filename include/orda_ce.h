@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define ORDA_ABI_VERSION 1
+#define ORDA_ABI_VERSION 2
 
 /* Teacher modes (reference api.py:21-52, ops/separate_teacher.py:1102). */
 enum orda_mode {
@@ -73,6 +73,16 @@ enum orda_divergence {
 #define ORDA_COMPUTE_TEACHER_CE (1u << 4) /* teacher CE value (and its grads) */
 #define ORDA_COMPUTE_DIVERGENCE (1u << 5) /* kl_weight != 0                  */
 #define ORDA_REDUCTION_SUM (1u << 6)      /* else mean                        */
+/* Compute the requested gradients inside orda_forward, one token chunk at a
+ * time, as the reference's Functions do (ops/tied_teacher.py:366-516): the
+ * chunk's logits are materialised in the workspace (vocabulary-major), turned
+ * into dlogits in place, and multiplied into the gradients; grad W is
+ * accumulated across chunks in the weight dtype (the reference's default,
+ * fp32_grad_weight_accumulation=False, ops/tied_teacher.py:354,488-495).
+ * orda_backward then only multiplies the gradients by grad_output
+ * (ops/tied_teacher.py:531-564).  TIED and SEPARATE modes; not the two-pass
+ * divergences (JSD, skew KLs, TVD): those return ORDA_EUNSUPPORTED. */
+#define ORDA_GRADS_IN_FORWARD (1u << 7)
 
 /* Error codes. */
 #define ORDA_OK 0
@@ -101,6 +111,9 @@ typedef struct orda_problem {
   float kl_weight;
   float div_alpha;        /* alpha of renyi, amari_alpha, ab, skew_*_kl       */
   float div_beta;         /* beta of jsd and ab                               */
+  int32_t reserved;
+  int64_t token_chunk;    /* tokens per chunk with ORDA_GRADS_IN_FORWARD;
+                             0 = library choice (chunk logits <= 512 MiB)     */
 } orda_problem_t;
 
 /* Tensors of one loss evaluation.  Unused pointers may be NULL. */
@@ -154,7 +167,9 @@ size_t orda_backward_workspace_bytes(const orda_problem_t* p);
  * PrecomputedCEFunction.forward (ops/precomputed_teacher.py:358-475): the
  * logits GEMMs (tied_teacher.py:444-445), the Triton row kernels
  * (tied_teacher.py:13-189) and the loss reduction (tied_teacher.py:499-516).
- * Writes out_loss/out_student_ce/out_teacher_ce/out_kl and `saved`. */
+ * Writes out_loss/out_student_ce/out_teacher_ce/out_kl and `saved`.  With
+ * ORDA_GRADS_IN_FORWARD it also writes every requested gradient (the grad_*
+ * pointers of t), scaled by the mean scale but not yet by grad_output. */
 int orda_forward(const orda_problem_t* p, const orda_tensors_t* t,
                  void* workspace, size_t workspace_bytes, void* stream);
 
@@ -163,7 +178,8 @@ int orda_forward(const orda_problem_t* p, const orda_tensors_t* t,
  * forward (ops/tied_teacher.py:468-495, separate_teacher.py:660-674,
  * 919-948, precomputed_teacher.py:443-457) and the scaling in backward
  * (ops/tied_teacher.py:531-564 and analogues).  Reads `saved` from the
- * matching orda_forward call. */
+ * matching orda_forward call.  With ORDA_GRADS_IN_FORWARD it only multiplies
+ * the gradients orda_forward wrote by grad_output, in place (no workspace). */
 int orda_backward(const orda_problem_t* p, const orda_tensors_t* t,
                   void* workspace, size_t workspace_bytes, void* stream);
 
@@ -174,6 +190,19 @@ int orda_backward(const orda_problem_t* p, const orda_tensors_t* t,
  * matmuls at ops/tied_teacher.py:445,473,493). */
 int orda_gemm_abt(int32_t dtype, int64_t M, int64_t N, int64_t K,
                   const void* A, const void* B, void* C, void* stream);
+
+/* General C = op(A) * op(B)^T in `dtype` with fp32 accumulation: a_mn = 0
+ * means A is [M x K] K-contiguous (leading dimension lda), a_mn = 1 means A
+ * is stored [K x M] (element (m, k) at A[k * lda + m]); likewise b_mn for B
+ * ([N x K] or [K x N]).  C is [M x N] with leading dimension ldc.  splits > 1
+ * splits K into that many fp32 partials summed in a fixed order; the
+ * workspace must then hold splits * M * N floats (else it may be NULL).
+ * Exposed for tests and callers that want the engine; it stands for the
+ * torch matmuls of ops/tied_teacher.py:445,473,493, whose operands the
+ * materialised path reads in both layouts. */
+int orda_gemm(int32_t dtype, int32_t a_mn, int32_t b_mn, int64_t M, int64_t N, int64_t K, const void* A,
+              int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int32_t splits, void* workspace,
+              size_t workspace_bytes, void* stream);
 
 /* Per-kernel-class timing, for benchmarks.  No counterpart in the reference,
  * whose benchmarks bracket whole steps with torch.cuda.Event

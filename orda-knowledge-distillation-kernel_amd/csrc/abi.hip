@@ -1,6 +1,7 @@
 // abi.hip -- the C ABI of liborda_ce.so (declared in include/orda_ce.h):
 // argument validation, the tile / workspace plan, and the launch sequences
 // of the forward and backward passes.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -43,6 +44,13 @@ inline size_t carve(size_t& off, size_t bytes) {
 constexpr int64_t kDefaultStagingBytes = 512ll << 20;
 // Target number of workgroups of a forward scan launch.
 constexpr int64_t kScanTargetGroups = 2048;
+// Default size of one token chunk's materialised logits (ORDA_GRADS_IN_FORWARD).
+constexpr int64_t kFusedLogitsBytes = 512ll << 20;
+// Workgroups of one chunk's scan: one per CU of an MI355X (256 CUs, one
+// 144 KiB-LDS workgroup each), so each walks a long run of vocabulary tiles.
+constexpr int64_t kFusedScanGroups = 256;
+// Target number of workgroups of a split-K grad-hidden GEMM.
+constexpr int64_t kSplitTargetGroups = 512;
 
 struct Plan {
   int mode, dtype, eb, kelems;
@@ -60,6 +68,12 @@ struct Plan {
   int bwd_tsrc;
   int64_t NP, ldT, ldh, Vc, nchunks;
   size_t off_hT, off_htT, off_dLT, off_dLNs, off_dLNt, off_WT, off_WtT, off_g32s, off_g32t, bwd_bytes;
+  // gradients inside forward (materialised token chunks)
+  bool fused, store_t;
+  int64_t fn, fnP, fldL, fnchunks;
+  int f_nvr, f_tpr, splits_s, splits_t;
+  int64_t kps_s, kps_t;
+  size_t off_L, off_fpart, off_flabelx, off_frowp, off_frowv, off_split;
 };
 
 constexpr int kScalFloats = 64;  // scalars at the head of the saved buffer
@@ -207,6 +221,57 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
   pl.off_g32s = (pl.need_gs && pl.nchunks > 1) ? carve(off, (size_t)pl.N * pl.H * 4) : 0;
   pl.off_g32t = (pl.w_dln_t && pl.nchunks > 1) ? carve(off, (size_t)pl.N * pl.Ht * 4) : 0;
   pl.bwd_bytes = off + kAlign;
+
+  // gradients inside forward: one token chunk of logits at a time
+  pl.fused = (f & ORDA_GRADS_IN_FORWARD) != 0;
+  if (pl.fused) {
+    if (!tied && !sep) return fail(ORDA_EUNSUPPORTED, "ORDA_GRADS_IN_FORWARD needs the TIED or SEPARATE mode");
+    if (pl.two_pass)
+      return fail(ORDA_EUNSUPPORTED, "ORDA_GRADS_IN_FORWARD does not support the two-pass divergences");
+    pl.store_t = pl.tsrc != TSRC_NONE;
+    const int64_t ncol = pl.store_t ? 2 : 1;
+    const int64_t Nr = round_up(pl.N, 8);
+    int64_t n = p->token_chunk;
+    if (n > 0) {
+      n = round_up(n, 8);
+    } else {
+      n = kFusedLogitsBytes / (pl.V * ncol * pl.eb) / 128 * 128;
+      if (n < 128) n = 128;
+    }
+    if (n > Nr) n = Nr;
+    pl.fn = n;
+    pl.fnP = round_up(n, 8);
+    pl.fldL = ncol * pl.fnP;
+    pl.fnchunks = cdiv(pl.N, n);
+    const int64_t ntt = cdiv(n, 128);
+    int64_t nvr = cdiv(kFusedScanGroups, ntt);
+    if (nvr < 1) nvr = 1;
+    if (nvr > pl.n_vtiles) nvr = pl.n_vtiles;
+    pl.f_tpr = (int)cdiv(pl.n_vtiles, nvr);
+    pl.f_nvr = (int)cdiv(pl.n_vtiles, pl.f_tpr);
+    auto split_plan = [&](int64_t cols, int& splits, int64_t& kps) {
+      const int64_t tiles = cdiv(n, 256) * cdiv(cols, 256);
+      int64_t sp = cdiv(kSplitTargetGroups, tiles);
+      if (sp > 16) sp = 16;
+      if (sp < 1) sp = 1;
+      kps = round_up(cdiv(pl.V, sp), 64);
+      splits = (int)cdiv(pl.V, kps);
+    };
+    split_plan(pl.H, pl.splits_s, pl.kps_s);
+    split_plan(pl.Ht, pl.splits_t, pl.kps_t);
+    size_t fo = 0;
+    pl.off_L = carve(fo, (size_t)pl.V * pl.fldL * pl.eb);
+    pl.off_fpart = carve(fo, (size_t)pl.f_nvr * kNStat * pl.fnP * 4);
+    pl.off_flabelx = carve(fo, (size_t)2 * pl.fnP * 4);
+    pl.off_frowp = carve(fo, (size_t)kNRowP * pl.fnP * 4);
+    pl.off_frowv = carve(fo, (size_t)3 * pl.N * 4);
+    int64_t split_cols = 0;
+    if (pl.need_gs && pl.splits_s > 1) split_cols = pl.splits_s * pl.H;
+    if (pl.w_dln_t && pl.splits_t > 1 && pl.splits_t * pl.Ht > split_cols) split_cols = pl.splits_t * pl.Ht;
+    pl.off_split = split_cols ? carve(fo, (size_t)split_cols * pl.fnP * 4) : 0;
+    pl.fwd_bytes = fo + kAlign;
+    pl.bwd_bytes = 0;
+  }
   return ORDA_OK;
 }
 
@@ -310,7 +375,7 @@ int run_forward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t
   M.t_is_one = pl.t1; M.has_t = pl.tsrc != TSRC_NONE; M.teacher_ce = pl.teacher_ce; M.div_on = pl.div_on;
   M.invT = F.invT; M.temperature = p->temperature; M.alpha = p->div_alpha; M.beta = p->div_beta;
   for (int i = 0; i < 3; ++i) { M.pa[i] = pl.pa[i]; M.pb[i] = pl.pb[i]; }
-  M.npow = pl.npow; M.rowp = rowp; M.rowv = rowv;
+  M.npow = pl.npow; M.rowp = rowp; M.rowv = rowv; M.ldv = pl.N;
   { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
 
   if (pl.two_pass) {
@@ -465,6 +530,184 @@ int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* 
   return ORDA_OK;
 }
 
+// One launch of the general GEMM (k_gemm2); B1/b_kseg/b_kval* describe an
+// MN-major B in two row segments (b_kseg = K, b_kval0 = K, B1 = NULL for
+// one).  splits > 1 writes fp32 partials [splits][M][N] to C32 (mode SPLIT).
+template <class T>
+int gemm2(int la, int lb, const void* A, int64_t lda, const void* B, int64_t ldb, const void* B1, int64_t ldb1,
+          int64_t b_kseg, int64_t b_kval0, int64_t b_kval1, void* C, float* C32, int64_t ldc, int64_t M,
+          int64_t N, int64_t K, int mode, int splits, int64_t kps, hipStream_t s, int kind, double alg) {
+  GemmParams G{};
+  G.A = A; G.B = B; G.C = C; G.C32 = C32;
+  G.M = M; G.N = N; G.K = K; G.lda = lda; G.ldb = ldb; G.ldc = ldc;
+  G.tiles_m = (int)cdiv(M, 256); G.tiles_n = (int)cdiv(N, 256); G.mode = mode;
+  G.la = la; G.lb = lb; G.B1 = B1; G.ldb1 = ldb1; G.b_kseg = b_kseg; G.b_kval0 = b_kval0; G.b_kval1 = b_kval1;
+  G.splits = splits < 1 ? 1 : splits;
+  G.k_per_split = G.splits > 1 ? kps : K;
+  G.split_stride = M * ldc;
+  if ((int64_t)G.tiles_m * G.tiles_n * G.splits > 0x7fffffffll) return fail(ORDA_EINVAL, "gemm grid too large");
+  Timed tm_(kind, s, alg, 2.0 * (double)M * (double)N * (double)K);
+  ORDA_CHECK_LAUNCH(launch_gemm2<T>(G, s));
+  return ORDA_OK;
+}
+
+// Forward with the gradients (ORDA_GRADS_IN_FORWARD), token chunk by token
+// chunk: label logits, the scan with the logits stored vocabulary-major in L,
+// the per-row merge, dlogits in place (k_dlm), grad W += dL^T [hs; ht]
+// (A = L K-major over tokens, B = the chunk's hidden states read MN-major),
+// grad hidden = dL W (A = L and B = W both MN-major, split over V).
+template <class T>
+int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, char* ws, hipStream_t s) {
+  const bool tied = pl.mode == ORDA_MODE_TIED, sep = pl.mode == ORDA_MODE_SEPARATE;
+  const int eb = pl.eb;
+  const int64_t N = pl.N, V = pl.V, H = pl.H, Ht = pl.Ht, nP = pl.fnP, ldL = pl.fldL;
+  char* L = ws + pl.off_L;
+  float* part = reinterpret_cast<float*>(ws + pl.off_fpart);
+  float* labelx = reinterpret_cast<float*>(ws + pl.off_flabelx);
+  float* rowp = reinterpret_cast<float*>(ws + pl.off_frowp);
+  float* rowv = reinterpret_cast<float*>(ws + pl.off_frowv);
+  float* split = reinterpret_cast<float*>(ws + pl.off_split);
+  float* scal = static_cast<float*>(t->saved);
+  const bool reduction_sum = (p->flags & ORDA_REDUCTION_SUM) != 0;
+  const bool tgrad = pl.w_dlt_t || pl.w_dln_t;
+  const bool any_grad = pl.need_gs || pl.need_gw || tgrad;
+  const T* hs = static_cast<const T*>(t->student_hidden);
+  const T* ht = static_cast<const T*>(t->teacher_hidden);
+  const T* W = static_cast<const T*>(t->weight);
+  const T* Wt = static_cast<const T*>(t->teacher_weight);
+
+  // mean scale first: the chunks' dlogits need it before the loss rows exist
+  { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_count(t->labels, N, p->ignore_index, reduction_sum, scal, s)); }
+
+  for (int64_t c = 0; c < pl.fnchunks; ++c) {
+    const int64_t r0 = c * pl.fn;
+    const int64_t nc = (N - r0 < pl.fn) ? N - r0 : pl.fn;
+
+    LabelParams Lb{};
+    Lb.hs = hs + r0 * H; Lb.W = W; Lb.ht = ht ? ht + r0 * Ht : nullptr; Lb.Wt = Wt; Lb.Lt = nullptr;
+    Lb.labels = t->labels + r0;
+    Lb.N = nc; Lb.V = V; Lb.H = H; Lb.Ht = Ht; Lb.ignore_index = p->ignore_index;
+    Lb.tsrc = pl.tsrc; Lb.lt_dtype = p->logits_dtype; Lb.out = labelx;
+    { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_label<T>(Lb, s)); }
+
+    FusedParams F{};
+    F.W = W; F.hs = hs + r0 * H; F.ht = ht ? ht + r0 * Ht : nullptr; F.Wt = Wt; F.Lt = nullptr;
+    F.labels = t->labels + r0;
+    F.N = nc; F.V = V; F.H = H; F.Ht = Ht; F.ignore_index = p->ignore_index;
+    F.tsrc = pl.tsrc; F.lt_dtype = p->logits_dtype;
+    F.div = pl.div; F.fam = pl.fam; F.t_is_one = pl.t1; F.tgrad = 0;
+    F.temperature = p->temperature; F.invT = 1.0f / p->temperature;
+    F.alpha = p->div_alpha; F.beta = p->div_beta;
+    F.log_alpha = std::log(p->div_alpha); F.log_1m_alpha = std::log1p(-p->div_alpha);
+    F.log_beta = std::log(p->div_beta); F.log_1m_beta = std::log1p(-p->div_beta);
+    for (int i = 0; i < 3; ++i) { F.pa[i] = pl.pa[i]; F.pb[i] = pl.pb[i]; }
+    F.npow = pl.npow;
+    F.phase = 0; F.n_ttiles = (int)cdiv(nc, 128); F.n_vranges = pl.f_nvr;
+    F.tiles_per_range = pl.f_tpr; F.n_vtiles = pl.n_vtiles;
+    F.partial = part; F.rowp = rowp;
+    F.Lout = L; F.ldL = ldL; F.tcolL = nP; F.store_t = pl.store_t;
+    const double scan_flops = 2.0 * (double)nc * (double)V * ((double)H + (pl.store_t ? (double)Ht : 0.0));
+    { Timed tm_(ORDA_K_SCAN, s, scan_flops, scan_flops); ORDA_CHECK_LAUNCH(launch_scan_store<T>(F, F.n_ttiles * pl.f_nvr, s)); }
+
+    MergeParams M{};
+    M.partial = part; M.n_vranges = pl.f_nvr; M.N = nc; M.V = V; M.ignore_index = p->ignore_index;
+    M.labels = t->labels + r0; M.label_x = labelx; M.phase = 0; M.fam = pl.fam; M.div = pl.div;
+    M.t_is_one = pl.t1; M.has_t = pl.tsrc != TSRC_NONE; M.teacher_ce = pl.teacher_ce; M.div_on = pl.div_on;
+    M.invT = F.invT; M.temperature = p->temperature; M.alpha = p->div_alpha; M.beta = p->div_beta;
+    for (int i = 0; i < 3; ++i) { M.pa[i] = pl.pa[i]; M.pb[i] = pl.pb[i]; }
+    M.npow = pl.npow; M.rowp = rowp; M.rowv = rowv + r0; M.ldv = N;
+    { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
+
+    if (!any_grad) continue;
+
+    DlmParams D{};
+    D.L = L; D.ldL = ldL; D.tcol = nP; D.labels = t->labels + r0; D.rowp = rowp; D.mean_scale = scal;
+    D.N = nc; D.V = V; D.ignore_index = p->ignore_index;
+    D.div = pl.div; D.t_is_one = pl.t1; D.tgrad = tgrad;
+    D.rows_per_block = (int)std::max<int64_t>(64, cdiv(V, 65535));  // grid.y stays <= 65535
+    D.invT = F.invT; D.temperature = p->temperature; D.alpha = p->div_alpha; D.beta = p->div_beta;
+    D.w_s = p->student_ce_weight; D.w_t = p->teacher_ce_weight; D.w_kl = pl.div_on ? p->kl_weight : 0.f;
+    { Timed tm_(ORDA_K_DLOGITS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_dlm<T>(D, s)); }
+
+    // token columns [nc, nP) of L are read by the grad-W GEMM (K = tokens):
+    // keep them zero (the matching hidden rows read as zero too)
+    if (nc < nP) {
+      { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(L, ldL, V, nc, nP, eb, s)); }
+      if (pl.store_t) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(L, ldL, V, nP + nc, 2 * nP, eb, s)); }
+    }
+
+    const int wmode = c == 0 ? GEMM_STORE : GEMM_ACC_T;
+    if (pl.need_gw) {
+      const bool both = tied && pl.w_dlt_t;
+      const int64_t K = both ? 2 * nP : nP;
+      ORDA_TRY(gemm2<T>(KMAJ, MNMAJ, L, ldL, hs + r0 * H, H, both ? ht + r0 * H : nullptr, H, nP, nc,
+                        both ? nc : 0, t->grad_weight, nullptr, H, V, H, K, wmode, 1, 0, s, ORDA_K_GEMM_W,
+                        2.0 * (double)V * (double)H * (double)(both ? 2 * nc : nc)));
+    }
+    if (sep && pl.need_gwt && pl.w_dlt_t) {
+      ORDA_TRY(gemm2<T>(KMAJ, MNMAJ, static_cast<char*>(L) + nP * eb, ldL, ht + r0 * Ht, Ht, nullptr, 0, nP, nc, 0,
+                        t->grad_teacher_weight, nullptr, Ht, V, Ht, nP, wmode, 1, 0, s, ORDA_K_GEMM_W,
+                        2.0 * (double)V * (double)Ht * (double)nc));
+    }
+    auto grad_hidden = [&](const char* Lcol, const T* Wx, int64_t Hx, void* out, int splits, int64_t kps) -> int {
+      const double fl = 2.0 * (double)nc * (double)Hx * (double)V;
+      T* dst = static_cast<T*>(out) + r0 * Hx;
+      if (splits <= 1)
+        return gemm2<T>(MNMAJ, MNMAJ, Lcol, ldL, Wx, Hx, nullptr, 0, V, V, 0, dst, nullptr, Hx, nc, Hx, V,
+                        GEMM_STORE, 1, 0, s, ORDA_K_GEMM_H, fl);
+      ORDA_TRY(gemm2<T>(MNMAJ, MNMAJ, Lcol, ldL, Wx, Hx, nullptr, 0, V, V, 0, nullptr, split, Hx, nc, Hx, V,
+                        GEMM_SPLIT, splits, kps, s, ORDA_K_GEMM_H, fl));
+      Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+      ORDA_CHECK_LAUNCH(launch_splitk_reduce<T>(split, splits, nc * Hx, dst, Hx, nc, Hx, s));
+      return ORDA_OK;
+    };
+    if (pl.need_gs) ORDA_TRY(grad_hidden(L, W, H, t->grad_student_hidden, pl.splits_s, pl.kps_s));
+    if (pl.w_dln_t)
+      ORDA_TRY(grad_hidden(L + nP * eb, tied ? W : Wt, Ht, t->grad_teacher_hidden, pl.splits_t, pl.kps_t));
+  }
+
+  FinalizeParams Z{};
+  Z.rowv = rowv; Z.labels = t->labels; Z.N = N; Z.ignore_index = p->ignore_index;
+  Z.reduction_sum = reduction_sum; Z.teacher_ce = pl.teacher_ce; Z.div_on = pl.div_on;
+  Z.w_s = p->student_ce_weight; Z.w_t = p->teacher_ce_weight; Z.w_kl = p->kl_weight;
+  Z.out_loss = t->out_loss; Z.out_ce_s = t->out_student_ce; Z.out_ce_t = t->out_teacher_ce; Z.out_kl = t->out_kl;
+  Z.scal = scal;
+  { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_finalize(Z, s)); }
+
+  // requested gradients that no loss term reaches are zero
+  if (pl.need_gt && !pl.w_dln_t)
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, Ht, N, 0, Ht, eb, s)); }
+  if (sep && pl.need_gwt && !pl.w_dlt_t)
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_weight, Ht, V, 0, Ht, eb, s)); }
+  return ORDA_OK;
+}
+
+// Backward of the ORDA_GRADS_IN_FORWARD mode: gradients *= grad_output.
+template <class T>
+int run_scale(const Plan& pl, const orda_tensors_t* t, hipStream_t s) {
+  auto sc = [&](void* g, int64_t n) -> int {
+    if (!g) return ORDA_OK;
+    Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+    ORDA_CHECK_LAUNCH(launch_scale<T>(g, n, t->grad_output, s));
+    return ORDA_OK;
+  };
+  if (pl.need_gs) ORDA_TRY(sc(t->grad_student_hidden, pl.N * pl.H));
+  if (pl.need_gw) ORDA_TRY(sc(t->grad_weight, pl.V * pl.H));
+  if (pl.need_gt) ORDA_TRY(sc(t->grad_teacher_hidden, pl.N * pl.Ht));
+  if (pl.need_gwt) ORDA_TRY(sc(t->grad_teacher_weight, pl.V * pl.Ht));
+  return ORDA_OK;
+}
+
+int check_grads(const Plan& pl, const orda_tensors_t* t) {
+  if (pl.need_gs && !t->grad_student_hidden) return fail(ORDA_EINVAL, "grad_student_hidden is required");
+  if (pl.need_gw && !t->grad_weight) return fail(ORDA_EINVAL, "grad_weight is required");
+  if (pl.need_gt && !t->grad_teacher_hidden) return fail(ORDA_EINVAL, "grad_teacher_hidden is required");
+  if (pl.need_gwt && !t->grad_teacher_weight) return fail(ORDA_EINVAL, "grad_teacher_weight is required");
+  for (const void* g : {t->grad_student_hidden, t->grad_weight, t->grad_teacher_hidden, t->grad_teacher_weight})
+    if (g && !aligned16(g)) return fail(ORDA_EINVAL, "gradient buffers must be 16-byte aligned");
+  return ORDA_OK;
+}
+
 int check_operands(const Plan& pl, const orda_tensors_t* t) {
   if (!t) return fail(ORDA_EINVAL, "tensors is NULL");
   if (!t->student_hidden || !t->weight || !t->labels) return fail(ORDA_EINVAL, "student_hidden, weight and labels are required");
@@ -518,6 +761,14 @@ int orda_forward(const orda_problem_t* p, const orda_tensors_t* t, void* workspa
     return fail(ORDA_EWORKSPACE, "forward workspace too small: need %zu bytes, got %zu", pl.fwd_bytes, workspace_bytes);
   char* ws = aligned_base(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.fused) {
+    ORDA_TRY(check_grads(pl, t));
+    switch (pl.dtype) {
+      case ORDA_BF16: return run_fused<bf16>(pl, p, t, ws, s);
+      case ORDA_F16: return run_fused<f16>(pl, p, t, ws, s);
+      default: return run_fused<float>(pl, p, t, ws, s);
+    }
+  }
   switch (pl.dtype) {
     case ORDA_BF16: return run_forward<bf16>(pl, p, t, ws, s);
     case ORDA_F16: return run_forward<f16>(pl, p, t, ws, s);
@@ -532,10 +783,15 @@ int orda_backward(const orda_problem_t* p, const orda_tensors_t* t, void* worksp
   ORDA_TRY(make_plan(p, pl));
   ORDA_TRY(check_operands(pl, t));
   if (!t->grad_output) return fail(ORDA_EINVAL, "grad_output is required");
-  if (pl.need_gs && !t->grad_student_hidden) return fail(ORDA_EINVAL, "grad_student_hidden is required");
-  if (pl.need_gw && !t->grad_weight) return fail(ORDA_EINVAL, "grad_weight is required");
-  if (pl.need_gt && !t->grad_teacher_hidden) return fail(ORDA_EINVAL, "grad_teacher_hidden is required");
-  if (pl.need_gwt && !t->grad_teacher_weight) return fail(ORDA_EINVAL, "grad_teacher_weight is required");
+  ORDA_TRY(check_grads(pl, t));
+  if (pl.fused) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (pl.dtype) {
+      case ORDA_BF16: return run_scale<bf16>(pl, t, s);
+      case ORDA_F16: return run_scale<f16>(pl, t, s);
+      default: return run_scale<float>(pl, t, s);
+    }
+  }
   if (pl.bwd_bytes > 0 && (!workspace || workspace_bytes < pl.bwd_bytes))
     return fail(ORDA_EWORKSPACE, "backward workspace too small: need %zu bytes, got %zu", pl.bwd_bytes, workspace_bytes);
   char* ws = aligned_base(workspace);
@@ -561,6 +817,57 @@ int orda_gemm_abt(int32_t dtype, int64_t M, int64_t N, int64_t K, const void* A,
     case ORDA_BF16: return gemm<bf16>(A, K, B, K, C, nullptr, N, M, N, K, GEMM_STORE, s);
     case ORDA_F16: return gemm<f16>(A, K, B, K, C, nullptr, N, M, N, K, GEMM_STORE, s);
     default: return gemm<float>(A, K, B, K, C, nullptr, N, M, N, K, GEMM_STORE, s);
+  }
+}
+
+int orda_gemm(int32_t dtype, int32_t a_mn, int32_t b_mn, int64_t M, int64_t N, int64_t K, const void* A,
+              int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, int32_t splits, void* workspace,
+              size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  if (M <= 0 || N <= 0 || K <= 0) return fail(ORDA_EINVAL, "M, N, K must be > 0");
+  if (!A || !B || !C) return fail(ORDA_EINVAL, "A, B and C are required");
+  if (dtype < ORDA_BF16 || dtype > ORDA_F32) return fail(ORDA_EINVAL, "unknown dtype %d", dtype);
+  if ((a_mn != 0 && a_mn != 1) || (b_mn != 0 && b_mn != 1)) return fail(ORDA_EINVAL, "a_mn and b_mn must be 0 or 1");
+  if (splits < 1 || splits > 64) return fail(ORDA_EINVAL, "splits must be in [1, 64]");
+  const int kel = dtype == ORDA_F32 ? 4 : 8;
+  const int64_t eb = dtype == ORDA_F32 ? 4 : 2;
+  // K-major operands load K in 16-byte chunks; MN-major ones load rows in
+  // 16-byte chunks: the contiguous extent and the leading dimension must be
+  // multiples of a chunk, and the bases 16-byte aligned.
+  if (!a_mn && (K % kel || lda % kel || lda < K)) return fail(ORDA_EINVAL, "K-major A needs K and lda multiples of %d, lda >= K", kel);
+  if (a_mn && (M % kel || lda % kel || lda < M)) return fail(ORDA_EINVAL, "MN-major A needs M and lda multiples of %d, lda >= M", kel);
+  if (!b_mn && (K % kel || ldb % kel || ldb < K)) return fail(ORDA_EINVAL, "K-major B needs K and ldb multiples of %d, ldb >= K", kel);
+  if (b_mn && (N % kel || ldb % kel || ldb < N)) return fail(ORDA_EINVAL, "MN-major B needs N and ldb multiples of %d, ldb >= N", kel);
+  if (ldc < N || ldc % 4) return fail(ORDA_EINVAL, "ldc must be >= N and a multiple of 4");
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return fail(ORDA_EINVAL, "A, B and C must be 16-byte aligned");
+  int64_t kps = round_up(cdiv(K, splits), 64);
+  const int sp = (int)cdiv(K, kps);
+  float* part = nullptr;
+  if (sp > 1) {
+    if (N % 4) return fail(ORDA_EINVAL, "split-K needs N a multiple of 4");
+    const size_t need = (size_t)sp * M * N * 4 + kAlign;
+    if (!workspace || workspace_bytes < need)
+      return fail(ORDA_EWORKSPACE, "gemm workspace too small: need %zu bytes, got %zu", need, workspace_bytes);
+    part = reinterpret_cast<float*>(aligned_base(workspace));
+  }
+  (void)eb;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int la = a_mn ? MNMAJ : KMAJ, lb = b_mn ? MNMAJ : KMAJ;
+  auto go = [&](auto tag) -> int {
+    using T = decltype(tag);
+    if (sp == 1)
+      return gemm2<T>(la, lb, A, lda, B, ldb, nullptr, 0, K, K, 0, C, nullptr, ldc, M, N, K, GEMM_STORE, 1, 0, s,
+                      ORDA_K_AUX, 0.0);
+    if (la != MNMAJ || lb != MNMAJ) return fail(ORDA_EUNSUPPORTED, "split-K is built for MN-major A and B");
+    ORDA_TRY(gemm2<T>(la, lb, A, lda, B, ldb, nullptr, 0, K, K, 0, nullptr, part, N, M, N, K, GEMM_SPLIT, sp, kps,
+                      s, ORDA_K_AUX, 0.0));
+    ORDA_CHECK_LAUNCH(launch_splitk_reduce<T>(part, sp, M * N, C, ldc, M, N, s));
+    return ORDA_OK;
+  };
+  switch (dtype) {
+    case ORDA_BF16: return go(bf16{});
+    case ORDA_F16: return go(f16{});
+    default: return go(float{});
   }
 }
 

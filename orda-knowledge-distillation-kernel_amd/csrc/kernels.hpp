@@ -309,9 +309,46 @@ __device__ __forceinline__ void scan_variant(RowState& S, const f32x16 (&acc)[4]
   }
 }
 
+// Logits of the tile to the vocabulary-major buffer Lout[v][t] (student
+// columns from 0, teacher columns from tcolL), in T: the 4 consecutive
+// vocabulary rows of a lane are transposed inside the lane quad so each lane
+// stores 4 consecutive tokens of one row with one 8-byte (16-bit types) or
+// 16-byte (fp32) store.  Every lane of the wave must call this (DPP).
+template <class T>
+__device__ __forceinline__ void store_logits(const f32x16 (&acc)[4][2], const FusedParams& P, int64_t v0,
+                                             int64_t t0) {
+  const int lane = threadIdx.x & 63;
+  const int wm = wave_m(), wn = wave_n();
+  const int q = lane & 3;
+  const int64_t tb = t0 + wn * 32 + (lane & 31) - q;  // first token of the quad
+  const int64_t nt = P.N - tb;
+  const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
+  T* L = static_cast<T*>(P.Lout);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t v = v0 + wm * 128 + acc_row(mb, g * 4, lane) + q;
+      const bool ok = v < P.V && ntok > 0;
+      T* dst = L + v * P.ldL + tb;
+      float x[4], o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = acc[mb][0][g * 4 + e];
+      quad_transpose(x, o);
+      if (ok) store4(dst, o, ntok == 4, ntok);
+      if (P.store_t) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = acc[mb][1][g * 4 + e];
+        quad_transpose(x, o);
+        if (ok) store4(dst + P.tcolL, o, ntok == 4, ntok);
+      }
+    }
+}
+
 // One workgroup: 128 tokens x a contiguous range of 256-row vocabulary
-// tiles; writes one partial RowState per (range, token).
-template <class T, int SV>
+// tiles; writes one partial RowState per (range, token).  With STORE it also
+// writes the tile's logits (store_logits) for the materialised path.
+template <class T, int SV, bool STORE = false>
 __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   f32x16 acc[4][2];
@@ -340,6 +377,7 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
     int64_t t0v = t0;
     asm volatile("" : "+s"(t0v));
     fused_logits<T>(acc, lds, P, v0, t0v);
+    if constexpr (STORE) store_logits<T>(acc, P, v0, t0v);
     const int vlane0 = wm * 128 + (lane >> 5) * 4;
     const int64_t vlimit = P.V - v0;
     scan_variant<SV>(st, acc, vlane0, vlimit, vlimit >= 256, lse_sT, lse_tT, P);
@@ -376,26 +414,6 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
 }
 
 // ----------------------------------------------------------- dlogits kernel
-// Store 4 consecutive elements (one 8-byte or 16-byte store when full; p is
-// then aligned by construction), else the first n.
-template <class T>
-__device__ __forceinline__ void store4(T* p, const float (&x)[4], bool full, int n) {
-  if (full) {
-    if constexpr (sizeof(T) == 2) {
-      union { T e[4]; uint2 u; } v;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v.e[i] = from_f32<T>(x[i]);
-      *reinterpret_cast<uint2*>(p) = v.u;
-    } else {
-      *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i < n) p[i] = from_f32<T>(x[i]);
-  }
-}
-
 template <class T, int DIV, bool T1>
 __device__ __forceinline__ void dl_tile(const f32x16 (&acc)[4][2], const FusedParams& P, int64_t v0,
                                         int64_t t0) {
@@ -552,6 +570,246 @@ __global__ __launch_bounds__(kThreads) void k_gemm(GemmParams P) {
     case GEMM_ACC_FIRST: gemm_epilogue<T, GEMM_ACC_FIRST>(acc, P, m0, n0); break;
     case GEMM_ACC: gemm_epilogue<T, GEMM_ACC>(acc, P, m0, n0); break;
     default: gemm_epilogue<T, GEMM_ACC_LAST>(acc, P, m0, n0); break;
+  }
+}
+
+// ------------------------------------------------------------ general GEMM
+// Load 4 consecutive elements as fp32 (one vector load when full).
+template <class T>
+__device__ __forceinline__ void load4(const T* p, float (&x)[4], bool full, int n) {
+  if (full) {
+    if constexpr (sizeof(T) == 2) {
+      union { T e[4]; uint2 u; } v;
+      v.u = *reinterpret_cast<const uint2*>(p);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = to_f32(v.e[i]);
+    } else {
+      const float4 f = *reinterpret_cast<const float4*>(p);
+      x[0] = f.x; x[1] = f.y; x[2] = f.z; x[3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (i < n) ? to_f32(p[i]) : 0.f;
+  }
+}
+
+// Epilogue with 4-wide accesses: a lane's 4 consecutive rows of one column
+// are transposed inside the lane quad into 4 consecutive columns of one row
+// (C row-major, ldc a multiple of 4, tile base 8-byte aligned for 16-bit C
+// and 16-byte aligned for fp32).  Every lane must call this (DPP).
+template <class T, int MODE>
+__device__ __forceinline__ void gemm_epilogue_q(const f32x16 (&acc)[4][2], const GemmParams& P, float* C32,
+                                                int64_t m0, int64_t n0) {
+  const int lane = threadIdx.x & 63;
+  const int wm = wave_m(), wn = wave_n();
+  const int q = lane & 3;
+  T* C = static_cast<T*>(P.C) + m0 * P.ldc + n0;
+  float* D = C32 + m0 * P.ldc + n0;
+  const int ldc = (int)P.ldc;
+  const int mlim = (int)min<int64_t>(P.M - m0, 256), nlim = (int)min<int64_t>(P.N - n0, 256);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float x[4], o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = acc[mb][nb][g * 4 + e];
+        quad_transpose(x, o);
+        const int m = wm * 128 + acc_row(mb, g * 4, lane) + q;
+        const int nbase = acc_col0(nb, wn) + (lane & 31) - q;
+        const int rem = nlim - nbase;
+        const int cnt = rem <= 0 ? 0 : (rem >= 4 ? 4 : rem);
+        if (m < mlim && cnt > 0) {
+          const int off = m * ldc + nbase;
+          const bool full = cnt == 4;
+          if constexpr (MODE == GEMM_STORE) {
+            store4(C + off, o, full, cnt);
+          } else if constexpr (MODE == GEMM_ACC_T) {
+            float c[4];
+            load4(C + off, c, full, cnt);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) c[e] += o[e];
+            store4(C + off, c, full, cnt);
+          } else if constexpr (MODE == GEMM_ACC_FIRST || MODE == GEMM_SPLIT) {
+            store4(D + off, o, full, cnt);
+          } else {
+            float c[4];
+            load4(D + off, c, full, cnt);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) c[e] += o[e];
+            if constexpr (MODE == GEMM_ACC) store4(D + off, c, full, cnt);
+            else store4(C + off, c, full, cnt);
+          }
+        }
+      }
+}
+
+template <class T, int L>
+__device__ __forceinline__ auto gemm_operand(const T* p, int64_t ld, int64_t row0, int64_t rows, int64_t kb,
+                                             int64_t klen) {
+  if constexpr (L == KMAJ) return KOperand<T>{p + row0 * ld + kb, ld, rows};
+  else return MnOperand<T>{p + kb * ld + row0, nullptr, ld, 0, klen, klen, 0, rows};
+}
+
+// General GEMM: C[M x N] (mode) A * B^T with A and B each K-major or
+// MN-major (Layout), split-K over gridDim = tiles x splits (split s covers
+// K rows [s * k_per_split, ...) and writes its own fp32 partial in GEMM_SPLIT
+// mode), and, for an MN-major B, two row segments (B rows [0, b_kseg) from B,
+// the rest from B1): the student and teacher hidden states of one token
+// chunk feeding one grad-W GEMM.
+template <class T, int LA, int LB, int MODE>
+__global__ __launch_bounds__(kThreads) void k_gemm2(GemmParams P) {
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  f32x16 acc[4][2];
+  const int tiles = P.tiles_m * P.tiles_n;
+  const int tall = xcd_order(blockIdx.x, gridDim.x);
+  const int split = tall / tiles;
+  const int t = tall - split * tiles;
+  constexpr int G = 8;
+  const int band = t / (G * P.tiles_n);
+  const int first_m = band * G;
+  const int gm = min(P.tiles_m - first_m, G);
+  const int rem = t % (G * P.tiles_n);
+  const int tm = first_m + rem % gm;
+  const int tn = rem / gm;
+  const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
+  const int64_t kb = (int64_t)split * P.k_per_split;
+  const int64_t klen = min<int64_t>(P.K - kb, P.k_per_split);
+  const T* A = static_cast<const T*>(P.A);
+  const T* B = static_cast<const T*>(P.B);
+  zero_acc(acc);
+  const auto a = gemm_operand<T, LA>(A, P.lda, m0, P.M - m0, kb, klen);
+  if constexpr (LB == KMAJ) {
+    const KOperand<T> b{B + n0 * P.ldb + kb, P.ldb, P.N - n0};
+    mainloop_g<T, LA, LB>(acc, lds, a, b, klen);
+  } else {
+    const T* B1 = static_cast<const T*>(P.B1);
+    MnOperand<T> b;
+    b.p0 = B + kb * P.ldb + n0;
+    b.ld0 = P.ldb;
+    b.kseg = P.b_kseg - kb;
+    b.kval0 = min<int64_t>(P.b_kval0 - kb, klen);
+    b.p1 = B1 ? B1 + n0 : nullptr;
+    b.ld1 = P.ldb1;
+    b.kval1 = P.b_kval1;
+    b.cols = P.N - n0;
+    mainloop_g<T, LA, LB>(acc, lds, a, b, klen);
+  }
+  gemm_epilogue_q<T, MODE>(acc, P, P.C32 + (int64_t)split * P.split_stride, m0, n0);
+}
+
+// out[m][n] = sum over s of part[s][m][n] (fixed order), converted to T.
+// Thread: 4 consecutive columns.  part has leading dimension N (dense),
+// N a multiple of 4.
+template <class T>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, int splits, int64_t stride,
+                                                       T* __restrict__ out, int64_t ldo, int64_t M, int64_t N) {
+  const int64_t nq = N / 4;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * nq) return;
+  const int64_t m = i / nq, c = (i - m * nq) * 4;
+  float x[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) {
+    const float4 v = *reinterpret_cast<const float4*>(part + s * stride + m * N + c);
+    x[0] += v.x; x[1] += v.y; x[2] += v.z; x[3] += v.w;
+  }
+  store4(out + m * ldo + c, x, true, 4);
+}
+
+// x *= g[0] in place (n elements, n a multiple of 4, x 8-byte aligned);
+// nothing to do when g[0] == 1.
+template <class T>
+__global__ __launch_bounds__(256) void k_scale(T* __restrict__ x, int64_t n, const float* __restrict__ g) {
+  const float s = g[0];
+  if (s == 1.0f) return;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
+    float v[4];
+    load4(x + i, v, true, 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] *= s;
+    store4(x + i, v, true, 4);
+  }
+}
+
+// ------------------------------------------------- materialised dlogits
+// In place on the logits L[v][t] of one token chunk (vocabulary-major,
+// student columns [0, N), teacher columns [tcol, tcol + N)): student
+// dlogits w_s (p_s - 1_y) + w_kl T dD/dz_s and teacher dlogits
+// w_t (p_t - 1_y), times mean_scale (the caller's grad_output is applied
+// later).  Ignored rows give 0.  Thread: 4 consecutive tokens x
+// rows_per_block vocabulary rows; block: 256 threads = 1024 tokens.
+template <class T, int DIV, bool T1>
+__global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
+  const int64_t t0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (t0 >= P.N) return;
+  const int nt = (int)min<int64_t>(P.N - t0, 4);
+  const int64_t v0 = (int64_t)blockIdx.y * P.rows_per_block;
+  const int64_t v1 = min<int64_t>(P.V, v0 + P.rows_per_block);
+  const float scale = P.mean_scale[0];
+  const float invT = P.invT;
+  int64_t yeff[4];
+  float lse_s[4], lse_sT[4], lse_t[4], lse_tT[4], c[4][4], sc_s[4], sc_t[4], sc_d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool ok = i < nt;
+    const int64_t t = t0 + (ok ? i : 0);
+    const int64_t y = P.labels[t];
+    const bool ign = !ok || y == P.ignore_index;
+    yeff[i] = (y >= 0 && y < P.V) ? y : 0;
+    lse_s[i] = P.rowp[0 * P.N + t];
+    lse_sT[i] = P.rowp[1 * P.N + t];
+    lse_t[i] = P.rowp[2 * P.N + t];
+    lse_tT[i] = P.rowp[3 * P.N + t];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) c[i][k] = P.rowp[(4 + k) * P.N + t];
+    sc_s[i] = ign ? 0.f : scale * P.w_s;
+    sc_t[i] = ign ? 0.f : scale * P.w_t;
+    sc_d[i] = ign ? 0.f : scale * P.w_kl * P.temperature;
+  }
+  T* Ls = static_cast<T*>(P.L) + t0;
+  T* Lt = Ls + P.tcol;
+  const bool full = nt == 4;
+  const bool need_t = DIV >= 0 || P.tgrad;
+  // R rows in flight per iteration: their loads are issued together
+  constexpr int R = 4;
+  for (int64_t vb = v0; vb < v1; vb += R) {
+    float xs[R][4], xt[R][4];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t v = vb + r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[r][i] = xt[r][i] = 0.f;
+      if (v < v1) {
+        load4(Ls + v * P.ldL, xs[r], full, nt);
+        if (need_t) load4(Lt + v * P.ldL, xt[r], full, nt);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t v = vb + r;
+      float ds[4], dt[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float onehot = (v == yeff[i]) ? 1.f : 0.f;
+        const float ps1 = fexp(xs[r][i] - lse_s[i]);
+        float d = sc_s[i] * (ps1 - onehot);
+        if constexpr (DIV >= 0) {
+          const float lps = xs[r][i] * invT - lse_sT[i];
+          const float lpt = xt[r][i] * invT - lse_tT[i];
+          const float psT = T1 ? ps1 : fexp(lps);
+          const float ptT = fexp(lpt);
+          d += sc_d[i] * div_grad<DIV>(lps, lpt, psT, ptT, c[i], P.alpha, P.beta);
+        }
+        ds[i] = d;
+        dt[i] = sc_t[i] * (fexp(xt[r][i] - lse_t[i]) - onehot);
+      }
+      if (v < v1) {
+        store4(Ls + v * P.ldL, ds, full, nt);
+        if (P.tgrad) store4(Lt + v * P.ldL, dt, full, nt);
+      }
+    }
   }
 }
 
@@ -712,6 +970,89 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
   hipLaunchKernelGGL(k_label<T>, dim3(grid), dim3(256), 0, s, P);
   return hipGetLastError();
 }
+
+// Materialised path: scan variants with the logits store (phase 0 only).
+#define ORDA_SCANST_CASE(T, SV) \
+  case SV: hipLaunchKernelGGL((k_scan<T, SV, true>), dim3(grid), dim3(kThreads), 0, s, P); break;
+#define ORDA_INSTANTIATE_SCAN_STORE(T)                                                     \
+  template <> hipError_t launch_scan_store<T>(const FusedParams& P, int grid, hipStream_t s) { \
+    if (P.phase != 0) return hipErrorInvalidValue;                                         \
+    switch (scan_variant_of(P)) {                                                          \
+      ORDA_SCANST_CASE(T, SV_STUDENT)                                                      \
+      ORDA_SCANST_CASE(T, SV_TCE_T1)                                                       \
+      ORDA_SCANST_CASE(T, SV_TCE)                                                          \
+      ORDA_SCANST_CASE(T, SV_LIN_T1)                                                       \
+      ORDA_SCANST_CASE(T, SV_LIN)                                                          \
+      ORDA_SCANST_CASE(T, SV_POW)                                                          \
+      default: return hipErrorInvalidValue;                                                \
+    }                                                                                      \
+    return hipGetLastError();                                                              \
+  }
+
+// General GEMM: the (layout, layout, mode) combinations the library uses.
+template <class T, int LA, int LB, int MODE>
+inline void gemm2_go(const GemmParams& P, hipStream_t s) {
+  const int grid = P.tiles_m * P.tiles_n * P.splits;
+  hipLaunchKernelGGL((k_gemm2<T, LA, LB, MODE>), dim3(grid), dim3(kThreads), 0, s, P);
+}
+#define ORDA_INSTANTIATE_GEMM2(T)                                                          \
+  template <> hipError_t launch_gemm2<T>(const GemmParams& P, hipStream_t s) {             \
+    const int key = P.la * 100 + P.lb * 10 + P.mode;                                       \
+    switch (key) {                                                                         \
+      case KMAJ * 100 + MNMAJ * 10 + GEMM_STORE: gemm2_go<T, KMAJ, MNMAJ, GEMM_STORE>(P, s); break; \
+      case KMAJ * 100 + MNMAJ * 10 + GEMM_ACC_T: gemm2_go<T, KMAJ, MNMAJ, GEMM_ACC_T>(P, s); break; \
+      case MNMAJ * 100 + MNMAJ * 10 + GEMM_STORE: gemm2_go<T, MNMAJ, MNMAJ, GEMM_STORE>(P, s); break; \
+      case MNMAJ * 100 + MNMAJ * 10 + GEMM_SPLIT: gemm2_go<T, MNMAJ, MNMAJ, GEMM_SPLIT>(P, s); break; \
+      case KMAJ * 100 + KMAJ * 10 + GEMM_STORE: gemm2_go<T, KMAJ, KMAJ, GEMM_STORE>(P, s); break; \
+      case MNMAJ * 100 + KMAJ * 10 + GEMM_STORE: gemm2_go<T, MNMAJ, KMAJ, GEMM_STORE>(P, s); break; \
+      default: return hipErrorInvalidValue;                                                \
+    }                                                                                      \
+    return hipGetLastError();                                                              \
+  }
+
+// In-place dlogits variants (the divergences of families LIN and POW).
+template <class T, int DIV, bool T1>
+inline void dlm_go(const DlmParams& P, hipStream_t s) {
+  const dim3 grid((unsigned)((P.N + 1023) / 1024), (unsigned)((P.V + P.rows_per_block - 1) / P.rows_per_block));
+  hipLaunchKernelGGL((k_dlm<T, DIV, T1>), grid, dim3(256), 0, s, P);
+}
+#define ORDA_DLM_CASE(T, D) \
+  case D: dlm_go<T, D, false>(P, s); break;
+#define ORDA_INSTANTIATE_FB(T)                                                             \
+  template <> hipError_t launch_dlm<T>(const DlmParams& P, hipStream_t s) {                \
+    const bool t1 = P.t_is_one != 0;                                                       \
+    switch (P.div) {                                                                       \
+      case -1: dlm_go<T, -1, true>(P, s); break;                                           \
+      case DIV_FKL: if (t1) dlm_go<T, DIV_FKL, true>(P, s); else dlm_go<T, DIV_FKL, false>(P, s); break; \
+      case DIV_SOFT: if (t1) dlm_go<T, DIV_SOFT, true>(P, s); else dlm_go<T, DIV_SOFT, false>(P, s); break; \
+      ORDA_DLM_CASE(T, DIV_RKL)                                                            \
+      ORDA_DLM_CASE(T, DIV_SYM)                                                            \
+      ORDA_DLM_CASE(T, DIV_HELL)                                                           \
+      ORDA_DLM_CASE(T, DIV_BHAT)                                                           \
+      ORDA_DLM_CASE(T, DIV_RENYI)                                                          \
+      ORDA_DLM_CASE(T, DIV_AMARI)                                                          \
+      ORDA_DLM_CASE(T, DIV_CHI2)                                                           \
+      ORDA_DLM_CASE(T, DIV_L2)                                                             \
+      ORDA_DLM_CASE(T, DIV_AB)                                                             \
+      default: return hipErrorInvalidValue;                                                \
+    }                                                                                      \
+    return hipGetLastError();                                                              \
+  }                                                                                        \
+  template <>                                                                              \
+  hipError_t launch_splitk_reduce<T>(const float* part, int splits, int64_t stride, void* out, int64_t ldo, \
+                                     int64_t M, int64_t N, hipStream_t s) {                \
+    const int64_t n = M * (N / 4);                                                        \
+    hipLaunchKernelGGL(k_splitk_reduce<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part, splits, \
+                       stride, static_cast<T*>(out), ldo, M, N);                           \
+    return hipGetLastError();                                                              \
+  }                                                                                        \
+  template <> hipError_t launch_scale<T>(void* x, int64_t n, const float* g, hipStream_t s) { \
+    int64_t blocks = (n / 4 + 255) / 256;                                                  \
+    if (blocks > 8192) blocks = 8192;                                                      \
+    if (blocks < 1) blocks = 1;                                                            \
+    hipLaunchKernelGGL(k_scale<T>, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<T*>(x), n, g); \
+    return hipGetLastError();                                                              \
+  }
 
 #define ORDA_INSTANTIATE_GEMM(T)                                                                     \
   template hipError_t launch_gemm<T>(const GemmParams&, hipStream_t);                                \

@@ -17,7 +17,11 @@ enum TeacherSource {
   TSRC_MEM = 3      // precomputed logits [N x V]
 };
 
-enum GemmMode { GEMM_STORE = 0, GEMM_ACC_FIRST = 1, GEMM_ACC = 2, GEMM_ACC_LAST = 3 };
+// GEMM epilogues: STORE writes C in T; ACC_FIRST / ACC / ACC_LAST build an
+// fp32 sum in C32 over calls (the last one writes C); ACC_T adds into C in
+// T (C = T(C + A B^T)); SPLIT writes split s's fp32 partial to
+// C32 + s * split_stride.
+enum GemmMode { GEMM_STORE = 0, GEMM_ACC_FIRST = 1, GEMM_ACC = 2, GEMM_ACC_LAST = 3, GEMM_ACC_T = 4, GEMM_SPLIT = 5 };
 
 struct FusedParams {
   const void* W;
@@ -51,6 +55,11 @@ struct FusedParams {
   void* dLNt;
   int64_t ldN;
   int w_dlt_s, w_dlt_t, w_dln_s, w_dln_t;
+  // logits written by the scan of the materialised path: Lout[v][t],
+  // teacher columns from tcolL (stored when store_t)
+  void* Lout;
+  int64_t ldL, tcolL;
+  int store_t;
 };
 
 struct GemmParams {
@@ -60,6 +69,24 @@ struct GemmParams {
   float* C32;
   int64_t M, N, K, lda, ldb, ldc;
   int tiles_m, tiles_n, mode;
+  // general GEMM (k_gemm2)
+  int la, lb;                                // Layout of A and B
+  const void* B1;                            // MN-major B: rows [b_kseg, K) come from B1
+  int64_t ldb1, b_kseg, b_kval0, b_kval1;    // valid rows of each segment
+  int splits;
+  int64_t k_per_split, split_stride;         // split-K (GEMM_SPLIT partials)
+};
+
+// In-place dlogits on materialised logits (k_dlm).
+struct DlmParams {
+  void* L;  // [V][ldL]; student columns [0, N), teacher columns [tcol, tcol + N)
+  int64_t ldL, tcol;
+  const int64_t* labels;
+  const float* rowp;        // [kNRowP][N]
+  const float* mean_scale;  // device scalar
+  int64_t N, V, ignore_index;
+  int div, t_is_one, tgrad, rows_per_block;
+  float invT, temperature, alpha, beta, w_s, w_t, w_kl;
 };
 
 struct LabelParams {
@@ -78,6 +105,13 @@ template <class T> hipError_t launch_scan(const FusedParams& P, int grid, hipStr
 template <class T> hipError_t launch_dl(const FusedParams& P, int grid, hipStream_t s);
 template <class T> hipError_t launch_gemm(const GemmParams& P, hipStream_t s);
 template <class T> hipError_t launch_label(const LabelParams& P, hipStream_t s);
+template <class T> hipError_t launch_scan_store(const FusedParams& P, int grid, hipStream_t s);
+template <class T> hipError_t launch_gemm2(const GemmParams& P, hipStream_t s);
+template <class T> hipError_t launch_dlm(const DlmParams& P, hipStream_t s);
+template <class T>
+hipError_t launch_splitk_reduce(const float* part, int splits, int64_t stride, void* out, int64_t ldo, int64_t M,
+                                int64_t N, hipStream_t s);
+template <class T> hipError_t launch_scale(void* x, int64_t n, const float* g, hipStream_t s);
 template <class T>
 hipError_t launch_transpose(const void* in, int64_t ldi, void* out, int64_t ldo, int64_t R, int64_t C,
                             hipStream_t s);
@@ -94,7 +128,8 @@ struct MergeParams {
   float pa[3], pb[3];
   int npow;
   float* rowp;  // [kNRowP][N]
-  float* rowv;  // [3][N]: student CE, teacher CE, T^2 * divergence
+  float* rowv;  // [3][ldv]: student CE, teacher CE, T^2 * divergence
+  int64_t ldv;
 };
 hipError_t launch_merge(const MergeParams& P, hipStream_t s);
 
@@ -111,6 +146,12 @@ struct FinalizeParams {
   float* scal;  // [0] = mean_scale, [1] = count of non-ignored rows
 };
 hipError_t launch_finalize(const FinalizeParams& P, hipStream_t s);
+
+// scal[0] = mean scale (1 / max(count, 1), or 1 for sum), scal[1] = count of
+// non-ignored labels: the same values k_finalize writes, available before
+// the loss rows exist.
+hipError_t launch_count(const int64_t* labels, int64_t N, int64_t ignore_index, int reduction_sum, float* scal,
+                        hipStream_t s);
 
 // out[r * ld + c] = 0 for r < R, c0 <= c < c1 (element size esize bytes)
 hipError_t launch_zero2d(void* out, int64_t ld, int64_t R, int64_t c0, int64_t c1, int esize, hipStream_t s);

@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace orda {
 
 typedef __bf16 bf16;
@@ -31,10 +33,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 512;            // 8 waves of 64, 2 per SIMD
-constexpr int kRowBytes = 128;           // bytes of K staged per row per step
-constexpr int kLdsRow = kRowBytes + 16;  // padded LDS row: conflict-free b128 reads
-constexpr int kLdsTile = 256 * kLdsRow;  // one operand tile
-constexpr int kLdsBytes = 4 * kLdsTile;  // double-buffered A and B: 144 KiB
 
 constexpr float kInf = __builtin_huge_valf();
 constexpr float kLog2e = 1.4426950408889634f;
@@ -142,55 +140,51 @@ __device__ __forceinline__ void quad_transpose(const float (&x)[4], float (&out)
   }
 }
 
-// ------------------------------------------------- global -> LDS staging
-// A ROWS x 128-byte slab of a row-major [rows x K] operand.  Thread i moves
-// 16-byte chunk (i % 8) of rows i/8, i/8 + 64, ...: each row segment is one
-// fully used 128-byte line.  Rows >= rows_valid and columns >= K read as 0.
-// Contract (checked by the host): the operand base and leading dimension
-// are 16-byte aligned and K is a multiple of 16 / sizeof(T), so a chunk is
-// either wholly inside or wholly outside [0, K).
-template <class T, int ROWS>
-struct Stage {
-  static constexpr int kRowsPerPass = kThreads / 8;
-  static constexpr int kLoads = ROWS / kRowsPerPass;
-  static constexpr int kElems = 16 / sizeof(T);
-  uint4 v[kLoads];
+// ------------------------------------------- global -> LDS, direct (DMA)
+// Operand tiles reach LDS by buffer_load_dwordx4 ... lds: each lane of a wave
+// names any 16-byte source, and the 64 chunks land consecutively at the
+// wave's LDS base (lane l at +16 l, checked on gfx950 with an in-bounds
+// probe).  No VGPRs hold staged data and no ds_write is issued.  A source
+// offset past the buffer resource's range writes zeros (same probe): every
+// invalid chunk (rows past the operand, K past its end) is sent there, so
+// tiles at the edges come out zero-padded.
+//
+// LDS tiles are unpadded and XOR-swizzled on 16-byte chunks:
+//   K-major tile: 256 rows x 128 bytes of K (64 bf16/f16, 32 fp32); logical
+//     chunk c of row r sits at chunk c ^ ((r >> 1) & 7): the 16 rows read by
+//     16 consecutive lanes of a fragment read hit 16 distinct 16-byte bank
+//     groups (two rows per 256-byte bank line).
+//   MN-major tile: BK rows of K x 256 elements (512 bytes bf16, 1 KiB fp32);
+//     16-bit: chunk c of K row k sits at c ^ ((k & 3) << 2), so the 4 K rows x
+//     64 bytes read by a half-wave's transposing reads cover all 64 banks;
+//     fp32: c ^ ((k & 1) << 3) for the 2 K rows of a fragment.
+// Pipeline (2 stages of A + B, 2 x 64 KiB): the wait for step kt+1 and the
+// workgroup barrier sit before the last MFMA sub-step of step kt; after the
+// barrier stage kt is free and receives step kt+2, and the first fragments
+// of step kt+1 are read during the last sub-step of step kt.
+constexpr int kTileBytes = 32768;         // one operand tile of one stage
+constexpr int kLdsTile = kTileBytes;
+constexpr int kLdsBytes = 4 * kTileBytes;  // 2 stages x (A + B): 128 KiB
 
-  __device__ __forceinline__ void load(const T* base, int64_t ld, int64_t rows_valid, int64_t k0, int64_t K) {
-    const int tid = threadIdx.x;
-    const int64_t kc = k0 + (int64_t)(tid & 7) * kElems;
-    const T* p = base + (int64_t)(tid >> 3) * ld + kc;
-#pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-      const int r = (tid >> 3) + kRowsPerPass * j;
-      v[j] = (r < rows_valid && kc < K)
-                 ? *reinterpret_cast<const uint4*>(p + (int64_t)(kRowsPerPass * j) * ld)
-                 : make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
-  __device__ __forceinline__ void store(char* lds) const {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-      const int r = (tid >> 3) + kRowsPerPass * j;
-      *reinterpret_cast<uint4*>(lds + r * kLdsRow + (tid & 7) * 16) = v[j];
-    }
-  }
-};
+constexpr uint32_t kOob = 0x80000000u;  // a source offset past every resource
 
-// MFMA operand fragment: lane l supplies row (row0 + l%32) and the K slice
-// selected by l/32 of K step ks.
-template <class T>
-__device__ __forceinline__ typename Traits<T>::Frag frag(const char* tile, int row0, int ks) {
-  const int lane = threadIdx.x & 63;
-  if constexpr (sizeof(T) == 2) {
-    const char* p = tile + (row0 + (lane & 31)) * kLdsRow + ks * 32 + (lane >> 5) * 16;
-    return *reinterpret_cast<const typename Traits<T>::Frag*>(p);
-  } else {
-    const char* p = tile + (row0 + (lane & 31)) * kLdsRow + ks * 8 + (lane >> 5) * 4;
-    return *reinterpret_cast<const float*>(p);
-  }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t off, char* lds_wave) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16, off, 0, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Workgroup barrier without the memory fences of __syncthreads: the caller's
+// vmcnt wait covers the DMA; LDS reads of this wave are complete first.
+__device__ __forceinline__ void tile_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+}
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 __device__ __forceinline__ void zero_acc(f32x16 (&acc)[4][2]) {
 #pragma unroll
@@ -201,79 +195,343 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[4][2]) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 }
 
-// acc[mb][nb] += A[wm*128 + mb*32 .. +32, :] * Bhalf_nb[wn*32 .. +32, :]^T over K.
-// H0/H1 select which 128-row halves of the B tile take part.  A points at the
-// tile's first row with a_rows valid rows from there (likewise B0, B1).
-// Double-buffered LDS with register prefetch of the next K step (written to
-// LDS halfway through the current one) and MFMA fragments read one K
-// sub-step ahead; one barrier per K step.
-template <class T, bool H0, bool H1>
-__device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], char* lds,
-                                         const T* A, int64_t lda, int64_t a_rows,
-                                         const T* B0, int64_t ldb0, int64_t b0_rows,
-                                         const T* B1, int64_t ldb1, int64_t b1_rows,
-                                         int64_t K) {
+__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 7; }
+
+// K-major operand: rows [0, rows) at p (leading dimension ld), K contiguous;
+// contract (host-checked): p and ld 16-byte aligned, K a multiple of 16 bytes.
+template <class T>
+struct KOperand {
+  const T* p;
+  int64_t ld, rows;
+};
+
+// MN-major operand: element (row r, k) at base[k * ld + r].  Rows of K in up
+// to two segments: [0, kseg) at p0 (the first kval0 valid), [kseg, K) at p1
+// (the first kval1 valid); columns [0, cols) valid, cols rounded up to a
+// 16-byte chunk readable.
+template <class T>
+struct MnOperand {
+  const T* p0;
+  const T* p1;
+  int64_t ld0, ld1, kseg, kval0, kval1, cols;
+};
+
+enum Layout { KMAJ = 0, MNMAJ = 1 };
+
+// Per-thread DMA plan of one K-major tile of 256 rows: 4 chunks per thread,
+// chunk i of wave w covers rows (8 i + w) * 8 .. + 8 (i < 2: rows 0..127).
+template <class T>
+struct KDma {
+  uint32_t off[4];  // byte offset of the chunk from the row-0/k0 corner
+  int kc[4];        // first K element of the chunk
+  __device__ __forceinline__ void init(int64_t ld, int64_t rows, int row_base) {
+    const int w = wave_id(), l = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pslot = (i * 8 + w) * 64 + l;
+      const int r = pslot >> 3;
+      const int c = (pslot & 7) ^ kswz(r);
+      kc[i] = c * (16 / (int)sizeof(T));
+      const int rr = r - row_base;
+      off[i] = (rr >= 0 && rr < rows) ? (uint32_t)((rr * ld) * (int64_t)sizeof(T) + c * 16) : kOob;
+    }
+  }
+  // chunks [i0, i1) of step k0 (K valid elements in all) to `tile`
+  template <int I0, int I1>
+  __device__ __forceinline__ void issue(const T* p, int64_t k0, int64_t K, char* tile) const {
+    const int w = wave_id();
+    const auto rs = rsrc_of(p + k0);
+    const int64_t krem = K - k0;
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+      const uint32_t o = (kc[i] < krem) ? off[i] : kOob;
+      dma16(rs, o, tile + (i * 8 + w) * 1024);
+    }
+  }
+};
+
+// Per-thread DMA plan of one MN-major tile (BK rows of K x 256 columns).
+template <class T>
+struct MnDma {
+  static constexpr int kChunks = 256 * (int)sizeof(T) / 16;   // per K row: 32 (16-bit), 64 (fp32)
+  static constexpr int kRowsPerInst = 64 / kChunks;           // 2, 1
+  uint32_t coff[4];  // byte offset of the chunk's columns (kOob if past cols)
+  int kr[4];         // K row of the chunk inside the step
+  __device__ __forceinline__ void init(int64_t cols) {
+    const int w = wave_id(), l = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pslot = (i * 8 + w) * 64 + l;
+      const int k = pslot / kChunks;
+      const int pc = pslot % kChunks;
+      const int c = sizeof(T) == 2 ? (pc ^ ((k & 3) << 2)) : (pc ^ ((k & 1) << 3));
+      kr[i] = k;
+      const int col = c * (16 / (int)sizeof(T));
+      coff[i] = col < cols ? (uint32_t)(col * (int)sizeof(T)) : kOob;
+    }
+  }
+  __device__ __forceinline__ void issue(const MnOperand<T>& o, int64_t k0, char* tile) const {
+    const int w = wave_id();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // the chunk's K row is the same for the whole wave: pick its segment
+      const int64_t krow = k0 + (i * 8 + w) * kRowsPerInst;
+      const bool seg0 = krow < o.kseg;
+      const T* base = seg0 ? o.p0 + krow * o.ld0 : o.p1 + (krow - o.kseg) * o.ld1;
+      const int64_t ld = seg0 ? o.ld0 : o.ld1;
+      const int64_t kval = seg0 ? o.kval0 - krow : o.kval1 - (krow - o.kseg);  // valid rows from krow
+      const int dk = kr[i] - (i * 8 + w) * kRowsPerInst;                        // 0 or 1 (16-bit)
+      const uint32_t off = (dk < kval && coff[i] != kOob) ? (uint32_t)(dk * ld * (int64_t)sizeof(T)) + coff[i] : kOob;
+      dma16(rsrc_of(base), off, tile + (i * 8 + w) * 1024);
+    }
+  }
+};
+
+// MFMA operand fragment from a K-major tile: lane l supplies row row0 + l%32
+// and the K slice of sub-step ks selected by l/32.
+template <class T>
+__device__ __forceinline__ typename Traits<T>::Frag frag(const char* tile, int row0, int ks) {
+  const int lane = threadIdx.x & 63;
+  const int r = row0 + (lane & 31);
+  if constexpr (sizeof(T) == 2) {
+    const int c = ks * 2 + (lane >> 5);
+    return *reinterpret_cast<const typename Traits<T>::Frag*>(tile + r * 128 + ((c ^ kswz(r)) << 4));
+  } else {
+    const int k = ks * 2 + (lane >> 5);
+    return *reinterpret_cast<const float*>(tile + r * 128 + (((k >> 2) ^ kswz(r)) << 4) + ((k & 3) << 2));
+  }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+// ds_read_b64_tr_b16 as inline assembly: the compiler's wait insertion treats
+// the builtin as possibly reading LDS still being written by an in-flight
+// DMA and puts s_waitcnt vmcnt(0) before it, which would serialise every K
+// step on its own prefetch.  The pipeline orders these reads with its own
+// waits: the barrier before a stage is read, and lds_wait_tie before the
+// fragments are used.
+__device__ __forceinline__ s16x4 lds_read_tr16(const char* p) {
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+  s16x4 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(a));
+  return v;
+}
+
+// Wait for every LDS read of this wave, then pass x through an empty asm
+// so any later use of x is ordered after the wait.
+template <class F>
+__device__ __forceinline__ void lds_tie(F& x) {
+  asm volatile("" : "+v"(x));
+}
+
+// MFMA fragment from an MN-major tile: the same operand as frag<T> (lane l:
+// row row0 + l%32, K slice 8*(l/32)..+8 of sub-step ks).
+// ds_read_b64_tr_b16 works on groups of 16 lanes: lane s of a group supplies
+// the address of 4 consecutive 16-bit elements, and lane i of the group
+// receives element i%4 of the rows supplied by lanes i/4, i/4+4, i/4+8,
+// i/4+12 (checked on gfx950 with an in-bounds probe).  Lane s therefore
+// points at K row k0 + s/4, columns m0 + 4*(s%4): lane i gets column m0 + i
+// at K rows k0..k0+3.  Group g covers columns 16*(g%2).. and K rows
+// 8*(g/2)..; a second read 4 rows further completes the 8-element slice.
+template <class T>
+__device__ __forceinline__ typename Traits<T>::Frag frag_mn(const char* tile, int row0, int ks) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (sizeof(T) == 2) {
+    const int g = lane >> 4, s = lane & 15;
+    const int k = ks * 16 + 8 * (g >> 1) + (s >> 2);
+    const int m = row0 + 16 * (g & 1) + 4 * (s & 3);
+    const int c = m >> 3, b = (m & 7) * 2;
+    const s16x4 lo = lds_read_tr16(tile + k * 512 + ((c ^ ((k & 3) << 2)) << 4) + b);
+    const int k4 = k + 4;
+    const s16x4 hi = lds_read_tr16(tile + k4 * 512 + ((c ^ ((k4 & 3) << 2)) << 4) + b);
+    const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(typename Traits<T>::Frag, both);
+  } else {
+    const int k = ks * 2 + (lane >> 5);
+    const int m = row0 + (lane & 31);
+    const int c = m >> 2;
+    return *reinterpret_cast<const float*>(tile + k * 1024 + ((c ^ ((k & 1) << 3)) << 4) + ((m & 3) << 2));
+  }
+}
+
+template <class T, int L>
+__device__ __forceinline__ typename Traits<T>::Frag op_frag(const char* tile, int row0, int ks) {
+  if constexpr (L == KMAJ) return frag<T>(tile, row0, ks);
+  else return frag_mn<T>(tile, row0, ks);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_dma_steps(int n) {  // n = later steps allowed in flight (0 or 1)
+  if (n <= 0) wait_vmem<0>();
+  else wait_vmem<N>();
+}
+
+// The pipeline shared by every GEMM-shaped kernel.  Loader issue(step, tile)
+// sends the A and B chunks of K step `step` to the given stage; H0 / H1
+// select which 128-row halves of the B tile take part (the fused loss
+// kernels put student tokens in half 0 and the same tokens' teacher rows in
+// half 1).  acc[mb][nb] += A[wm*128 + mb*32 ..] x B[nb*128 + wn*32 ..]^T.
+template <class T, int LA, int LB, bool H0, bool H1, int DMA_PER_STEP, class Issue>
+__device__ __forceinline__ void pipeline(f32x16 (&acc)[4][2], char* lds, int64_t K, const Issue& issue) {
   using Tr = Traits<T>;
   using Frag = typename Tr::Frag;
   constexpr int BK = Tr::kBK;
   constexpr int KS = BK / Tr::kKStep;
-  constexpr int kStoreAt = KS / 2 - 1;
+  static_assert(KS % 2 == 0, "fragment double buffer parity");
+  constexpr bool kMN = (LA == MNMAJ || LB == MNMAJ) && sizeof(T) == 2;
   const int wm = wave_m(), wn = wave_n();
-  Stage<T, 256> ga;
-  Stage<T, 128> gb0, gb1;
   const int nk = (int)((K + BK - 1) / BK);
-  char* const abuf0 = lds;
-  char* const bbuf0 = lds + kLdsTile;
-  char* const abuf1 = lds + 2 * kLdsTile;
-  char* const bbuf1 = lds + 3 * kLdsTile;
+  auto stage = [&](int step) { return lds + (step & 1) * (2 * kTileBytes); };
 
-  __syncthreads();  // the previous user of LDS is done
-  ga.load(A, lda, a_rows, 0, K);
-  if (H0) gb0.load(B0, ldb0, b0_rows, 0, K);
-  if (H1) gb1.load(B1, ldb1, b1_rows, 0, K);
-  ga.store(abuf0);
-  if (H0) gb0.store(bbuf0);
-  if (H1) gb1.store(bbuf0 + 128 * kLdsRow);
-  __syncthreads();
+  tile_barrier();  // the previous user of LDS is done
+  issue(0, stage(0));
+  if (nk > 1) issue(1, stage(1));
+  wait_dma_steps<DMA_PER_STEP>(nk > 1 ? 1 : 0);
+  tile_barrier();
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    const char* as = (kt & 1) ? abuf1 : abuf0;
-    const char* bs = (kt & 1) ? bbuf1 : bbuf0;
-    if (more) {
-      const int64_t k0 = (int64_t)(kt + 1) * BK;
-      ga.load(A, lda, a_rows, k0, K);
-      if (H0) gb0.load(B0, ldb0, b0_rows, k0, K);
-      if (H1) gb1.load(B1, ldb1, b1_rows, k0, K);
-    }
-    Frag a[2][4], b[2][2];
+  Frag a[2][4], b[2][2];
+  {
+    const char* as = stage(0);
+    const char* bs = as + kTileBytes;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) a[0][mb] = frag<T>(as, wm * 128 + mb * 32, 0);
-    if (H0) b[0][0] = frag<T>(bs, acc_col0(0, wn), 0);
-    if (H1) b[0][1] = frag<T>(bs, acc_col0(1, wn), 0);
+    for (int mb = 0; mb < 4; ++mb) a[0][mb] = op_frag<T, LA>(as, wm * 128 + mb * 32, 0);
+    if (H0) b[0][0] = op_frag<T, LB>(bs, acc_col0(0, wn), 0);
+    if (H1) b[0][1] = op_frag<T, LB>(bs, acc_col0(1, wn), 0);
+    if constexpr (kMN) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if constexpr (LA == MNMAJ) {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) lds_tie(a[0][mb]);
+      }
+      if constexpr (LB == MNMAJ) {
+        if (H0) lds_tie(b[0][0]);
+        if (H1) lds_tie(b[0][1]);
+      }
+    }
+  }
+  for (int kt = 0; kt < nk; ++kt) {
+    const char* as = stage(kt);
+    const char* bs = as + kTileBytes;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int cur = ks & 1;
       if (ks + 1 < KS) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) a[cur ^ 1][mb] = frag<T>(as, wm * 128 + mb * 32, ks + 1);
-        if (H0) b[cur ^ 1][0] = frag<T>(bs, acc_col0(0, wn), ks + 1);
-        if (H1) b[cur ^ 1][1] = frag<T>(bs, acc_col0(1, wn), ks + 1);
+        for (int mb = 0; mb < 4; ++mb) a[cur ^ 1][mb] = op_frag<T, LA>(as, wm * 128 + mb * 32, ks + 1);
+        if (H0) b[cur ^ 1][0] = op_frag<T, LB>(bs, acc_col0(0, wn), ks + 1);
+        if (H1) b[cur ^ 1][1] = op_frag<T, LB>(bs, acc_col0(1, wn), ks + 1);
+      } else if (kt + 1 < nk) {
+        // stage kt is fully read (its last fragments are in registers): wait
+        // for step kt+1, hand stage kt to step kt+2, prefetch step kt+1
+        wait_dma_steps<DMA_PER_STEP>(0);
+        tile_barrier();
+        if (kt + 2 < nk) issue(kt + 2, stage(kt));
+        const char* an = stage(kt + 1);
+        const char* bn = an + kTileBytes;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) a[cur ^ 1][mb] = op_frag<T, LA>(an, wm * 128 + mb * 32, 0);
+        if (H0) b[cur ^ 1][0] = op_frag<T, LB>(bn, acc_col0(0, wn), 0);
+        if (H1) b[cur ^ 1][1] = op_frag<T, LB>(bn, acc_col0(1, wn), 0);
       }
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         if (H0) acc[mb][0] = Tr::mma(a[cur][mb], b[cur][0], acc[mb][0]);
         if (H1) acc[mb][1] = Tr::mma(a[cur][mb], b[cur][1], acc[mb][1]);
       }
-      if (ks == kStoreAt && more) {
-        char* an = (kt & 1) ? abuf0 : abuf1;
-        char* bn = (kt & 1) ? bbuf0 : bbuf1;
-        ga.store(an);
-        if (H0) gb0.store(bn);
-        if (H1) gb1.store(bn + 128 * kLdsRow);
+      if constexpr (kMN) {
+        // the next sub-step's transposed fragments came from inline
+        // assembly: wait for them after this sub-step's MFMAs are issued
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if constexpr (LA == MNMAJ) {
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) lds_tie(a[cur ^ 1][mb]);
+        }
+        if constexpr (LB == MNMAJ) {
+          if (H0) lds_tie(b[cur ^ 1][0]);
+          if (H1) lds_tie(b[cur ^ 1][1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
+  }
+}
+
+// Fused loss tiles: acc[mb][nb] += A[wm*128 + mb*32 ..] x Bnb[wn*32 ..]^T with
+// A [a_rows x K] and two separate K-major B halves of 128 rows each.
+template <class T, bool H0, bool H1>
+__device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], char* lds,
+                                         const T* A, int64_t lda, int64_t a_rows,
+                                         const T* B0, int64_t ldb0, int64_t b0_rows,
+                                         const T* B1, int64_t ldb1, int64_t b1_rows,
+                                         int64_t K) {
+  KDma<T> da, db;
+  da.init(lda, a_rows, 0);
+  // B chunks i = 0, 1 hold rows 0..127 (half 0), i = 2, 3 rows 128..255 (half 1)
+  db.init(H0 ? ldb0 : ldb1, 0, 0);
+  {
+    const int w = wave_id(), l = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pslot = (i * 8 + w) * 64 + l;
+      const int r = pslot >> 3;
+      const int c = (pslot & 7) ^ kswz(r);
+      const bool half1 = i >= 2;
+      const int rr = half1 ? r - 128 : r;
+      const int64_t ld = half1 ? ldb1 : ldb0;
+      const int64_t rows = half1 ? b1_rows : b0_rows;
+      db.kc[i] = c * (16 / (int)sizeof(T));
+      db.off[i] = (rr < rows) ? (uint32_t)((rr * ld) * (int64_t)sizeof(T) + c * 16) : kOob;
+    }
+  }
+  constexpr int kDma = 4 + (H0 ? 2 : 0) + (H1 ? 2 : 0);
+  auto issue = [&](int step, char* st) {
+    const int64_t k0 = (int64_t)step * Traits<T>::kBK;
+    da.template issue<0, 4>(A, k0, K, st);
+    if (H0) db.template issue<0, 2>(B0, k0, K, st + kTileBytes);
+    if (H1) db.template issue<2, 4>(B1, k0, K, st + kTileBytes);
+  };
+  pipeline<T, KMAJ, KMAJ, H0, H1, kDma>(acc, lds, K, issue);
+}
+
+// General GEMM tile: A (256 rows) and B (256 rows) each K-major (KOperand)
+// or MN-major (MnOperand, 256 columns).
+template <class T, int LA, int LB, class OA, class OB>
+__device__ __forceinline__ void mainloop_g(f32x16 (&acc)[4][2], char* lds, const OA& A, const OB& B, int64_t K) {
+  using DA = typename std::conditional<LA == KMAJ, KDma<T>, MnDma<T>>::type;
+  using DB = typename std::conditional<LB == KMAJ, KDma<T>, MnDma<T>>::type;
+  DA da;
+  DB db;
+  if constexpr (LA == KMAJ) da.init(A.ld, A.rows, 0); else da.init(A.cols);
+  if constexpr (LB == KMAJ) db.init(B.ld, B.rows, 0); else db.init(B.cols);
+  auto issue = [&](int step, char* st) {
+    const int64_t k0 = (int64_t)step * Traits<T>::kBK;
+    if constexpr (LA == KMAJ) da.template issue<0, 4>(A.p, k0, K, st);
+    else da.issue(A, k0, st);
+    if constexpr (LB == KMAJ) db.template issue<0, 4>(B.p, k0, K, st + kTileBytes);
+    else db.issue(B, k0, st + kTileBytes);
+  };
+  pipeline<T, LA, LB, true, true, 8>(acc, lds, K, issue);
+}
+
+// Store 4 consecutive elements (one 8-byte or 16-byte store when full; p is
+// then aligned by construction), else the first n.
+template <class T>
+__device__ __forceinline__ void store4(T* p, const float (&x)[4], bool full, int n) {
+  if (full) {
+    if constexpr (sizeof(T) == 2) {
+      union { T e[4]; uint2 u; } v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v.e[i] = from_f32<T>(x[i]);
+      *reinterpret_cast<uint2*>(p) = v.u;
+    } else {
+      *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < n) p[i] = from_f32<T>(x[i]);
   }
 }
 

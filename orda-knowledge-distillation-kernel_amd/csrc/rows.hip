@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void k_merge(MergeParams P) {
     }
     P.rowp[4 * N + t] = (float)c0;
     P.rowp[5 * N + t] = (float)c1;
-    P.rowv[2 * N + t] = ignored ? 0.f : (float)(T * T * D);
+    P.rowv[2 * P.ldv + t] = ignored ? 0.f : (float)(T * T * D);
     return;
   }
 
@@ -104,9 +104,9 @@ __global__ __launch_bounds__(256) void k_merge(MergeParams P) {
   P.rowp[2 * N + t] = (float)lse_t;
   P.rowp[3 * N + t] = (float)lse_tT;
   for (int i = 0; i < 4; ++i) P.rowp[(4 + i) * N + t] = (float)c[i];
-  P.rowv[0 * N + t] = (float)ce_s;
-  P.rowv[1 * N + t] = (float)ce_t;
-  P.rowv[2 * N + t] = (P.div_on && !ignored) ? (float)(T * T * D) : 0.f;
+  P.rowv[0 * P.ldv + t] = (float)ce_s;
+  P.rowv[1 * P.ldv + t] = (float)ce_t;
+  P.rowv[2 * P.ldv + t] = (P.div_on && !ignored) ? (float)(T * T * D) : 0.f;
 }
 
 // Single workgroup: fixed-order fp64 sums of the row losses, the count of
@@ -151,6 +151,27 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeParams P) {
   }
 }
 
+// Count of non-ignored labels and the mean scale, as k_finalize computes them.
+__global__ __launch_bounds__(1024) void k_count(const int64_t* labels, int64_t N, int64_t ignore_index,
+                                                int reduction_sum, float* scal) {
+  __shared__ double red[1024];
+  const int tid = threadIdx.x;
+  double cnt = 0.0;
+  for (int64_t t = tid; t < N; t += 1024) cnt += (labels[t] != ignore_index) ? 1.0 : 0.0;
+  red[tid] = cnt;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const double count = red[0];
+    const double denom = count < 1.0 ? 1.0 : count;
+    scal[0] = reduction_sum ? 1.0f : 1.0f / (float)denom;
+    scal[1] = (float)count;
+  }
+}
+
 __global__ void k_zero2d(char* out, int64_t ld_bytes, int64_t R, int64_t c0_bytes, int64_t w_bytes) {
   const int64_t total = R * w_bytes;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
@@ -171,6 +192,11 @@ hipError_t launch_finalize(const FinalizeParams& P, hipStream_t s) {
   return hipGetLastError();
 }
 
+hipError_t launch_count(const int64_t* labels, int64_t N, int64_t ignore_index, int reduction_sum, float* scal,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(k_count, dim3(1), dim3(1024), 0, s, labels, N, ignore_index, reduction_sum, scal);
+  return hipGetLastError();
+}
 hipError_t launch_zero2d(void* out, int64_t ld, int64_t R, int64_t c0, int64_t c1, int esize, hipStream_t s) {
   if (R <= 0 || c1 <= c0) return hipSuccess;
   const int64_t total = R * (c1 - c0) * esize;

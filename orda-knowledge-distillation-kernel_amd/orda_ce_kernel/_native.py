@@ -16,11 +16,11 @@ import torch
 
 __all__ = [
     "ABI_VERSION", "Problem", "Tensors", "library", "library_path", "forward", "backward",
-    "saved_bytes", "forward_workspace_bytes", "backward_workspace_bytes", "gemm_abt",
+    "saved_bytes", "forward_workspace_bytes", "backward_workspace_bytes", "gemm_abt", "gemm",
     "MODE", "DTYPE", "FLAG", "KERNEL_CLASSES", "timing_enable", "timing_collect",
 ]
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MODE = {"tied": 0, "separate": 1, "precomputed_logits": 2, "precomputed_hidden": 3}
 DTYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -32,6 +32,7 @@ FLAG = {
     "compute_teacher_ce": 1 << 4,
     "compute_divergence": 1 << 5,
     "reduction_sum": 1 << 6,
+    "grads_in_forward": 1 << 7,
 }
 
 
@@ -57,6 +58,8 @@ class Problem(ctypes.Structure):
         ("kl_weight", ctypes.c_float),
         ("div_alpha", ctypes.c_float),
         ("div_beta", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+        ("token_chunk", ctypes.c_int64),
     ]
 
 
@@ -129,6 +132,12 @@ def library() -> ctypes.CDLL:
             ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
         ]
+        lib.orda_gemm.restype = ctypes.c_int
+        lib.orda_gemm.argtypes = [
+            ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+            ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ]
         lib.orda_timing_enable.restype = ctypes.c_int
         lib.orda_timing_enable.argtypes = [ctypes.c_int]
         lib.orda_timing_collect.restype = ctypes.c_int
@@ -197,6 +206,34 @@ def gemm_abt(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     c = torch.empty((M, N), dtype=a.dtype, device=a.device)
     rc = library().orda_gemm_abt(DTYPE[a.dtype], M, N, K, a.data_ptr(), b.data_ptr(), c.data_ptr(), _stream(a.device))
     _check(rc, "orda_gemm_abt")
+    return c
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, *, a_mn: bool = False, b_mn: bool = False, splits: int = 1) -> torch.Tensor:
+    """C = op(a) @ op(b).T on the library's general GEMM.
+
+    ``a`` is [M, K] (``a_mn=False``) or stored [K, M] (``a_mn=True``: the
+    operand is read MN-major, i.e. C = a.T @ ...); likewise ``b`` is [N, K]
+    or stored [K, N].  ``splits`` > 1 splits K into fp32 partials summed in a
+    fixed order (MN-major a and b only)."""
+    if a.dtype != b.dtype or a.dtype not in DTYPE:
+        raise ValueError("a and b must share a dtype among bf16, fp16, fp32")
+    a = a.contiguous()
+    b = b.contiguous()
+    M, K = (a.shape[1], a.shape[0]) if a_mn else (a.shape[0], a.shape[1])
+    N, Kb = (b.shape[1], b.shape[0]) if b_mn else (b.shape[0], b.shape[1])
+    if Kb != K:
+        raise ValueError(f"inner dimensions differ: {K} vs {Kb}")
+    c = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    ws = None
+    if splits > 1:
+        ws = torch.empty(splits * M * N * 4 + 512, dtype=torch.uint8, device=a.device)
+    rc = library().orda_gemm(
+        DTYPE[a.dtype], int(a_mn), int(b_mn), M, N, K, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+        c.data_ptr(), N, int(splits), ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        _stream(a.device),
+    )
+    _check(rc, "orda_gemm")
     return c
 
 

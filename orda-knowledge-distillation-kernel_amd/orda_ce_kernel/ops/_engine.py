@@ -1,13 +1,19 @@
 """Host side of the fused HIP path, shared by the four autograd Functions.
 
-Forward runs ``orda_forward``: the logits GEMMs with an online-softmax
-epilogue (no ``[N x V]`` tensor), per-row statistics and the loss scalars.
-Backward runs ``orda_backward``: it recomputes logits per vocabulary chunk,
-forms dlogits already scaled by ``grad_output * mean_scale`` and feeds the
-gradient GEMMs (fp32 accumulation).  The reference instead computes the
-gradients inside forward and scales them in backward
-(``ops/tied_teacher.py:468-495,531-564``); the results are the same, this
-order just never holds gradients that are not asked for.
+Two schedules, chosen per call by :func:`grads_in_forward`:
+
+* gradients inside forward (the reference's schedule,
+  ``ops/tied_teacher.py:366-516,531-564``; default for tied and separate
+  teachers when ``fp32_grad_weight_accumulation`` is off): ``orda_forward``
+  walks token chunks, materialises each chunk's logits in a workspace,
+  turns them into dlogits in place and multiplies them into the gradients,
+  accumulating grad W across chunks in the weight dtype as the reference's
+  ``addmm_`` does; backward only multiplies by ``grad_output``;
+* two-phase (``fp32_grad_weight_accumulation=True``, precomputed teachers,
+  the two-pass divergences, and forward-only calls): ``orda_forward``
+  computes the losses with an online-softmax scan (no logits stored) and
+  ``orda_backward`` recomputes the logits per vocabulary chunk, so every
+  grad W element is one fp32-accumulated GEMM rounded once.
 
 PyTorch allocates every buffer (outputs, the saved statistics, workspaces),
 so an out-of-memory error is a ``torch.cuda.OutOfMemoryError`` that the
@@ -25,7 +31,8 @@ from .. import _native
 from .._runtime import HAS_NATIVE, native_error
 from ..divergences import Divergence, resolve_divergence
 
-__all__ = ["FusedCall", "cast_to", "fused_forward", "fused_backward", "vocab_chunk_for", "require_native"]
+__all__ = ["FusedCall", "cast_to", "fused_forward", "fused_backward", "vocab_chunk_for", "require_native",
+           "grads_in_forward", "token_chunk_for"]
 
 
 def require_native(entry: str) -> None:
@@ -49,6 +56,27 @@ def vocab_chunk_for(BT: int, V: int, chunk_size, max_chunks) -> int:
 
     _, num_chunks = resolve_chunk_size(BT, chunk_size, V=V, max_chunks=max_chunks)
     return -(-int(V) // int(num_chunks))
+
+
+def token_chunk_for(chunk_size) -> int:
+    """Tokens per chunk of the gradients-in-forward schedule: twice the
+    reference's chunk (``utils/resolver.py:28-62``, as the dispatcher passes
+    it).  A chunk keeps only its student and teacher logits (16-bit) in HBM;
+    twice the reference's token count keeps a 128K vocabulary near 0.5 GB,
+    and the dispatcher's OOM retry, which halves the chunk, still halves it.
+    0 lets the library choose."""
+    if chunk_size is None or isinstance(chunk_size, str):
+        return 0
+    return 2 * int(chunk_size)
+
+
+def grads_in_forward(mode: str, use_fp32_accum, divergence, any_grad: bool) -> bool:
+    """Whether a call takes the gradients-in-forward schedule."""
+    from ..divergences import TWO_PASS
+
+    if not any_grad or bool(use_fp32_accum) or mode not in ("tied", "separate"):
+        return False
+    return resolve_divergence(divergence).name not in TWO_PASS
 
 
 def _kelems(dtype: torch.dtype) -> int:
@@ -94,6 +122,8 @@ class FusedCall:
     need_grad_weight: bool
     need_grad_teacher_hidden: bool = False
     need_grad_teacher_weight: bool = False
+    grads_in_forward: bool = False
+    token_chunk: int = 0
 
 
 def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None) -> _native.Problem:
@@ -112,6 +142,8 @@ def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None)
         flags |= _native.FLAG["compute_divergence"]
     if call.reduction == "sum":
         flags |= _native.FLAG["reduction_sum"]
+    if call.grads_in_forward:
+        flags |= _native.FLAG["grads_in_forward"]
     div = call.divergence
     p = _native.Problem()
     p.abi_version = _native.ABI_VERSION
@@ -132,6 +164,7 @@ def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None)
     p.kl_weight = float(call.kl_weight)
     p.div_alpha = float(div.alpha) if div.alpha is not None else 0.0
     p.div_beta = float(div.beta) if div.beta is not None else 0.0
+    p.token_chunk = int(call.token_chunk)
     return p
 
 
@@ -176,31 +209,47 @@ def fused_forward(ctx, call: FusedCall):
     t.teacher_hidden, t.teacher_weight, t.teacher_logits = _ptr(ht), _ptr(wt), _ptr(lt)
     t.out_loss, t.out_student_ce, t.out_teacher_ce, t.out_kl = (o.data_ptr() for o in outs)
     t.saved = saved.data_ptr()
+    grads = (None, None, None, None)
+    if call.grads_in_forward:
+        grads = _alloc_grads(problem.flags, hs, w, ht, wt)
+        t.grad_student_hidden, t.grad_weight, t.grad_teacher_hidden, t.grad_teacher_weight = (_ptr(g) for g in grads)
     _native.forward(problem, t, ws)
     del ws
 
     ctx.orda_problem = problem
     ctx.orda_shapes = (H, Ht)
     ctx.orda_mode = call.mode
-    ctx.save_for_backward(hs, w, ht, wt, lt, labels, saved)
+    if call.grads_in_forward:
+        ctx.save_for_backward(hs, w, ht, wt, lt, labels, saved, *grads)
+    else:
+        ctx.save_for_backward(hs, w, ht, wt, lt, labels, saved)
     return tuple(outs)
 
 
-def fused_backward(ctx, grad_output: torch.Tensor):
-    """Gradients ``(d_student_hidden, d_weight, d_teacher_hidden,
-    d_teacher_weight)`` in the compute dtype, unpadded; None where not needed."""
-    hs, w, ht, wt, lt, labels, saved = ctx.saved_tensors
-    problem = ctx.orda_problem
-    H, Ht = ctx.orda_shapes
-    flags = problem.flags
-    dev = hs.device
+def _alloc_grads(flags: int, hs, w, ht, wt):
     need = lambda name: bool(flags & _native.FLAG[name])  # noqa: E731
     g_hs = torch.empty_like(hs) if need("need_grad_student_hidden") else None
     g_w = torch.empty_like(w) if need("need_grad_weight") else None
     g_ht = torch.empty_like(ht) if (need("need_grad_teacher_hidden") and ht is not None) else None
     g_wt = torch.empty_like(wt) if (need("need_grad_teacher_weight") and wt is not None) else None
+    return g_hs, g_w, g_ht, g_wt
+
+
+def fused_backward(ctx, grad_output: torch.Tensor):
+    """Gradients ``(d_student_hidden, d_weight, d_teacher_hidden,
+    d_teacher_weight)`` in the compute dtype, unpadded; None where not needed."""
+    saved_tensors = ctx.saved_tensors
+    hs, w, ht, wt, lt, labels, saved = saved_tensors[:7]
+    problem = ctx.orda_problem
+    H, Ht = ctx.orda_shapes
+    flags = problem.flags
+    dev = hs.device
+    if flags & _native.FLAG["grads_in_forward"]:
+        g_hs, g_w, g_ht, g_wt = saved_tensors[7:]
+    else:
+        g_hs, g_w, g_ht, g_wt = _alloc_grads(flags, hs, w, ht, wt)
     go = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()
-    ws_bytes = _native.backward_workspace_bytes(problem)
+    ws_bytes = 0 if flags & _native.FLAG["grads_in_forward"] else _native.backward_workspace_bytes(problem)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     t = _native.Tensors()
     t.student_hidden, t.weight, t.labels = _ptr(hs), _ptr(w), _ptr(labels)

@@ -16,17 +16,20 @@ from torch.autograd.function import once_differentiable
 from .._runtime import default_compute_dtype
 from ..utils.resolver import DEFAULT_MAX_FUSED_SIZE
 from ._checks import check_common, check_labels_in_range, check_scalars
-from ._engine import FusedCall, cast_to, fused_backward, fused_forward, require_native, vocab_chunk_for
+from ._engine import (FusedCall, cast_to, fused_backward, fused_forward, grads_in_forward, require_native,
+                      token_chunk_for, vocab_chunk_for)
 
 __all__ = ["SeparateFullCEFunction", "SeparateStudentCEFunction", "separate_distillation_loss"]
 
 
 def _separate_call(student_hidden, teacher_hidden, weight, teacher_weight, labels, *, student_ce_weight,
                    ignore_index, reduction, chunk_size, kl_weight, kl_temperature, teacher_ce_weight, max_chunks,
-                   divergence, full):
+                   divergence, full, use_fp32_accum=None):
     BT = student_hidden.shape[0]
     V = weight.shape[0]
     dtype = default_compute_dtype(weight, teacher_weight, student_hidden, teacher_hidden)
+    need = (student_hidden.requires_grad, weight.requires_grad, full and teacher_hidden.requires_grad,
+            full and teacher_weight.requires_grad)
     return FusedCall(
         mode="separate",
         student_hidden=student_hidden.contiguous().to(dtype),
@@ -44,10 +47,12 @@ def _separate_call(student_hidden, teacher_hidden, weight, teacher_weight, label
         vocab_chunk=vocab_chunk_for(BT, V, chunk_size, max_chunks),
         divergence=divergence,
         compute_teacher_ce=full,
-        need_grad_student_hidden=student_hidden.requires_grad,
-        need_grad_weight=weight.requires_grad,
-        need_grad_teacher_hidden=full and teacher_hidden.requires_grad,
-        need_grad_teacher_weight=full and teacher_weight.requires_grad,
+        need_grad_student_hidden=need[0],
+        need_grad_weight=need[1],
+        need_grad_teacher_hidden=need[2],
+        need_grad_teacher_weight=need[3],
+        grads_in_forward=grads_in_forward("separate", use_fp32_accum, divergence, any(need)),
+        token_chunk=token_chunk_for(chunk_size),
     )
 
 
@@ -89,7 +94,7 @@ class SeparateStudentCEFunction(torch.autograd.Function):
             student_hidden, teacher_hidden, weight, teacher_weight, labels, student_ce_weight=student_ce_weight,
             ignore_index=ignore_index, reduction=reduction, chunk_size=chunk_size, kl_weight=kl_weight,
             kl_temperature=kl_temperature, teacher_ce_weight=0.0, max_chunks=max_chunks, divergence=divergence,
-            full=False,
+            full=False, use_fp32_accum=use_fp32_accum,
         )
         loss, ce_s, ce_t, kl = fused_forward(ctx, call)
         ctx.mark_non_differentiable(ce_s, ce_t, kl)
@@ -146,7 +151,7 @@ class SeparateFullCEFunction(torch.autograd.Function):
             student_hidden, teacher_hidden, weight, teacher_weight, labels, student_ce_weight=student_ce_weight,
             ignore_index=ignore_index, reduction=reduction, chunk_size=chunk_size, kl_weight=kl_weight,
             kl_temperature=kl_temperature, teacher_ce_weight=teacher_ce_weight, max_chunks=max_chunks,
-            divergence=divergence, full=True,
+            divergence=divergence, full=True, use_fp32_accum=use_fp32_accum,
         )
         loss, ce_s, ce_t, kl = fused_forward(ctx, call)
         ctx.mark_non_differentiable(ce_s, ce_t, kl)

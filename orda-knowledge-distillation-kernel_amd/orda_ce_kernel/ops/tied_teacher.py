@@ -20,7 +20,8 @@ from torch.autograd.function import once_differentiable
 from .._runtime import default_compute_dtype
 from ..utils.resolver import DEFAULT_MAX_FUSED_SIZE
 from ._checks import check_common, check_labels_in_range, check_scalars
-from ._engine import FusedCall, cast_to, fused_backward, fused_forward, require_native, vocab_chunk_for
+from ._engine import (FusedCall, cast_to, fused_backward, fused_forward, grads_in_forward, require_native,
+                      token_chunk_for, vocab_chunk_for)
 
 __all__ = ["TiedCEFunction", "tied_distillation_loss"]
 
@@ -79,6 +80,8 @@ class TiedCEFunction(torch.autograd.Function):
             need_grad_student_hidden=student_hidden.requires_grad,
             need_grad_weight=weight.requires_grad,
             need_grad_teacher_hidden=teacher_hidden.requires_grad,
+            grads_in_forward=grads_in_forward("tied", use_fp32_accum, divergence, ctx.compute_grad),
+            token_chunk=token_chunk_for(chunk_size),
         )
         loss, ce_s, ce_t, kl = fused_forward(ctx, call)
         ctx.mark_non_differentiable(ce_s, ce_t, kl)

@@ -70,7 +70,8 @@ def _grad_tol(dtype):
 
 
 def _run(mode, dtype, *, N=96, H=64, V=1000, Ht=None, seed=0, reduction="mean", w_s=1.0, w_t=None, kl_w=0.5,
-         T=1.0, div="forward_kl", config=None, ignore_frac=0.05, grad_teacher=True, grad_output=1.0):
+         T=1.0, div="forward_kl", config=None, ignore_frac=0.05, grad_teacher=True, grad_output=1.0,
+         profile="balanced"):
     o = _orda()
     hs, ht, W, Wt, y = _make(seed, N, H, V, dtype, Ht=Ht, ignore_frac=ignore_frac)
     dev = "cuda"
@@ -96,7 +97,7 @@ def _run(mode, dtype, *, N=96, H=64, V=1000, Ht=None, seed=0, reduction="mean", 
         kw = dict(teacher_hidden=_np(ht), teacher_weight=_np(Wt))
     out = o.distillation_loss(
         hs_d, W_d, y_d, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t, kl_weight=kl_w,
-        kl_temperature=T, reduction=reduction, backend="triton", config=config, divergence=div,
+        kl_temperature=T, reduction=reduction, backend="triton", config=config, divergence=div, profile=profile,
     )
     (out.loss * grad_output).backward()
     omode = "precomputed" if mode.startswith("precomputed") else mode
@@ -262,3 +263,97 @@ def test_gemm_engine_matches_torch():
             tol = 1e-4 if dtype == torch.float32 else 2e-2
             err = (c.double() - ref).abs().max().item()
             assert err <= tol * max(1.0, ref.abs().max().item()), (dtype, M, N, K, err)
+
+
+# ------------------------------------------------------------------ schedules
+# profile="balanced" (default): gradients inside forward over token chunks
+# with materialised logits (tied / separate, one-pass divergences);
+# profile="debug" (fp32 grad-W accumulation): scan forward + recomputing
+# backward.  Both against the oracle, and against each other.
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("mode", ["tied", "separate"])
+def test_two_phase_schedule_matches_oracle(dtype, mode):
+    out, ref, hs, W, teacher = _run(mode, dtype, Ht=96 if mode == "separate" else None, T=1.6, kl_w=0.4, w_t=0.3,
+                                    profile="debug")
+    _check(out, ref, hs, W, dtype)
+    tol = _grad_tol(dtype)
+    _close_grad(teacher.hidden.grad, ref["grad_teacher_hidden"], "grad_teacher_hidden", tol)
+    if mode == "separate":
+        _close_grad(teacher.weight.grad, ref["grad_teacher_weight"], "grad_teacher_weight", tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("mode", ["tied", "separate"])
+def test_grads_in_forward_over_ragged_token_chunks(dtype, mode):
+    """chunk_size=20 -> 40-token chunks over N=96: 40 + 40 + 16, the last one
+    ragged (zeroed padding columns), grad W accumulated across chunks."""
+    from orda_ce_kernel import KernelConfig
+
+    for div in ("forward_kl", "reverse_kl", "hellinger", "squared_l2"):
+        out, ref, hs, W, teacher = _run(mode, dtype, Ht=72 if mode == "separate" else None, T=1.3, kl_w=0.6,
+                                        w_t=0.5, div=div, config=KernelConfig(chunk_size=20))
+        _check(out, ref, hs, W, dtype)
+        tol = _grad_tol(dtype)
+        _close_grad(teacher.hidden.grad, ref["grad_teacher_hidden"], "grad_teacher_hidden", tol)
+        if mode == "separate":
+            _close_grad(teacher.weight.grad, ref["grad_teacher_weight"], "grad_teacher_weight", tol)
+
+
+def test_schedules_agree_on_a_larger_problem():
+    """N=600 tokens, V=5000, H=256 (several vocabulary tiles, split-K grad
+    hidden, 3 token chunks): balanced vs debug gradients."""
+    from orda_ce_kernel import KernelConfig
+
+    res = {}
+    for profile, cfg in (("balanced", KernelConfig(chunk_size=128)), ("debug", None)):
+        out, ref, hs, W, teacher = _run("tied", torch.bfloat16, N=600, H=256, V=5000, T=1.0, kl_w=1.0, w_t=1.0,
+                                        config=cfg, profile=profile, seed=3)
+        _check(out, ref, hs, W, torch.bfloat16)
+        res[profile] = (hs.grad.float(), W.grad.float(), teacher.hidden.grad.float())
+    for a, b in zip(res["balanced"], res["debug"]):
+        scale = b.abs().max().item()
+        assert (a - b).abs().max().item() <= 2e-2 * scale
+
+
+def test_grads_in_forward_are_bit_stable():
+    o = _orda()
+    hs, ht, W, _, y = _make(12, 300, 128, 2000, torch.bfloat16)
+    grads = []
+    for _ in range(2):
+        hs_d, ht_d, W_d = (x.cuda().requires_grad_(True) for x in (hs, ht, W))
+        out = o.distillation_loss(hs_d, W_d, y.cuda(), o.TiedTeacher(ht_d), kl_weight=1.0, backend="triton",
+                                  config=o.KernelConfig(chunk_size=64))
+        out.loss.backward()
+        grads.append((out.loss.detach(), hs_d.grad, W_d.grad, ht_d.grad))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+# --------------------------------------------------------- general GEMM
+def _gemm_case(dtype, a_mn, b_mn, M, N, K, splits=1, seed=0):
+    from orda_ce_kernel import _native
+
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(M, K, generator=g).to(dtype)
+    b = torch.randn(N, K, generator=g).to(dtype)
+    a_in = a.t().contiguous() if a_mn else a
+    b_in = b.t().contiguous() if b_mn else b
+    c = _native.gemm(a_in.cuda(), b_in.cuda(), a_mn=a_mn, b_mn=b_mn, splits=splits).float().cpu()
+    ref = a.double() @ b.double().t()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    err = (c.double() - ref).abs().max().item()
+    assert err <= tol * max(1.0, ref.abs().max().item()), (dtype, a_mn, b_mn, M, N, K, splits, err)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("a_mn, b_mn", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_general_gemm_layouts_match_torch(dtype, a_mn, b_mn):
+    for M, N, K in ((264, 272, 520), (8, 264, 64), (256, 256, 200), (520, 16, 1000)):
+        _gemm_case(dtype, a_mn, b_mn, M, N, K)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "f16", "f32"])
+def test_general_gemm_split_k_matches_torch(dtype):
+    for M, N, K, splits in ((264, 272, 5000, 4), (40, 512, 3000, 7), (256, 256, 128, 3)):
+        _gemm_case(dtype, 1, 1, M, N, K, splits=splits)

@@ -26,7 +26,7 @@ def _declared_functions():
 
 def test_library_loads_with_matching_abi():
     lib = _native.library()
-    assert lib.orda_abi_version() == _native.ABI_VERSION == 1
+    assert lib.orda_abi_version() == _native.ABI_VERSION == 2
 
 
 def test_every_declared_function_is_exported():
@@ -53,7 +53,7 @@ int main(void) {
   printf("orda_tensors_t %zu\n", sizeof(orda_tensors_t));
   printf("orda_timing_t %zu\n", sizeof(orda_timing_t));
   F(orda_problem_t, n_rows) F(orda_problem_t, vocab_chunk) F(orda_problem_t, flags) F(orda_problem_t, divergence)
-  F(orda_problem_t, temperature) F(orda_problem_t, div_beta)
+  F(orda_problem_t, temperature) F(orda_problem_t, div_beta) F(orda_problem_t, token_chunk)
   F(orda_tensors_t, labels) F(orda_tensors_t, saved) F(orda_tensors_t, grad_output)
   F(orda_tensors_t, grad_teacher_weight)
   F(orda_timing_t, milliseconds) F(orda_timing_t, executed_flops)
@@ -90,7 +90,7 @@ def test_struct_layout_matches_the_header(tmp_path):
 
 def _problem(**kw):
     p = _native.Problem()
-    p.abi_version = 1
+    p.abi_version = _native.ABI_VERSION
     p.mode = 0
     p.dtype = 0
     p.n_rows, p.vocab, p.hidden, p.teacher_hidden = 8192, 128256, 4096, 4096
@@ -119,7 +119,7 @@ def test_workspace_queries_for_the_headline_shape():
 @pytest.mark.parametrize(
     "field, value, message",
     [
-        ("abi_version", 2, "abi_version"),
+        ("abi_version", 1, "abi_version"),
         ("mode", 9, "unknown mode"),
         ("dtype", 7, "unknown dtype"),
         ("n_rows", 0, "must be > 0"),
@@ -155,6 +155,39 @@ def test_gemm_entry_validates_shapes():
     lib = _native.library()
     assert lib.orda_gemm_abt(0, 0, 4, 8, None, None, None, None) == -1
     assert lib.orda_gemm_abt(0, 4, 4, 12, 16, 16, 16, None) == -1  # K not a multiple of 8 (bf16)
+    # general entry: MN-major A needs M a multiple of 8; K-major needs K; splits in range
+    assert lib.orda_gemm(0, 1, 0, 12, 16, 16, 16, 16, 16, 16, 16, 16, 1, None, 0, None) == -1
+    assert lib.orda_gemm(0, 0, 0, 16, 16, 12, 16, 16, 16, 16, 16, 16, 1, None, 0, None) == -1
+    assert lib.orda_gemm(0, 0, 0, 16, 16, 16, 16, 16, 16, 16, 16, 16, 0, None, 0, None) == -1
+    assert lib.orda_gemm(0, 2, 0, 16, 16, 16, 16, 16, 16, 16, 16, 16, 1, None, 0, None) == -1
+    assert b"a_mn" in lib.orda_last_error()
+
+
+GIF = _native.FLAG["grads_in_forward"]
+
+
+def test_grads_in_forward_plan_for_the_headline_shape():
+    p = _problem(flags=0x33 | GIF)
+    ws = _native.forward_workspace_bytes(p)
+    # one token chunk of student + teacher logits (1024 tokens x V x 2 x bf16)
+    # plus split-K partials and row state; far below an [N x V] tensor
+    assert 1024 * 128256 * 2 * 2 < ws < 900 << 20
+    p.token_chunk = 512
+    assert _native.forward_workspace_bytes(p) < ws
+    # the backward only scales the gradients: no workspace
+    assert lib_backward_bytes(p) == 0
+
+
+def lib_backward_bytes(p):
+    return _native.library().orda_backward_workspace_bytes(ctypes.byref(p))
+
+
+@pytest.mark.parametrize("field, value", [("mode", 2), ("mode", 3), ("divergence", 11), ("divergence", 14)])
+def test_grads_in_forward_rejects_unsupported_cases(field, value):
+    p = _problem(flags=0x33 | GIF, div_alpha=0.1, div_beta=0.5, **{field: value})
+    lib = _native.library()
+    assert lib.orda_forward_workspace_bytes(ctypes.byref(p)) == 0
+    assert b"ORDA_GRADS_IN_FORWARD" in lib.orda_last_error()
 
 
 def test_timing_hook_without_launches_reports_zeros():
