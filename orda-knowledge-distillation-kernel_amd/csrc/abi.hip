@@ -73,7 +73,8 @@ struct Plan {
   int64_t fn, fnP, fldL, fnchunks;
   int f_nvr, f_tpr, splits_s, splits_t;
   int64_t kps_s, kps_t;
-  size_t off_L, off_fpart, off_flabelx, off_frowp, off_frowv, off_split;
+  size_t off_L, off_fpart, off_flabelx, off_frowp, off_frowv, off_split, off_fhT, off_fhtT;
+  int64_t fldh;
 };
 
 constexpr int kScalFloats = 64;  // scalars at the head of the saved buffer
@@ -269,6 +270,10 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     if (pl.need_gs && pl.splits_s > 1) split_cols = pl.splits_s * pl.H;
     if (pl.w_dln_t && pl.splits_t > 1 && pl.splits_t * pl.Ht > split_cols) split_cols = pl.splits_t * pl.Ht;
     pl.off_split = split_cols ? carve(fo, (size_t)split_cols * pl.fnP * 4) : 0;
+    // the chunk's hidden states transposed (token-contiguous) for the grad-W GEMMs
+    pl.fldh = (tied && pl.w_dlt_t) ? 2 * pl.fnP : pl.fnP;
+    pl.off_fhT = pl.need_gw ? carve(fo, (size_t)pl.H * pl.fldh * pl.eb) : 0;
+    pl.off_fhtT = (sep && pl.need_gwt && pl.w_dlt_t) ? carve(fo, (size_t)pl.Ht * pl.fnP * pl.eb) : 0;
     pl.fwd_bytes = fo + kAlign;
     pl.bwd_bytes = 0;
   }
@@ -636,16 +641,27 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       if (pl.store_t) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(L, ldL, V, nP + nc, 2 * nP, eb, s)); }
     }
 
+    // grad W (+)= dL^T [hs; ht] with both operands K-major over tokens: the
+    // chunk's hidden states are transposed into hT (padding columns zero)
     const int wmode = c == 0 ? GEMM_STORE : GEMM_ACC_T;
+    auto transpose_chunk = [&](const T* src, int64_t cols, char* dst, int64_t ldd, int64_t col0) -> int {
+      { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_transpose<T>(src, cols, dst + col0 * eb, ldd, nc, cols, s)); }
+      if (nc < nP) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(dst, ldd, cols, col0 + nc, col0 + nP, eb, s)); }
+      return ORDA_OK;
+    };
     if (pl.need_gw) {
       const bool both = tied && pl.w_dlt_t;
+      char* hT = ws + pl.off_fhT;
+      ORDA_TRY(transpose_chunk(hs + r0 * H, H, hT, pl.fldh, 0));
+      if (both) ORDA_TRY(transpose_chunk(ht + r0 * H, H, hT, pl.fldh, nP));
       const int64_t K = both ? 2 * nP : nP;
-      ORDA_TRY(gemm2<T>(KMAJ, MNMAJ, L, ldL, hs + r0 * H, H, both ? ht + r0 * H : nullptr, H, nP, nc,
-                        both ? nc : 0, t->grad_weight, nullptr, H, V, H, K, wmode, 1, 0, s, ORDA_K_GEMM_W,
-                        2.0 * (double)V * (double)H * (double)(both ? 2 * nc : nc)));
+      ORDA_TRY(gemm2<T>(KMAJ, KMAJ, L, ldL, hT, pl.fldh, nullptr, 0, K, K, 0, t->grad_weight, nullptr, H, V, H, K,
+                        wmode, 1, 0, s, ORDA_K_GEMM_W, 2.0 * (double)V * (double)H * (double)(both ? 2 * nc : nc)));
     }
     if (sep && pl.need_gwt && pl.w_dlt_t) {
-      ORDA_TRY(gemm2<T>(KMAJ, MNMAJ, static_cast<char*>(L) + nP * eb, ldL, ht + r0 * Ht, Ht, nullptr, 0, nP, nc, 0,
+      char* htT = ws + pl.off_fhtT;
+      ORDA_TRY(transpose_chunk(ht + r0 * Ht, Ht, htT, nP, 0));
+      ORDA_TRY(gemm2<T>(KMAJ, KMAJ, static_cast<char*>(L) + nP * eb, ldL, htT, nP, nullptr, 0, nP, nP, 0,
                         t->grad_teacher_weight, nullptr, Ht, V, Ht, nP, wmode, 1, 0, s, ORDA_K_GEMM_W,
                         2.0 * (double)V * (double)Ht * (double)nc));
     }

@@ -607,6 +607,42 @@ __device__ __forceinline__ void gemm_epilogue_q(const f32x16 (&acc)[4][2], const
   float* D = C32 + m0 * P.ldc + n0;
   const int ldc = (int)P.ldc;
   const int mlim = (int)min<int64_t>(P.M - m0, 256), nlim = (int)min<int64_t>(P.N - n0, 256);
+  if constexpr (MODE == GEMM_ACC_T && sizeof(T) == 2) {
+    if (mlim == 256 && nlim == 256) {
+      // interior tile: issue every read of C before the first add, so one
+      // memory latency covers the whole read-modify-write
+      uint2 cv[4][2][4];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int m = wm * 128 + acc_row(mb, g * 4, lane) + q;
+            const int nbase = acc_col0(nb, wn) + (lane & 31) - q;
+            cv[mb][nb][g] = *reinterpret_cast<const uint2*>(C + m * ldc + nbase);
+          }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float x[4], o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = acc[mb][nb][g * 4 + e];
+            quad_transpose(x, o);
+            const int m = wm * 128 + acc_row(mb, g * 4, lane) + q;
+            const int nbase = acc_col0(nb, wn) + (lane & 31) - q;
+            union { T e[4]; uint2 u; } v;
+            v.u = cv[mb][nb][g];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
+            store4(C + m * ldc + nbase, o, true, 4);
+          }
+      return;
+    }
+  }
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
@@ -773,7 +809,7 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
   const bool full = nt == 4;
   const bool need_t = DIV >= 0 || P.tgrad;
   // R rows in flight per iteration: their loads are issued together
-  constexpr int R = 4;
+  constexpr int R = 8;
   for (int64_t vb = v0; vb < v1; vb += R) {
     float xs[R][4], xt[R][4];
 #pragma unroll
@@ -1004,6 +1040,7 @@ inline void gemm2_go(const GemmParams& P, hipStream_t s) {
       case MNMAJ * 100 + MNMAJ * 10 + GEMM_STORE: gemm2_go<T, MNMAJ, MNMAJ, GEMM_STORE>(P, s); break; \
       case MNMAJ * 100 + MNMAJ * 10 + GEMM_SPLIT: gemm2_go<T, MNMAJ, MNMAJ, GEMM_SPLIT>(P, s); break; \
       case KMAJ * 100 + KMAJ * 10 + GEMM_STORE: gemm2_go<T, KMAJ, KMAJ, GEMM_STORE>(P, s); break; \
+      case KMAJ * 100 + KMAJ * 10 + GEMM_ACC_T: gemm2_go<T, KMAJ, KMAJ, GEMM_ACC_T>(P, s); break; \
       case MNMAJ * 100 + KMAJ * 10 + GEMM_STORE: gemm2_go<T, MNMAJ, KMAJ, GEMM_STORE>(P, s); break; \
       default: return hipErrorInvalidValue;                                                \
     }                                                                                      \
