@@ -806,48 +806,60 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
   }
   T* Ls = static_cast<T*>(P.L) + t0;
   T* Lt = Ls + P.tcol;
-  const bool full = nt == 4;
   const bool need_t = DIV >= 0 || P.tgrad;
-  // R rows in flight per iteration: their loads are issued together
-  constexpr int R = 8;
-  for (int64_t vb = v0; vb < v1; vb += R) {
-    float xs[R][4], xt[R][4];
+  // dlogits of one row from its loaded logits (4 tokens)
+  auto row = [&](int64_t v, const float (&xs)[4], const float (&xt)[4], float (&ds)[4], float (&dt)[4]) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t v = vb + r;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xs[r][i] = xt[r][i] = 0.f;
-      if (v < v1) {
-        load4(Ls + v * P.ldL, xs[r], full, nt);
-        if (need_t) load4(Lt + v * P.ldL, xt[r], full, nt);
+    for (int i = 0; i < 4; ++i) {
+      const float onehot = (v == yeff[i]) ? 1.f : 0.f;
+      const float ps1 = fexp(xs[i] - lse_s[i]);
+      float d = sc_s[i] * (ps1 - onehot);
+      if constexpr (DIV >= 0) {
+        const float lps = xs[i] * invT - lse_sT[i];
+        const float lpt = xt[i] * invT - lse_tT[i];
+        const float psT = T1 ? ps1 : fexp(lps);
+        const float ptT = fexp(lpt);
+        d += sc_d[i] * div_grad<DIV>(lps, lpt, psT, ptT, c[i], P.alpha, P.beta);
       }
+      ds[i] = d;
+      dt[i] = sc_t[i] * (fexp(xt[i] - lse_t[i]) - onehot);
     }
+  };
+  int64_t v = v0;
+  if (nt == 4) {
+    // interior: R rows per iteration, every load issued before any use
+    constexpr int R = 8;
+    for (; v + R <= v1; v += R) {
+      float xs[R][4], xt[R][4];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t v = vb + r;
-      float ds[4], dt[4];
+      for (int r = 0; r < R; ++r) {
+        load4(Ls + (v + r) * P.ldL, xs[r], true, 4);
+        if (need_t) load4(Lt + (v + r) * P.ldL, xt[r], true, 4);
+        else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float onehot = (v == yeff[i]) ? 1.f : 0.f;
-        const float ps1 = fexp(xs[r][i] - lse_s[i]);
-        float d = sc_s[i] * (ps1 - onehot);
-        if constexpr (DIV >= 0) {
-          const float lps = xs[r][i] * invT - lse_sT[i];
-          const float lpt = xt[r][i] * invT - lse_tT[i];
-          const float psT = T1 ? ps1 : fexp(lps);
-          const float ptT = fexp(lpt);
-          d += sc_d[i] * div_grad<DIV>(lps, lpt, psT, ptT, c[i], P.alpha, P.beta);
+          for (int i = 0; i < 4; ++i) xt[r][i] = 0.f;
         }
-        ds[i] = d;
-        dt[i] = sc_t[i] * (fexp(xt[r][i] - lse_t[i]) - onehot);
       }
-      if (v < v1) {
-        store4(Ls + v * P.ldL, ds, full, nt);
-        if (P.tgrad) store4(Lt + v * P.ldL, dt, full, nt);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float ds[4], dt[4];
+        row(v + r, xs[r], xt[r], ds, dt);
+        store4(Ls + (v + r) * P.ldL, ds, true, 4);
+        if (P.tgrad) store4(Lt + (v + r) * P.ldL, dt, true, 4);
       }
     }
   }
+  // edges: the last rows of the block, or a partial token quad
+  for (; v < v1; ++v) {
+    float xs[4], xt[4] = {0.f, 0.f, 0.f, 0.f}, ds[4], dt[4];
+    load4(Ls + v * P.ldL, xs, nt == 4, nt);
+    if (need_t) load4(Lt + v * P.ldL, xt, nt == 4, nt);
+    row(v, xs, xt, ds, dt);
+    store4(Ls + v * P.ldL, ds, nt == 4, nt);
+    if (P.tgrad) store4(Lt + v * P.ldL, dt, nt == 4, nt);
+  }
 }
+
 
 // ---------------------------------------------------------------- transpose
 // out[c * ldo + r] = in[r * ldi + c] for r < R, c < C (64 x 64 LDS tiles).
