@@ -225,21 +225,17 @@ def cpu_baseline(cfg, seed, budget_s):
     }
 
 
-KERNEL_OF_CLASS = {"scan": "k_scan", "dlogits": "k_dl", "gemm_w": "k_gemm", "gemm_h": "k_gemm"}
-
-
 def profiled_traffic(config: str, kernel_class: str):
     """HBM bytes per launch of ``kernel_class`` at ``config`` from the
     committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/*_pmc_traffic.md,
-    its fenced json line), or None when no summary covers it."""
-    kernel = KERNEL_OF_CLASS.get(kernel_class)
+    one fenced json line per kernel class), or None when none covers it."""
     for md in sorted((ROOT / "profiles").glob("*_pmc_traffic.md")):
         for line in md.read_text().splitlines():
             line = line.strip()
             if not (line.startswith("{") and "traffic_bytes_per_launch" in line):
                 continue
             rec = json.loads(line)
-            if rec.get("workload") == config and rec.get("kernel") == kernel:
+            if rec.get("workload") == config and rec.get("class") == kernel_class:
                 return float(rec["traffic_bytes_per_launch"]), md.name
     return None, None
 
