@@ -439,6 +439,23 @@ __device__ __forceinline__ void pipeline(f32x16 (&acc)[4][2], char* lds, int64_t
         if (H0) acc[mb][0] = Tr::mma(a[cur][mb], b[cur][0], acc[mb][0]);
         if (H1) acc[mb][1] = Tr::mma(a[cur][mb], b[cur][1], acc[mb][1]);
       }
+      if constexpr (!kMN) {
+        if (ks + 1 < KS) {
+          // interleave the next sub-step's fragment reads with this
+          // sub-step's MFMAs (MFMA, ds_read, MFMA, ...) instead of issuing
+          // every read first: the MFMA pipe keeps work while reads queue
+          constexpr int kMfma = 4 * ((H0 ? 1 : 0) + (H1 ? 1 : 0));
+          constexpr int kReads = 4 + (H0 ? 1 : 0) + (H1 ? 1 : 0);
+          constexpr int kPairs = kMfma < kReads ? kMfma : kReads;
+#pragma unroll
+          for (int q = 0; q < kPairs; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+          }
+          if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+          if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
+        }
+      }
       if constexpr (kMN) {
         // the next sub-step's transposed fragments came from inline
         // assembly: wait for them after this sub-step's MFMAs are issued
