@@ -317,7 +317,7 @@ __device__ __forceinline__ void scan_variant(RowState& S, const f32x16 (&acc)[4]
 template <class T>
 __device__ __forceinline__ void store_logits(const f32x16 (&acc)[4][2], const FusedParams& P, int64_t v0,
                                              int64_t t0) {
-  const int lane = threadIdx.x & 63;
+  const int lane = opaque_lane();
   const int wm = wave_m(), wn = wave_n();
   const int q = lane & 3;
   const int64_t tb = t0 + wn * 32 + (lane & 31) - q;  // first token of the quad
@@ -378,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
     asm volatile("" : "+s"(t0v));
     fused_logits<T>(acc, lds, P, v0, t0v);
     if constexpr (STORE) store_logits<T>(acc, P, v0, t0v);
-    const int vlane0 = wm * 128 + (lane >> 5) * 4;
+    const int vlane0 = wm * 128 + (opaque_lane() >> 5) * 4;
     const int64_t vlimit = P.V - v0;
     scan_variant<SV>(st, acc, vlane0, vlimit, vlimit >= 256, lse_sT, lse_tT, P);
   }
@@ -600,7 +600,7 @@ __device__ __forceinline__ void load4(const T* p, float (&x)[4], bool full, int 
 template <class T, int MODE>
 __device__ __forceinline__ void gemm_epilogue_q(const f32x16 (&acc)[4][2], const GemmParams& P, float* C32,
                                                 int64_t m0, int64_t n0) {
-  const int lane = threadIdx.x & 63;
+  const int lane = opaque_lane();
   const int wm = wave_m(), wn = wave_n();
   const int q = lane & 3;
   T* C = static_cast<T*>(P.C) + m0 * P.ldc + n0;
@@ -609,37 +609,41 @@ __device__ __forceinline__ void gemm_epilogue_q(const f32x16 (&acc)[4][2], const
   const int mlim = (int)min<int64_t>(P.M - m0, 256), nlim = (int)min<int64_t>(P.N - n0, 256);
   if constexpr (MODE == GEMM_ACC_T && sizeof(T) == 2) {
     if (mlim == 256 && nlim == 256) {
-      // interior tile: issue every read of C before the first add, so one
-      // memory latency covers the whole read-modify-write
-      uint2 cv[4][2][4];
+      // interior tile: issue the reads of C for half the tile (two row
+      // blocks) before its first add, so one memory latency covers 16 of the
+      // read-modify-writes and 32 registers hold the loaded values
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int h = 0; h < 2; ++h) {
+        uint2 cv[2][2][4];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int m = wm * 128 + acc_row(mb, g * 4, lane) + q;
-            const int nbase = acc_col0(nb, wn) + (lane & 31) - q;
-            cv[mb][nb][g] = *reinterpret_cast<const uint2*>(C + m * ldc + nbase);
-          }
+          for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+            for (int g = 0; g < 4; ++g) {
+              const int m = wm * 128 + acc_row(2 * h + j, g * 4, lane) + q;
+              const int nbase = acc_col0(nb, wn) + (lane & 31) - q;
+              cv[j][nb][g] = *reinterpret_cast<const uint2*>(C + m * ldc + nbase);
+            }
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float x[4], o[4];
+          for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = acc[mb][nb][g * 4 + e];
-            quad_transpose(x, o);
-            const int m = wm * 128 + acc_row(mb, g * 4, lane) + q;
-            const int nbase = acc_col0(nb, wn) + (lane & 31) - q;
-            union { T e[4]; uint2 u; } v;
-            v.u = cv[mb][nb][g];
+            for (int g = 0; g < 4; ++g) {
+              float x[4], o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
-            store4(C + m * ldc + nbase, o, true, 4);
-          }
+              for (int e = 0; e < 4; ++e) x[e] = acc[2 * h + j][nb][g * 4 + e];
+              quad_transpose(x, o);
+              const int m = wm * 128 + acc_row(2 * h + j, g * 4, lane) + q;
+              const int nbase = acc_col0(nb, wn) + (lane & 31) - q;
+              union { T e[4]; uint2 u; } v;
+              v.u = cv[j][nb][g];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
+              store4(C + m * ldc + nbase, o, true, 4);
+            }
+      }
       return;
     }
   }
@@ -690,50 +694,89 @@ __device__ __forceinline__ auto gemm_operand(const T* p, int64_t ld, int64_t row
 }
 
 // General GEMM: C[M x N] (mode) A * B^T with A and B each K-major or
-// MN-major (Layout), split-K over gridDim = tiles x splits (split s covers
-// K rows [s * k_per_split, ...) and writes its own fp32 partial in GEMM_SPLIT
-// mode), and, for an MN-major B, two row segments (B rows [0, b_kseg) from B,
-// the rest from B1): the student and teacher hidden states of one token
-// chunk feeding one grad-W GEMM.
+// MN-major (Layout), split-K (split s covers K rows [s * k_per_split, ...)
+// and writes its own fp32 partial in GEMM_SPLIT mode), and, for an MN-major
+// B, two row segments (B rows [0, b_kseg) from B, the rest from B1): the
+// student and teacher hidden states of one token chunk feeding one grad-W
+// GEMM.  Persistent: workgroup b (in XCD order) owns tiles b, b + grid, ...
+// in band order, run as one flattened pipeline (pipeline_tiles), so the next
+// tile's first K steps load while the current one finishes and writes out.
 template <class T, int LA, int LB, int MODE>
 __global__ __launch_bounds__(kThreads) void k_gemm2(GemmParams P) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   f32x16 acc[4][2];
+  constexpr int BK = Traits<T>::kBK;
   const int tiles = P.tiles_m * P.tiles_n;
-  const int tall = xcd_order(blockIdx.x, gridDim.x);
-  const int split = tall / tiles;
-  const int t = tall - split * tiles;
-  constexpr int G = 8;
-  const int band = t / (G * P.tiles_n);
-  const int first_m = band * G;
-  const int gm = min(P.tiles_m - first_m, G);
-  const int rem = t % (G * P.tiles_n);
-  const int tm = first_m + rem % gm;
-  const int tn = rem / gm;
-  const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
-  const int64_t kb = (int64_t)split * P.k_per_split;
-  const int64_t klen = min<int64_t>(P.K - kb, P.k_per_split);
+  const int total = tiles * P.splits;
+  const int grid = gridDim.x;
+  const int b = xcd_order(blockIdx.x, grid);
+  const int ntiles = b < total ? (total - 1 - b) / grid + 1 : 0;
+  const int nk = (int)((P.k_per_split + BK - 1) / BK);
+  struct Tile { int split; int64_t m0, n0, kb, klen; };
+  auto tile_of = [&](int i) {
+    const int t_all = b + i * grid;
+    Tile x;
+    x.split = t_all / tiles;
+    const int t = t_all - x.split * tiles;
+    constexpr int G = 8;
+    const int band = t / (G * P.tiles_n);
+    const int first_m = band * G;
+    const int gm = min(P.tiles_m - first_m, G);
+    const int rem = t % (G * P.tiles_n);
+    x.m0 = (int64_t)(first_m + rem % gm) * 256;
+    x.n0 = (int64_t)(rem / gm) * 256;
+    x.kb = (int64_t)x.split * P.k_per_split;
+    x.klen = min<int64_t>(P.K - x.kb, P.k_per_split);
+    return x;
+  };
   const T* A = static_cast<const T*>(P.A);
   const T* B = static_cast<const T*>(P.B);
+  const T* B1 = static_cast<const T*>(P.B1);
+  using DA = typename std::conditional<LA == KMAJ, KDma<T>, MnDma<T>>::type;
+  using DB = typename std::conditional<LB == KMAJ, KDma<T>, MnDma<T>>::type;
+  DA da;
+  DB db;
+  da.init();
+  db.init();
+  // pipeline_tiles issues the steps once each, in order: track the tile and
+  // K step of the next one instead of dividing the step index
+  int in = 0, kn = 0;
+  Tile x = tile_of(0);
+  auto issue = [&](int, char* st) {
+    if (kn == nk) {
+      kn = 0;
+      x = tile_of(++in);
+    }
+    const int64_t k0 = (int64_t)(kn++) * BK;  // inside the split
+    if constexpr (LA == KMAJ) {
+      if (k0 == 0) da.template place<0, 4>(P.lda, P.M - x.m0, 0);
+      da.template issue<0, 4>(A + x.m0 * P.lda + x.kb, k0, x.klen, st);
+    } else {
+      const MnOperand<T> o{A + x.kb * P.lda + x.m0, nullptr, P.lda, 0, x.klen, x.klen, 0, P.M - x.m0};
+      da.issue(o, k0, st);
+    }
+    if constexpr (LB == KMAJ) {
+      if (k0 == 0) db.template place<0, 4>(P.ldb, P.N - x.n0, 0);
+      db.template issue<0, 4>(B + x.n0 * P.ldb + x.kb, k0, x.klen, st + kTileBytes);
+    } else {
+      MnOperand<T> o;
+      o.p0 = B + x.kb * P.ldb + x.n0;
+      o.ld0 = P.ldb;
+      o.kseg = P.b_kseg - x.kb;
+      o.kval0 = min<int64_t>(P.b_kval0 - x.kb, x.klen);
+      o.p1 = B1 ? B1 + x.n0 : nullptr;
+      o.ld1 = P.ldb1;
+      o.kval1 = P.b_kval1;
+      o.cols = P.N - x.n0;
+      db.issue(o, k0, st + kTileBytes);
+    }
+  };
+  auto epilogue = [&](int i, f32x16 (&c)[4][2]) {
+    const Tile y = tile_of(i);
+    gemm_epilogue_q<T, MODE>(c, P, P.C32 + (int64_t)y.split * P.split_stride, y.m0, y.n0);
+  };
   zero_acc(acc);
-  const auto a = gemm_operand<T, LA>(A, P.lda, m0, P.M - m0, kb, klen);
-  if constexpr (LB == KMAJ) {
-    const KOperand<T> b{B + n0 * P.ldb + kb, P.ldb, P.N - n0};
-    mainloop_g<T, LA, LB>(acc, lds, a, b, klen);
-  } else {
-    const T* B1 = static_cast<const T*>(P.B1);
-    MnOperand<T> b;
-    b.p0 = B + kb * P.ldb + n0;
-    b.ld0 = P.ldb;
-    b.kseg = P.b_kseg - kb;
-    b.kval0 = min<int64_t>(P.b_kval0 - kb, klen);
-    b.p1 = B1 ? B1 + n0 : nullptr;
-    b.ld1 = P.ldb1;
-    b.kval1 = P.b_kval1;
-    b.cols = P.N - n0;
-    mainloop_g<T, LA, LB>(acc, lds, a, b, klen);
-  }
-  gemm_epilogue_q<T, MODE>(acc, P, P.C32 + (int64_t)split * P.split_stride, m0, n0);
+  pipeline_tiles<T, LA, LB, true, true, 8>(acc, lds, ntiles, nk, issue, epilogue);
 }
 
 // out[m][n] = sum over s of part[s][m][n] (fixed order), converted to T.
@@ -1038,9 +1081,23 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
   }
 
 // General GEMM: the (layout, layout, mode) combinations the library uses.
+// Persistent grid: one workgroup per CU (a 128 KiB-LDS workgroup fills a CU).
+inline int persistent_groups() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
 template <class T, int LA, int LB, int MODE>
 inline void gemm2_go(const GemmParams& P, hipStream_t s) {
-  const int grid = P.tiles_m * P.tiles_n * P.splits;
+  const int64_t total = (int64_t)P.tiles_m * P.tiles_n * P.splits;
+  const int grid = (int)(total < persistent_groups() ? total : persistent_groups());
   hipLaunchKernelGGL((k_gemm2<T, LA, LB, MODE>), dim3(grid), dim3(kThreads), 0, s, P);
 }
 #define ORDA_INSTANTIATE_GEMM2(T)                                                          \

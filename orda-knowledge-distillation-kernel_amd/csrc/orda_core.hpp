@@ -79,9 +79,9 @@ template <> struct Traits<float> {
 template <class T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
 template <class T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
 
-// Wave coordinates inside the workgroup tile.
-__device__ __forceinline__ int wave_m() { return (threadIdx.x >> 6) >> 2; }  // 0..1
-__device__ __forceinline__ int wave_n() { return (threadIdx.x >> 6) & 3; }   // 0..3
+// Wave coordinates inside the workgroup tile (wave-uniform: scalar registers).
+__device__ __forceinline__ int wave_m() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 2; }  // 0..1
+__device__ __forceinline__ int wave_n() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3; }   // 0..3
 
 // Row (within the wave's 128-row A slice) held by accumulator register r of
 // 32x32 block mb for this lane: 8*(r/4) + 4*(lane/32) + r%4 (+ 32*mb).
@@ -185,6 +185,14 @@ __device__ __forceinline__ void tile_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+// A lane-varying value the compiler cannot hoist out of a loop: epilogues
+// inside a persistent tile loop recompute their per-lane addresses from it
+// instead of keeping dozens of them live across the whole main loop.
+__device__ __forceinline__ int opaque_lane() {
+  int l = threadIdx.x & 63;
+  asm volatile("" : "+v"(l));
+  return l;
+}
 
 __device__ __forceinline__ void zero_acc(f32x16 (&acc)[4][2]) {
 #pragma unroll
@@ -218,46 +226,56 @@ struct MnOperand {
 
 enum Layout { KMAJ = 0, MNMAJ = 1 };
 
-// Per-thread DMA plan of one K-major tile of 256 rows: 4 chunks per thread,
-// chunk i of wave w covers rows (8 i + w) * 8 .. + 8 (i < 2: rows 0..127).
+// Per-thread DMA geometry of one K-major tile of 256 rows: 4 chunks per
+// thread, chunk i of wave w covers rows (8 i + w) * 8 .. + 8 (i < 2: rows
+// 0..127, i >= 2: rows 128..255).  place() fixes the row offsets of one
+// output tile (rows past the operand's end get the out-of-range offset);
+// issue() then only adds the K step, so a workgroup that moves from tile to
+// tile re-places once per tile, not once per step.
 template <class T>
 struct KDma {
-  uint32_t off[4];  // byte offset of the chunk from the row-0/k0 corner
-  int kc[4];        // first K element of the chunk
-  __device__ __forceinline__ void init(int64_t ld, int64_t rows, int row_base) {
-    const int w = wave_id(), l = threadIdx.x & 63;
+  int cb[4];        // byte offset of the chunk's K slice (logical chunk x 16)
+  uint32_t off[4];  // row offset + cb of the current tile, or kOob
+  __device__ __forceinline__ static int row_of(int i) {
+    return ((i * 8 + wave_id()) * 64 + (int)(threadIdx.x & 63)) >> 3;
+  }
+  __device__ __forceinline__ void init() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int pslot = (i * 8 + w) * 64 + l;
-      const int r = pslot >> 3;
-      const int c = (pslot & 7) ^ kswz(r);
-      kc[i] = c * (16 / (int)sizeof(T));
-      const int rr = r - row_base;
-      off[i] = (rr >= 0 && rr < rows) ? (uint32_t)((rr * ld) * (int64_t)sizeof(T) + c * 16) : kOob;
+      const int pslot = (i * 8 + wave_id()) * 64 + (int)(threadIdx.x & 63);
+      cb[i] = ((pslot & 7) ^ kswz(pslot >> 3)) * 16;
     }
   }
-  // chunks [i0, i1) of step k0 (K valid elements in all) to `tile`
+  // chunks [I0, I1): operand rows valid from tile row row_base up to `rows`
+  // of them, leading dimension ld (elements)
+  template <int I0, int I1>
+  __device__ __forceinline__ void place(int64_t ld, int64_t rows, int row_base) {
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+      const int rr = row_of(i) - row_base;
+      off[i] = rr < rows ? (uint32_t)rr * (uint32_t)(ld * (int64_t)sizeof(T)) + (uint32_t)cb[i] : kOob;
+    }
+  }
+  // chunks [I0, I1) of K step k0 to `tile`: p is the operand's row
+  // `row_base`, K its K extent (elements)
   template <int I0, int I1>
   __device__ __forceinline__ void issue(const T* p, int64_t k0, int64_t K, char* tile) const {
     const int w = wave_id();
     const auto rs = rsrc_of(p + k0);
-    const int64_t krem = K - k0;
+    const int64_t krem_bytes = (K - k0) * (int64_t)sizeof(T);
 #pragma unroll
-    for (int i = I0; i < I1; ++i) {
-      const uint32_t o = (kc[i] < krem) ? off[i] : kOob;
-      dma16(rs, o, tile + (i * 8 + w) * 1024);
-    }
+    for (int i = I0; i < I1; ++i) dma16(rs, cb[i] < krem_bytes ? off[i] : kOob, tile + (i * 8 + w) * 1024);
   }
 };
 
-// Per-thread DMA plan of one MN-major tile (BK rows of K x 256 columns).
+// Per-thread DMA geometry of one MN-major tile (BK rows of K x 256 columns).
 template <class T>
 struct MnDma {
   static constexpr int kChunks = 256 * (int)sizeof(T) / 16;   // per K row: 32 (16-bit), 64 (fp32)
   static constexpr int kRowsPerInst = 64 / kChunks;           // 2, 1
-  uint32_t coff[4];  // byte offset of the chunk's columns (kOob if past cols)
-  int kr[4];         // K row of the chunk inside the step
-  __device__ __forceinline__ void init(int64_t cols) {
+  int col[4];  // first column of the chunk
+  int dk[4];   // K row of the chunk relative to the wave's instruction row (0 or 1)
+  __device__ __forceinline__ void init() {
     const int w = wave_id(), l = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -265,11 +283,11 @@ struct MnDma {
       const int k = pslot / kChunks;
       const int pc = pslot % kChunks;
       const int c = sizeof(T) == 2 ? (pc ^ ((k & 3) << 2)) : (pc ^ ((k & 1) << 3));
-      kr[i] = k;
-      const int col = c * (16 / (int)sizeof(T));
-      coff[i] = col < cols ? (uint32_t)(col * (int)sizeof(T)) : kOob;
+      col[i] = c * (16 / (int)sizeof(T));
+      dk[i] = k - (i * 8 + w) * kRowsPerInst;
     }
   }
+  // K rows [k0, k0 + BK) of the operand, 256 columns from o's column 0
   __device__ __forceinline__ void issue(const MnOperand<T>& o, int64_t k0, char* tile) const {
     const int w = wave_id();
 #pragma unroll
@@ -278,10 +296,12 @@ struct MnDma {
       const int64_t krow = k0 + (i * 8 + w) * kRowsPerInst;
       const bool seg0 = krow < o.kseg;
       const T* base = seg0 ? o.p0 + krow * o.ld0 : o.p1 + (krow - o.kseg) * o.ld1;
-      const int64_t ld = seg0 ? o.ld0 : o.ld1;
+      const uint32_t ldb = (uint32_t)((seg0 ? o.ld0 : o.ld1) * (int64_t)sizeof(T));  // wave-uniform
       const int64_t kval = seg0 ? o.kval0 - krow : o.kval1 - (krow - o.kseg);  // valid rows from krow
-      const int dk = kr[i] - (i * 8 + w) * kRowsPerInst;                        // 0 or 1 (16-bit)
-      const uint32_t off = (dk < kval && coff[i] != kOob) ? (uint32_t)(dk * ld * (int64_t)sizeof(T)) + coff[i] : kOob;
+      // dk is 0 or 1: a select, not a multiply
+      const uint32_t off = (dk[i] < kval && col[i] < o.cols)
+                               ? (dk[i] ? ldb : 0u) + (uint32_t)(col[i] * (int)sizeof(T))
+                               : kOob;
       dma16(rsrc_of(base), off, tile + (i * 8 + w) * 1024);
     }
   }
@@ -372,8 +392,18 @@ __device__ __forceinline__ void wait_dma_steps(int n) {  // n = later steps allo
 // select which 128-row halves of the B tile take part (the fused loss
 // kernels put student tokens in half 0 and the same tokens' teacher rows in
 // half 1).  acc[mb][nb] += A[wm*128 + mb*32 ..] x B[nb*128 + wn*32 ..]^T.
-template <class T, int LA, int LB, bool H0, bool H1, int DMA_PER_STEP, class Issue>
-__device__ __forceinline__ void pipeline(f32x16 (&acc)[4][2], char* lds, int64_t K, const Issue& issue) {
+//
+// pipeline_tiles runs `ntiles` output tiles of `nk` K steps each as one
+// flattened sequence of steps: issue(g, stage) loads global step g (tile
+// g / nk, K step g % nk; called once per step, in increasing g), and after the last step of each tile epilogue(i,
+// acc) consumes the accumulators, which are then cleared for the next tile
+// (the last tile's sums are left in acc).  The first stages of
+// tile i+1 are loaded while tile i finishes and runs its epilogue, so a
+// persistent workgroup pays the pipeline's start-up latency once.  The
+// epilogue must not touch LDS (DPP and global memory only).
+template <class T, int LA, int LB, bool H0, bool H1, int DMA_PER_STEP, class Issue, class Epi>
+__device__ __forceinline__ void pipeline_tiles(f32x16 (&acc)[4][2], char* lds, int ntiles, int nk,
+                                               const Issue& issue, const Epi& epilogue) {
   using Tr = Traits<T>;
   using Frag = typename Tr::Frag;
   constexpr int BK = Tr::kBK;
@@ -381,13 +411,14 @@ __device__ __forceinline__ void pipeline(f32x16 (&acc)[4][2], char* lds, int64_t
   static_assert(KS % 2 == 0, "fragment double buffer parity");
   constexpr bool kMN = (LA == MNMAJ || LB == MNMAJ) && sizeof(T) == 2;
   const int wm = wave_m(), wn = wave_n();
-  const int nk = (int)((K + BK - 1) / BK);
+  const int total = ntiles * nk;
+  if (total <= 0) return;
   auto stage = [&](int step) { return lds + (step & 1) * (2 * kTileBytes); };
 
   tile_barrier();  // the previous user of LDS is done
   issue(0, stage(0));
-  if (nk > 1) issue(1, stage(1));
-  wait_dma_steps<DMA_PER_STEP>(nk > 1 ? 1 : 0);
+  if (total > 1) issue(1, stage(1));
+  wait_dma_steps<DMA_PER_STEP>(total > 1 ? 1 : 0);
   tile_barrier();
 
   Frag a[2][4], b[2][2];
@@ -410,8 +441,9 @@ __device__ __forceinline__ void pipeline(f32x16 (&acc)[4][2], char* lds, int64_t
       }
     }
   }
-  for (int kt = 0; kt < nk; ++kt) {
-    const char* as = stage(kt);
+  int kt = 0, tile = 0;
+  for (int g = 0; g < total; ++g) {
+    const char* as = stage(g);
     const char* bs = as + kTileBytes;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -421,18 +453,22 @@ __device__ __forceinline__ void pipeline(f32x16 (&acc)[4][2], char* lds, int64_t
         for (int mb = 0; mb < 4; ++mb) a[cur ^ 1][mb] = op_frag<T, LA>(as, wm * 128 + mb * 32, ks + 1);
         if (H0) b[cur ^ 1][0] = op_frag<T, LB>(bs, acc_col0(0, wn), ks + 1);
         if (H1) b[cur ^ 1][1] = op_frag<T, LB>(bs, acc_col0(1, wn), ks + 1);
-      } else if (kt + 1 < nk) {
-        // stage kt is fully read (its last fragments are in registers): wait
-        // for step kt+1, hand stage kt to step kt+2, prefetch step kt+1
+      } else if (g + 1 < total) {
+        // stage g is fully read (its last fragments are in registers): wait
+        // for step g+1, hand stage g to step g+2, prefetch step g+1 -- unless
+        // step g+1 starts a new tile: then its fragments are read after the
+        // epilogue, so they are not live across it
         wait_dma_steps<DMA_PER_STEP>(0);
         tile_barrier();
-        if (kt + 2 < nk) issue(kt + 2, stage(kt));
-        const char* an = stage(kt + 1);
-        const char* bn = an + kTileBytes;
+        if (g + 2 < total) issue(g + 2, stage(g));
+        if (kt + 1 < nk) {
+          const char* an = stage(g + 1);
+          const char* bn = an + kTileBytes;
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) a[cur ^ 1][mb] = op_frag<T, LA>(an, wm * 128 + mb * 32, 0);
-        if (H0) b[cur ^ 1][0] = op_frag<T, LB>(bn, acc_col0(0, wn), 0);
-        if (H1) b[cur ^ 1][1] = op_frag<T, LB>(bn, acc_col0(1, wn), 0);
+          for (int mb = 0; mb < 4; ++mb) a[cur ^ 1][mb] = op_frag<T, LA>(an, wm * 128 + mb * 32, 0);
+          if (H0) b[cur ^ 1][0] = op_frag<T, LB>(bn, acc_col0(0, wn), 0);
+          if (H1) b[cur ^ 1][1] = op_frag<T, LB>(bn, acc_col0(1, wn), 0);
+        }
       }
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
@@ -472,7 +508,42 @@ __device__ __forceinline__ void pipeline(f32x16 (&acc)[4][2], char* lds, int64_t
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    if (++kt == nk) {
+      epilogue(tile, acc);
+      if (g + 1 < total) zero_acc(acc);  // the last tile's sums stay for the caller
+      kt = 0;
+      ++tile;
+      {
+        // first fragments of the next tile (stage g+1 landed before the
+        // barrier; after the last tile this reads stale LDS, unused).  Always
+        // read, so the old fragments are provably dead across the epilogue.
+        const char* an = stage(g + 1);
+        const char* bn = an + kTileBytes;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) a[0][mb] = op_frag<T, LA>(an, wm * 128 + mb * 32, 0);
+        if (H0) b[0][0] = op_frag<T, LB>(bn, acc_col0(0, wn), 0);
+        if (H1) b[0][1] = op_frag<T, LB>(bn, acc_col0(1, wn), 0);
+        if constexpr (kMN) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if constexpr (LA == MNMAJ) {
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) lds_tie(a[0][mb]);
+          }
+          if constexpr (LB == MNMAJ) {
+            if (H0) lds_tie(b[0][0]);
+            if (H1) lds_tie(b[0][1]);
+          }
+        }
+      }
+    }
   }
+}
+
+// One output tile of nk = ceil(K / BK) steps (the accumulators keep the result).
+template <class T, int LA, int LB, bool H0, bool H1, int DMA_PER_STEP, class Issue>
+__device__ __forceinline__ void pipeline(f32x16 (&acc)[4][2], char* lds, int64_t K, const Issue& issue) {
+  const int nk = (int)((K + Traits<T>::kBK - 1) / Traits<T>::kBK);
+  pipeline_tiles<T, LA, LB, H0, H1, DMA_PER_STEP>(acc, lds, 1, nk, issue, [](int, f32x16 (&)[4][2]) {});
 }
 
 // Fused loss tiles: acc[mb][nb] += A[wm*128 + mb*32 ..] x Bnb[wn*32 ..]^T with
@@ -484,24 +555,12 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], char* lds,
                                          const T* B1, int64_t ldb1, int64_t b1_rows,
                                          int64_t K) {
   KDma<T> da, db;
-  da.init(lda, a_rows, 0);
+  da.init();
+  db.init();
+  da.template place<0, 4>(lda, a_rows, 0);
   // B chunks i = 0, 1 hold rows 0..127 (half 0), i = 2, 3 rows 128..255 (half 1)
-  db.init(H0 ? ldb0 : ldb1, 0, 0);
-  {
-    const int w = wave_id(), l = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int pslot = (i * 8 + w) * 64 + l;
-      const int r = pslot >> 3;
-      const int c = (pslot & 7) ^ kswz(r);
-      const bool half1 = i >= 2;
-      const int rr = half1 ? r - 128 : r;
-      const int64_t ld = half1 ? ldb1 : ldb0;
-      const int64_t rows = half1 ? b1_rows : b0_rows;
-      db.kc[i] = c * (16 / (int)sizeof(T));
-      db.off[i] = (rr < rows) ? (uint32_t)((rr * ld) * (int64_t)sizeof(T) + c * 16) : kOob;
-    }
-  }
+  if (H0) db.template place<0, 2>(ldb0, b0_rows, 0);
+  if (H1) db.template place<2, 4>(ldb1, b1_rows, 128);
   constexpr int kDma = 4 + (H0 ? 2 : 0) + (H1 ? 2 : 0);
   auto issue = [&](int step, char* st) {
     const int64_t k0 = (int64_t)step * Traits<T>::kBK;
@@ -512,6 +571,25 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[4][2], char* lds,
   pipeline<T, KMAJ, KMAJ, H0, H1, kDma>(acc, lds, K, issue);
 }
 
+// Issue one K step of a general-GEMM operand: K-major (KOperand, 256 rows
+// from p) or MN-major (MnOperand, 256 columns).
+template <class T>
+__device__ __forceinline__ void place_operand(KDma<T>& d, const KOperand<T>& o) {
+  d.template place<0, 4>(o.ld, o.rows, 0);
+}
+template <class T>
+__device__ __forceinline__ void place_operand(MnDma<T>&, const MnOperand<T>&) {}
+template <class T>
+__device__ __forceinline__ void issue_operand(const KDma<T>& d, const KOperand<T>& o, int64_t k0, int64_t K,
+                                              char* tile) {
+  d.template issue<0, 4>(o.p, k0, K, tile);
+}
+template <class T>
+__device__ __forceinline__ void issue_operand(const MnDma<T>& d, const MnOperand<T>& o, int64_t k0, int64_t,
+                                              char* tile) {
+  d.issue(o, k0, tile);
+}
+
 // General GEMM tile: A (256 rows) and B (256 rows) each K-major (KOperand)
 // or MN-major (MnOperand, 256 columns).
 template <class T, int LA, int LB, class OA, class OB>
@@ -520,14 +598,14 @@ __device__ __forceinline__ void mainloop_g(f32x16 (&acc)[4][2], char* lds, const
   using DB = typename std::conditional<LB == KMAJ, KDma<T>, MnDma<T>>::type;
   DA da;
   DB db;
-  if constexpr (LA == KMAJ) da.init(A.ld, A.rows, 0); else da.init(A.cols);
-  if constexpr (LB == KMAJ) db.init(B.ld, B.rows, 0); else db.init(B.cols);
+  da.init();
+  db.init();
+  place_operand(da, A);
+  place_operand(db, B);
   auto issue = [&](int step, char* st) {
     const int64_t k0 = (int64_t)step * Traits<T>::kBK;
-    if constexpr (LA == KMAJ) da.template issue<0, 4>(A.p, k0, K, st);
-    else da.issue(A, k0, st);
-    if constexpr (LB == KMAJ) db.template issue<0, 4>(B.p, k0, K, st + kTileBytes);
-    else db.issue(B, k0, st + kTileBytes);
+    issue_operand(da, A, k0, K, st);
+    issue_operand(db, B, k0, K, st + kTileBytes);
   };
   pipeline<T, LA, LB, true, true, 8>(acc, lds, K, issue);
 }
