@@ -4,6 +4,7 @@
 
 #include "launch.hpp"
 #include "orda_core.hpp"
+#include "ring4.hpp"
 
 namespace orda {
 
@@ -779,6 +780,121 @@ __global__ __launch_bounds__(kThreads) void k_gemm2(GemmParams P) {
   pipeline_tiles<T, LA, LB, true, true, 8>(acc, lds, ntiles, nk, issue, epilogue);
 }
 
+// C[M x N] (= or +=) A B^T with A [M x K] and B [N x K] both K-major, 16-bit,
+// on the four-wave ring engine (pipeline4): persistent, workgroup b (in XCD
+// order) owns tiles b, b + grid, ... in band order (8 row tiles wide).  The
+// MFMAs run swapped (B x A^T), so each lane holds four consecutive columns of
+// one C row and stores them with one 8-byte store.  MODE: GEMM_STORE (C = in
+// T) or GEMM_ACC_T (C += in T, fp32 sum rounded once).  Contract as k_gemm2,
+// plus K > 64.
+template <class T, int MODE>
+__global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
+  __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
+  Acc4 acc;
+  zero_acc4(acc);
+  const int tiles = P.tiles_m * P.tiles_n;
+  const int grid = gridDim.x;
+  const int b = xcd_order(blockIdx.x, grid);
+  const int ntiles = b < tiles ? (tiles - 1 - b) / grid + 1 : 0;
+  const T* A = static_cast<const T*>(P.A);
+  const T* B = static_cast<const T*>(P.B);
+  struct TI {
+    int m0, n0;
+    KOp4 a, b;
+  };
+  auto tile_info = [&](int i) {
+    const int t = b + (i < ntiles ? i : 0) * grid;
+    constexpr int G = 8;
+    const int band = t / (G * P.tiles_n);
+    const int first_m = band * G;
+    const int gm = min(P.tiles_m - first_m, G);
+    const int rem = t % (G * P.tiles_n);
+    TI x;
+    x.m0 = (first_m + rem % gm) * 256;
+    x.n0 = (rem / gm) * 256;
+    x.a = kop4(A + (int64_t)x.m0 * P.lda, P.lda, P.M - x.m0);
+    x.b = kop4(B + (int64_t)x.n0 * P.ldb, P.ldb, P.N - x.n0);
+    return x;
+  };
+  auto opnd = [](const TI& x, int op) { return op == 0 ? x.a : x.b; };
+  auto epilogue = [&](int, const TI& x, Acc4& c) {
+    const int lane = opaque_lane();
+    const int wm = w4_m(), wn = w4_n();
+    const int64_t ldc = P.ldc;
+    const int mlim = (int)min<int64_t>(P.M - x.m0, 256), nlim = (int)min<int64_t>(P.N - x.n0, 256);
+    T* C = static_cast<T*>(P.C) + (int64_t)x.m0 * ldc + x.n0;
+    const int cl = wn * 64 + (lane >> 5) * 4;  // tile column of this lane's group 0, block 0
+    auto col = [&](int nb, int g) { return (nb >> 1) * 128 + (nb & 1) * 32 + g * 8; };
+    if (mlim == 256 && nlim == 256) {
+      // interior tile; for GEMM_ACC_T the reads of C for two row blocks go
+      // out before the first add, so one memory latency covers 32 groups
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        uint2 cv[2][4][4];
+        if constexpr (MODE == GEMM_ACC_T) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const T* rp = C + (int64_t)(wm * 128 + (2 * hh + j) * 32 + (lane & 31)) * ldc + cl;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) cv[j][nb][g] = *reinterpret_cast<const uint2*>(rp + col(nb, g));
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int mb = 2 * hh + j;
+          T* rp = C + (int64_t)(wm * 128 + mb * 32 + (lane & 31)) * ldc + cl;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              float o[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
+              if constexpr (MODE == GEMM_ACC_T) {
+                union { T e[4]; uint2 u; } v;
+                v.u = cv[j][nb][g];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
+              }
+              store4(rp + col(nb, g), o, true, 4);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+      }
+      return;
+    }
+    // edge tile: rows past M and columns past N are skipped
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int mm = wm * 128 + mb * 32 + (lane & 31);
+      T* rp = C + (int64_t)mm * ldc + cl;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
+          const int rem = nlim - (cl + col(nb, g));
+          const int cnt = rem <= 0 ? 0 : (rem >= 4 ? 4 : rem);
+          if (mm < mlim && cnt > 0) {
+            if constexpr (MODE == GEMM_ACC_T) {
+              float cvf[4];
+              load4(rp + col(nb, g), cvf, cnt == 4, cnt);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o[e] += cvf[e];
+            }
+            store4(rp + col(nb, g), o, cnt == 4, cnt);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+  };
+  pipeline4<T, true, true, true>(acc, lds, ntiles, P.K, P.lda, P.ldb, tile_info, opnd, epilogue);
+}
+
 // out[m][n] = sum over s of part[s][m][n] (fixed order), converted to T.
 // Thread: 4 consecutive columns.  part has leading dimension N (dense),
 // N a multiple of 4.
@@ -1098,6 +1214,12 @@ template <class T, int LA, int LB, int MODE>
 inline void gemm2_go(const GemmParams& P, hipStream_t s) {
   const int64_t total = (int64_t)P.tiles_m * P.tiles_n * P.splits;
   const int grid = (int)(total < persistent_groups() ? total : persistent_groups());
+  if constexpr (sizeof(T) == 2 && LA == KMAJ && LB == KMAJ && (MODE == GEMM_STORE || MODE == GEMM_ACC_T)) {
+    if (P.splits == 1 && P.K > 64) {  // the ring engine (four waves, 160 KiB LDS)
+      hipLaunchKernelGGL((k_gemm4<T, MODE>), dim3(grid), dim3(kThreads4), 0, s, P);
+      return;
+    }
+  }
   hipLaunchKernelGGL((k_gemm2<T, LA, LB, MODE>), dim3(grid), dim3(kThreads), 0, s, P);
 }
 #define ORDA_INSTANTIATE_GEMM2(T)                                                          \

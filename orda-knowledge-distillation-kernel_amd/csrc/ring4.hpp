@@ -1,0 +1,291 @@
+// Four-wave ring engine for 16-bit operands (bf16, f16) on gfx950.
+//
+// Workgroup: 256 threads = 4 waves, one per SIMD.  Output tile 256 x 256,
+// wave tile 128 x 128 = 4 x 4 blocks of 32x32x16 MFMAs whose 256 fp32
+// accumulators live in AGPRs (one wave per SIMD may use all 512 registers).
+// Compared with eight waves of 128 x 64, each wave reads a third fewer LDS
+// bytes per MFMA.
+//
+// K advances in steps of 64.  A step's two operand tiles (256 rows x 128 B,
+// K-major, the same swizzled layout as the two-stage engine) sit in a ring of
+// five 32 KiB slots: slot j % 5 holds operand j % 2 of global step j / 2.  A
+// step runs as two halves of K = 32:
+//   half 0: fragment reads of its own second half, interleaved with the DMA of
+//           operand A of step g + 2 (the slot B of step g - 1 used), under the
+//           MFMAs of its first half;
+//   wait for step g + 1's DMA, barrier;
+//   half 1: fragment reads of step g + 1's first half, interleaved with the
+//           DMA of operand B of step g + 2 (the slot A of step g used), under
+//           the MFMAs of its second half.
+// So the loads are spread evenly over the step (eight 16-byte DMAs per thread
+// per half), each has one to one and a half steps to land, and every
+// fragment read sits between MFMAs.  The reads and DMAs are written in the
+// order they should issue (read, DMA, read, ...): the compiler cannot tell the
+// LDS slots apart, so it keeps LDS reads and DMA writes in program order, and
+// the MFMAs are then placed between them by sched_group_barrier.
+//
+// The step sequence is flattened over the output tiles a workgroup owns
+// (persistent kernels): the next tile's first steps load while the current
+// tile finishes, and epilogue(tile, acc) runs after each tile's last step.
+#pragma once
+#include "orda_core.hpp"
+
+namespace orda {
+
+constexpr int kThreads4 = 256;
+constexpr int kRing = 5;
+constexpr int kLds4Bytes = kRing * kTileBytes;  // 160 KiB
+
+typedef f32x16 Acc4[4][4];
+
+__device__ __forceinline__ void zero_acc4(Acc4& acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+}
+
+// Accumulator element -> VGPR at this point of the program.  Vector ALU
+// instructions cannot read AGPRs, so an epilogue needs copies; written as
+// volatile assembly (and fenced by the caller per group of four), the copies
+// cannot all be hoisted ahead of the first store, which would need 256 VGPRs.
+__device__ __forceinline__ float acc_get(const f32x16& v, int r) {
+  float x;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(v[r]));
+  return x;
+}
+
+// Wave coordinates: rows wm * 128 .. + 127 of A; B row (output column) of
+// block nb: blocks 0, 1 in B rows 0..127 (half 0), blocks 2, 3 in 128..255.
+__device__ __forceinline__ int w4_m() { return wave_id() >> 1; }
+__device__ __forceinline__ int w4_n() { return wave_id() & 1; }
+__device__ __forceinline__ int col4(int nb, int wn) { return (nb >> 1) * 128 + wn * 64 + (nb & 1) * 32; }
+
+// Per-thread DMA geometry of one 256-row K-major operand tile with 256
+// threads: chunk q (0..7) of wave w covers tile row (q % 4) * 32 + w * 8 +
+// lane / 8 of half q / 4 (rows 0..127, 128..255), at LDS byte (q * 4 + w) *
+// 1024 + lane * 16.  The swizzle of those rows does not depend on q, so one
+// chunk offset serves all eight.
+struct Dma4 {
+  uint32_t row0;  // tile row of chunk 0 within its half: w * 8 + lane / 8
+  uint32_t cb;    // byte offset of the thread's 16 bytes within its row
+  __device__ __forceinline__ void init() {
+    row0 = (uint32_t)(wave_id() * 8 + (int)((threadIdx.x & 63) >> 3));
+    cb = (uint32_t)((((int)threadIdx.x & 7) ^ kswz((int)row0)) * 16);
+  }
+};
+
+// A K-major operand tile (256 rows from its first row, K from column 0):
+// per half h (rows h * 128 ..), a buffer resource at the half's first row
+// whose record count ends at its last valid row (the row pitch is per
+// operand, not per tile).  A K step's DMA reads row r, 16 bytes at column byte c, at offset
+// r * ldb + c (vector) + k0 bytes (scalar): the hardware's range check covers
+// both, and c + k0 < ldb inside K, so rows past the record count read zeros.
+struct KOp4 {
+  __amdgpu_buffer_rsrc_t r[2];
+};
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_rows(const void* base, int64_t rows, uint32_t ldb) {
+  const int64_t n = rows <= 0 ? 0 : (rows >= 128 ? 128 : rows);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)(n * ldb), 0x00020000);
+}
+// p: the tile's first row (K column 0); rows: valid rows from there; ld: row
+// pitch (elements)
+template <class T>
+__device__ __forceinline__ KOp4 kop4(const T* p, int64_t ld, int64_t rows) {
+  KOp4 o;
+  const uint32_t ldb = (uint32_t)(ld * (int64_t)sizeof(T));
+  o.r[0] = rsrc_rows(p, rows, ldb);
+  o.r[1] = rsrc_rows(p + 128 * ld, rows - 128, ldb);
+  return o;
+}
+// Two halves from separate operands of the same row pitch (a fused B: rows
+// 0..127 from p0, rows 128..255 from p1), rows0 / rows1 valid rows of each.
+template <class T>
+__device__ __forceinline__ KOp4 kop4_split(const T* p0, int64_t rows0, const T* p1, int64_t rows1, int64_t ld) {
+  KOp4 o;
+  const uint32_t ldb = (uint32_t)(ld * (int64_t)sizeof(T));
+  o.r[0] = rsrc_rows(p0, rows0, ldb);
+  o.r[1] = rsrc_rows(p1, rows1, ldb);
+  return o;
+}
+
+// Barrier that no instruction crosses in the scheduler (MFMAs included).
+__device__ __forceinline__ void bar4() {
+  __builtin_amdgcn_sched_barrier(0);
+  tile_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <class T>
+__device__ __forceinline__ typename Traits<T>::Frag frag4(const char* tile, int row0, int ks, int lane) {
+  const int r = row0 + (lane & 31);
+  const int c = ks * 2 + (lane >> 5);
+  return *reinterpret_cast<const typename Traits<T>::Frag*>(tile + r * 128 + ((c ^ kswz(r)) << 4));
+}
+
+// Runs ntiles x nk steps (nk >= 2).  tile_info(i) -> TI describes output
+// tile i (any caller type; called once per tile for the tile after the
+// current one, i may equal ntiles); opnd(ti, op) -> KOp4 gives operand op
+// (0: A, 1: B) of that tile (selected per step, so it must not branch on
+// per-lane values); K: the operands' K extent (elements); lda, ldb: their
+// row pitches (elements).  epilogue(i, ti, acc) runs after tile i's last step and
+// must not touch LDS.  H0 / H1: which halves of B (and which accumulator
+// columns: blocks 0, 1 / 2, 3) are live.
+//
+// Accumulator layout (block acc[mb][nb], element r, lane l): with SWAP false
+// the MFMA computes A x B^T, so r holds A row wm * 128 + mb * 32 + acc_row
+// (= 8 (r / 4) + 4 (l / 32) + r % 4) and B row col4(nb, wn) + l % 32; with
+// SWAP true it computes B x A^T, so r holds B row col4(nb, wn) + acc_row and
+// A row wm * 128 + mb * 32 + l % 32 -- four consecutive r are then four
+// consecutive output columns of one row-major C row (8-byte stores).
+template <class T, bool H0, bool H1, bool SWAP, class TileInfo, class Opnd, class Epi>
+__device__ __forceinline__ void pipeline4(Acc4& acc, char* lds, int ntiles, int64_t K, int64_t lda, int64_t ldb,
+                                          const TileInfo& tile_info, const Opnd& opnd, const Epi& epilogue) {
+  static_assert(sizeof(T) == 2, "16-bit operands");
+  using Tr = Traits<T>;
+  using Frag = typename Tr::Frag;
+  const int w = wave_id(), wm = w >> 1, wn = w & 1;
+  const int nk = (int)((K + 63) / 64);
+  const int kbytes = (int)(K * (int64_t)sizeof(T));
+  if (ntiles <= 0 || nk < 2) return;
+  Dma4 dg;
+  dg.init();
+  auto mod5 = [](int j) { return j >= kRing ? j - kRing : j; };  // j < 10
+  auto slot = [&](int j) { return lds + j * kTileBytes; };       // j < 5
+  auto live_b = [](int nb) { return nb < 2 ? H0 : H1; };
+  auto live_dma = [](int op, int q) { return op == 0 || (q < 4 ? H0 : H1); };
+  // one operand step: the thread's vector offset per half (past every
+  // record when K is exhausted at its chunk) and the step's K byte offset
+  const uint32_t ldbs[2] = {(uint32_t)(lda * (int64_t)sizeof(T)), (uint32_t)(ldb * (int64_t)sizeof(T))};
+  struct Step {
+    KOp4 o;
+    uint32_t ldb, vb, k0;
+  };
+  auto prep = [&](const KOp4& o, int op, int kd, bool live) {
+    Step st;
+    st.o = o;
+    st.ldb = ldbs[op];
+    st.k0 = (uint32_t)kd * 128u;
+    const int krem = live ? kbytes - (int)st.k0 : 0;
+    const bool kok = (int)dg.cb < krem;
+    st.vb = kok ? dg.row0 * st.ldb + dg.cb : kOob;
+    return st;
+  };
+  auto chunk = [&](const Step& st, int q, char* sb) {
+    const int h = q >> 2;
+    const uint32_t so = (uint32_t)(q & 3) * 32u * st.ldb + st.k0;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(st.o.r[h], (__attribute__((address_space(3))) void*)(sb + (q * 4 + w) * 1024),
+                                             16, st.vb, so, 0, 0);
+  };
+  constexpr int kNB = (H0 ? 2 : 0) + (H1 ? 2 : 0);  // live B blocks
+  constexpr int kMfmaHalf = 2 * 4 * kNB;            // MFMAs per half step
+
+  Frag fa[2][2][4], fb[2][2][4];
+  // fragment reads of one half step from slots (ja, jb) into buffer buf,
+  // interleaved with one operand step's DMA into slot jd (program order per
+  // q: A read, DMA, B read)
+  auto reads_dma = [&](int buf, int ja, int jb, int hf, const Step& st, int op, int jd) {
+    char* sb = slot(jd);
+    const char* as = slot(ja);
+    const char* bs = slot(jb);
+    const int lane = opaque_lane();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int h = q >> 2, x = q & 3, ks = hf * 2 + h;
+      fa[buf][h][x] = frag4<T>(as, wm * 128 + x * 32, ks, lane);
+      if (live_dma(op, q)) chunk(st, q, sb);
+      if (live_b(x)) fb[buf][h][x] = frag4<T>(bs, col4(x, wn), ks, lane);
+    }
+  };
+  auto mfma_half = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          if (live_b(nb)) {
+            if constexpr (SWAP) acc[mb][nb] = Tr::mma(fb[buf][h][nb], fa[buf][h][mb], acc[mb][nb]);
+            else acc[mb][nb] = Tr::mma(fa[buf][h][mb], fb[buf][h][nb], acc[mb][nb]);
+          }
+  };
+  // MFMA placement: per q, [A read] M [DMA] M [B read] M..
+  auto schedule = [&](int op) {
+    constexpr int kPerQ = kMfmaHalf / 8;  // 4 (both halves of B) or 2
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (live_dma(op, q)) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (live_b(q & 3)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (kPerQ > 2) __builtin_amdgcn_sched_group_barrier(0x008, kPerQ - 2, 0);
+    }
+  };
+
+  auto cur = tile_info(0);
+  auto nxt = tile_info(1);
+  // prologue: steps 0 and 1 (both in tile 0) in flight, step 0 landed, its
+  // first half read
+  {
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int op = 0; op < 2; ++op) {
+        const Step st = prep(opnd(cur, op), op, g, true);
+        char* sb = slot(2 * g + op);
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (live_dma(op, q)) chunk(st, q, sb);
+      }
+    constexpr int kStep1 = 8 + 4 * kNB / 2;  // DMAs of step 1 (A: 8, B: 4 per live half)
+    wait_vmem<kStep1>();
+    bar4();
+    const int lane = opaque_lane();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int h = q >> 2, x = q & 3;
+      fa[0][h][x] = frag4<T>(slot(0), wm * 128 + x * 32, h, lane);
+      if (live_b(x)) fb[0][h][x] = frag4<T>(slot(1), col4(x, wn), h, lane);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+
+  int j0 = 0;  // slot of operand A of the current step: (2 g) % 5
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const bool nxt_live = tile + 1 < ntiles;
+    for (int kt = 0; kt < nk; ++kt) {
+      // step g + 2: K step kt + 2 of this tile, or of the next one
+      const bool in_cur = kt + 2 < nk;
+      const int kd = in_cur ? kt + 2 : kt + 2 - nk;
+      const bool dlive = in_cur || nxt_live;
+      const int j1 = mod5(j0 + 1), j2 = mod5(j0 + 2), j3 = mod5(j0 + 3), j4 = mod5(j0 + 4);
+      // half 0: second-half fragments of step g, DMA of A(g + 2) into j4
+      reads_dma(1, j0, j1, 1, prep(in_cur ? opnd(cur, 0) : opnd(nxt, 0), 0, kd, dlive), 0, j4);
+      mfma_half(0);
+      schedule(0);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      wait_vmem<8>();  // step g + 1 landed (A of step g + 2 may be in flight)
+      bar4();
+      // half 1: first-half fragments of step g + 1, DMA of B(g + 2) into j0
+      reads_dma(0, j2, j3, 0, prep(in_cur ? opnd(cur, 1) : opnd(nxt, 1), 1, kd, dlive), 1, j0);
+      mfma_half(1);
+      schedule(1);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      j0 = j2;
+    }
+    epilogue(tile, cur, acc);
+    if (nxt_live) {
+      zero_acc4(acc);
+      cur = nxt;
+      nxt = tile_info(tile + 2);
+    }
+  }
+  wait_vmem<0>();  // the dead steps' DMAs: nothing may land after the waves end
+}
+
+}  // namespace orda
