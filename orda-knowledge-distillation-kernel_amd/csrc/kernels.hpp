@@ -109,11 +109,25 @@ __device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][2], char* lds, con
 }
 
 // ------------------------------------------------------------- scan kernel
+// Logit accessors for the scan epilogues: s(mb, r) / t(mb, r) = student /
+// teacher logit of the lane's token at accumulator row (mb, r) of the tile.
+struct AccPair2 {  // two-stage engine: acc[mb][0] student, acc[mb][1] teacher
+  const f32x16 (&a)[4][2];
+  __device__ __forceinline__ float s(int mb, int r) const { return a[mb][0][r]; }
+  __device__ __forceinline__ float t(int mb, int r) const { return a[mb][1][r]; }
+};
+struct AccPair4 {  // ring engine, the lane's token j: acc[mb][j] student, acc[mb][j + 2] teacher
+  const Acc4& a;
+  int j;
+  __device__ __forceinline__ float s(int mb, int r) const { return acc_get(a[mb][j], r); }
+  __device__ __forceinline__ float t(int mb, int r) const { return acc_get(a[mb][j + 2], r); }
+};
+
 // Phase 0: online softmax statistics of this lane's token over its 64
 // vocabulary rows of the tile.  Template flags remove work that the problem
 // does not need.
-template <bool HAS_T, int FAM, bool T1, bool MASK>
-__device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][2], int vlane0, int64_t vlimit,
+template <bool HAS_T, int FAM, bool T1, bool MASK, class AP>
+__device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0, int64_t vlimit,
                                           const FusedParams& P) {
   const float invT = P.invT;
   float tms = -kInf, tmt = -kInf, tmu0 = -kInf, tmu1 = -kInf, tmu2 = -kInf;
@@ -122,10 +136,10 @@ __device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][2]
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
-      const float xs = acc[mb][0][r];
+      const float xs = acc.s(mb, r);
       tms = fmaxf(tms, xs);
       if (HAS_T) {
-        const float xt = acc[mb][1][r];
+        const float xt = acc.t(mb, r);
         tmt = fmaxf(tmt, xt);
         if (FAM == FAM_POW) {
           tmu0 = fmaxf(tmu0, P.pa[0] * xt + P.pb[0] * xs);
@@ -185,13 +199,13 @@ __device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][2]
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
-      const float xs = acc[mb][0][r];
+      const float xs = acc.s(mb, r);
       const float es = fexp(xs - nms);
       S.ss += es;
       const float esT = T1 ? es : fexp((xs - nms) * invT);
       if (!T1) S.sst += esT;
       if (HAS_T) {
-        const float xt = acc[mb][1][r];
+        const float xt = acc.t(mb, r);
         const float et = fexp(xt - nmt);
         S.st += et;
         const float etT = T1 ? et : fexp((xt - nmt) * invT);
@@ -213,8 +227,8 @@ __device__ __forceinline__ void scan_tile(RowState& S, const f32x16 (&acc)[4][2]
 
 // Phase 1 (two-pass divergences): sums of terms of the normalised
 // probabilities, given the row log-normalisers from phase 0.
-template <int DIV, bool MASK>
-__device__ __forceinline__ void rowsum_tile(RowState& S, const f32x16 (&acc)[4][2], int vlane0, int64_t vlimit,
+template <int DIV, bool MASK, class AP>
+__device__ __forceinline__ void rowsum_tile(RowState& S, const AP& acc, int vlane0, int64_t vlimit,
                                             float lse_sT, float lse_tT, const FusedParams& P) {
   const float invT = P.invT;
   float s0 = 0.f, s1 = 0.f;
@@ -223,8 +237,8 @@ __device__ __forceinline__ void rowsum_tile(RowState& S, const f32x16 (&acc)[4][
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
-      const float lps = acc[mb][0][r] * invT - lse_sT;
-      const float lpt = acc[mb][1][r] * invT - lse_tT;
+      const float lps = acc.s(mb, r) * invT - lse_sT;
+      const float lpt = acc.t(mb, r) * invT - lse_tT;
       const float ps = fexp(lps), pt = fexp(lpt);
       if constexpr (DIV == DIV_JSD) {
         const float lm = logaddexp(P.log_beta + lpt, P.log_1m_beta + lps);
@@ -282,8 +296,8 @@ enum ScanVariant {
   SV_TVD = 9
 };
 
-template <int SV>
-__device__ __forceinline__ void scan_variant(RowState& S, const f32x16 (&acc)[4][2], int vlane0, int64_t vlimit,
+template <int SV, class AP>
+__device__ __forceinline__ void scan_variant(RowState& S, const AP& acc, int vlane0, int64_t vlimit,
                                              bool full, float lse_sT, float lse_tT, const FusedParams& P) {
   if constexpr (SV == SV_STUDENT) {
     if (full) scan_tile<false, FAM_NONE, true, false>(S, acc, vlane0, vlimit, P);
@@ -381,7 +395,7 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
     if constexpr (STORE) store_logits<T>(acc, P, v0, t0v);
     const int vlane0 = wm * 128 + (opaque_lane() >> 5) * 4;
     const int64_t vlimit = P.V - v0;
-    scan_variant<SV>(st, acc, vlane0, vlimit, vlimit >= 256, lse_sT, lse_tT, P);
+    scan_variant<SV>(st, AccPair2{acc}, vlane0, vlimit, vlimit >= 256, lse_sT, lse_tT, P);
   }
 
   // combine lane l with l^32, then the two waves sharing the tokens (wm 0/1)
@@ -410,6 +424,132 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
       const float* sv = reinterpret_cast<const float*>(&st);
 #pragma unroll
       for (int f = 0; f < kNStat; ++f) dst[(int64_t)f * P.N] = sv[f];
+    }
+  }
+}
+
+// Logits of a ring-engine tile to Lout[v][t] (see store_logits): block
+// acc[mb][nb] holds vocabulary rows wm * 128 + mb * 32 + acc_row and tokens
+// wn * 64 + (nb & 1) * 32 + lane % 32, student for nb < 2, teacher for nb >= 2.
+template <class T>
+__device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams& P, int64_t v0, int64_t t0) {
+  const int lane = opaque_lane();
+  const int wm = w4_m(), wn = w4_n();
+  const int q = lane & 3;
+  T* L = static_cast<T*>(P.Lout);
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    if (nb >= 2 && !P.store_t) break;
+    const int64_t tb = t0 + wn * 64 + (nb & 1) * 32 + (lane & 31) - q;  // first token of the quad
+    const int64_t nt = P.N - tb;
+    const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
+    const int64_t col = tb + (nb >= 2 ? P.tcolL : 0);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t v = v0 + wm * 128 + acc_row(mb, g * 4, lane) + q;
+        float x[4], o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = acc_get(acc[mb][nb], g * 4 + e);
+        quad_transpose(x, o);
+        if (v < P.V && ntok > 0) store4(L + v * P.ldL + col, o, ntok == 4, ntok);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  }
+}
+
+// k_scan on the four-wave ring engine, for 16-bit operands with the teacher
+// sharing W (TSRC_SHARED): the same workgroup -> (128 tokens, vocabulary
+// range) mapping and partial output.  The fused B operand (student hidden
+// rows t0.., then the teacher's) is fixed per workgroup; the vocabulary tiles
+// of the range run as one persistent ring (pipeline4, MFMAs not swapped), so
+// each lane holds two tokens: j = 0, 1 at blocks (j, j + 2).
+template <class T, int SV, bool STORE>
+__global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
+  __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
+  Acc4 acc;
+  zero_acc4(acc);
+  constexpr bool kPhase1 = SV >= SV_JSD;
+  const int lane = threadIdx.x & 63;
+  const int wm = w4_m(), wn = w4_n();
+  int tt, vr;
+  grouped_tile<4>(xcd_order(blockIdx.x, gridDim.x), P.n_ttiles, P.n_vranges, tt, vr);
+  const int64_t t0 = (int64_t)tt * 128;
+  const int vt_begin = vr * P.tiles_per_range;
+  const int ntiles = min(vt_begin + P.tiles_per_range, P.n_vtiles) - vt_begin;
+
+  RowState st[2];
+  int64_t tok[2];
+  float lse_sT[2] = {0.f, 0.f}, lse_tT[2] = {0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    state_init_fam(st[j], kPhase1 ? FAM_NONE : P.fam);
+    tok[j] = t0 + wn * 64 + j * 32 + (lane & 31);
+    if (kPhase1 && tok[j] < P.N) {
+      lse_sT[j] = P.rowp[1 * P.N + tok[j]];
+      lse_tT[j] = P.rowp[3 * P.N + tok[j]];
+    }
+  }
+  const T* W = static_cast<const T*>(P.W);
+  const T* hs = static_cast<const T*>(P.hs);
+  const T* ht = static_cast<const T*>(P.ht);
+  const KOp4 bop = kop4_split(hs + t0 * P.H, P.N - t0, ht + t0 * P.H, P.N - t0, P.H);
+  struct TI {
+    int v0;
+    KOp4 a;
+  };
+  auto tile_info = [&](int i) {
+    TI x;
+    x.v0 = (vt_begin + (i < ntiles ? i : 0)) * 256;
+    x.a = kop4(W + (int64_t)x.v0 * P.H, P.H, P.V - x.v0);
+    return x;
+  };
+  auto opnd = [&](const TI& x, int op) { return op == 0 ? x.a : bop; };
+  auto epilogue = [&](int, const TI& x, Acc4& c) {
+    if constexpr (STORE) store_logits4<T>(c, P, x.v0, t0);
+    const int vlane0 = wm * 128 + (opaque_lane() >> 5) * 4;
+    const int64_t vlimit = P.V - x.v0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      scan_variant<SV>(st[j], AccPair4{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+  };
+  pipeline4<T, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
+
+  // combine lane l with l^32 (other vocabulary rows of the same tokens), then
+  // the two waves sharing the tokens (wm 0 / 1)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const RowState o = shfl32(st[j]);
+    merge_any<kPhase1>(st[j], o, P);
+  }
+  __syncthreads();
+  float* xch = reinterpret_cast<float*>(lds);  // [wn][j][kNStat][32]
+  if (wm == 1 && lane < 32) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float* d = xch + ((wn * 2 + j) * kNStat) * 32 + lane;
+      const float* sv = reinterpret_cast<const float*>(&st[j]);
+#pragma unroll
+      for (int f = 0; f < kNStat; ++f) d[f * 32] = sv[f];
+    }
+  }
+  __syncthreads();
+  if (wm == 0 && lane < 32) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      RowState o;
+      float* od = reinterpret_cast<float*>(&o);
+      const float* sv = xch + ((wn * 2 + j) * kNStat) * 32 + lane;
+#pragma unroll
+      for (int f = 0; f < kNStat; ++f) od[f] = sv[f * 32];
+      merge_any<kPhase1>(st[j], o, P);
+      if (tok[j] < P.N) {
+        float* dst = P.partial + (int64_t)vr * kNStat * P.N + tok[j];
+        const float* v = reinterpret_cast<const float*>(&st[j]);
+#pragma unroll
+        for (int f = 0; f < kNStat; ++f) dst[(int64_t)f * P.N] = v[f];
+      }
     }
   }
 }
@@ -1102,8 +1242,22 @@ hipError_t launch_scan_t(const FusedParams& P, int grid, hipStream_t s);
 template <class T>
 hipError_t launch_dl_t(const FusedParams& P, int grid, hipStream_t s);
 
-#define ORDA_SCAN_CASE(T, SV) \
-  case SV: hipLaunchKernelGGL((k_scan<T, SV>), dim3(grid), dim3(kThreads), 0, s, P); break;
+// The ring engine takes the 16-bit tied problems (K > 64); the rest run on
+// the two-stage engine.
+template <class T>
+inline bool scan_on_ring(const FusedParams& P) {
+  return sizeof(T) == 2 && P.tsrc == TSRC_SHARED && P.H > 64;
+}
+#define ORDA_SCAN_CASE(T, SV)                                                                    \
+  case SV:                                                                                       \
+    if constexpr (sizeof(T) == 2) {                                                              \
+      if (scan_on_ring<T>(P)) {                                                                  \
+        hipLaunchKernelGGL((k_scan4<T, SV, false>), dim3(grid), dim3(kThreads4), 0, s, P);       \
+        break;                                                                                   \
+      }                                                                                          \
+    }                                                                                            \
+    hipLaunchKernelGGL((k_scan<T, SV>), dim3(grid), dim3(kThreads), 0, s, P);                    \
+    break;
 #define ORDA_DL_CASE(T, D) \
   case D: hipLaunchKernelGGL((k_dl<T, D, false>), dim3(grid), dim3(kThreads), 0, s, P); break;
 
@@ -1179,8 +1333,16 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
 }
 
 // Materialised path: scan variants with the logits store (phase 0 only).
-#define ORDA_SCANST_CASE(T, SV) \
-  case SV: hipLaunchKernelGGL((k_scan<T, SV, true>), dim3(grid), dim3(kThreads), 0, s, P); break;
+#define ORDA_SCANST_CASE(T, SV)                                                                  \
+  case SV:                                                                                       \
+    if constexpr (sizeof(T) == 2) {                                                              \
+      if (scan_on_ring<T>(P)) {                                                                  \
+        hipLaunchKernelGGL((k_scan4<T, SV, true>), dim3(grid), dim3(kThreads4), 0, s, P);        \
+        break;                                                                                   \
+      }                                                                                          \
+    }                                                                                            \
+    hipLaunchKernelGGL((k_scan<T, SV, true>), dim3(grid), dim3(kThreads), 0, s, P);              \
+    break;
 #define ORDA_INSTANTIATE_SCAN_STORE(T)                                                     \
   template <> hipError_t launch_scan_store<T>(const FusedParams& P, int grid, hipStream_t s) { \
     if (P.phase != 0) return hipErrorInvalidValue;                                         \
