@@ -514,7 +514,7 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
     for (int j = 0; j < 2; ++j)
       scan_variant<SV>(st[j], AccPair4{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
   };
-  pipeline4<T, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
+  pipeline4<T, KMAJ, KMAJ, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
 
   // combine lane l with l^32 (other vocabulary rows of the same tokens), then
   // the two waves sharing the tokens (wm 0 / 1)
@@ -920,40 +920,54 @@ __global__ __launch_bounds__(kThreads) void k_gemm2(GemmParams P) {
   pipeline_tiles<T, LA, LB, true, true, 8>(acc, lds, ntiles, nk, issue, epilogue);
 }
 
-// C[M x N] (= or +=) A B^T with A [M x K] and B [N x K] both K-major, 16-bit,
-// on the four-wave ring engine (pipeline4): persistent, workgroup b (in XCD
-// order) owns tiles b, b + grid, ... in band order (8 row tiles wide).  The
+// C[M x N] (mode) A B^T for 16-bit operands on the four-wave ring engine
+// (pipeline4): A and B both K-major (MODE GEMM_STORE: C = in T, GEMM_ACC_T:
+// C += in T, the fp32 sum rounded once; one split), or both MN-major (GEMM_STORE,
+// or GEMM_SPLIT: split s covers K rows [s * k_per_split, ...) and writes its
+// fp32 partial).  Persistent: workgroup b (in XCD order) owns work items b,
+// b + grid, ... (split-major, tiles in band order, 8 row tiles wide).  The
 // MFMAs run swapped (B x A^T), so each lane holds four consecutive columns of
-// one C row and stores them with one 8-byte store.  MODE: GEMM_STORE (C = in
-// T) or GEMM_ACC_T (C += in T, fp32 sum rounded once).  Contract as k_gemm2,
-// plus K > 64.
-template <class T, int MODE>
+// one C row and stores them with one 8-byte (16-byte for fp32) store.
+// Contract as k_gemm2, plus k_per_split > 64 and, for MN-major operands,
+// k_per_split * ld * sizeof(T) < 2^31.
+template <class T, int LA, int LB, int MODE>
 __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
+  static_assert(LA == LB, "both operands K-major or both MN-major");
   __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
   Acc4 acc;
   zero_acc4(acc);
   const int tiles = P.tiles_m * P.tiles_n;
+  const int total = tiles * P.splits;
   const int grid = gridDim.x;
   const int b = xcd_order(blockIdx.x, grid);
-  const int ntiles = b < tiles ? (tiles - 1 - b) / grid + 1 : 0;
+  const int ntiles = b < total ? (total - 1 - b) / grid + 1 : 0;
   const T* A = static_cast<const T*>(P.A);
   const T* B = static_cast<const T*>(P.B);
   struct TI {
-    int m0, n0;
+    int m0, n0, split;
     KOp4 a, b;
   };
   auto tile_info = [&](int i) {
-    const int t = b + (i < ntiles ? i : 0) * grid;
+    const int t_all = b + (i < ntiles ? i : 0) * grid;
+    TI x;
+    x.split = t_all / tiles;
+    const int t = t_all - x.split * tiles;
     constexpr int G = 8;
     const int band = t / (G * P.tiles_n);
     const int first_m = band * G;
     const int gm = min(P.tiles_m - first_m, G);
     const int rem = t % (G * P.tiles_n);
-    TI x;
     x.m0 = (first_m + rem % gm) * 256;
     x.n0 = (rem / gm) * 256;
-    x.a = kop4(A + (int64_t)x.m0 * P.lda, P.lda, P.M - x.m0);
-    x.b = kop4(B + (int64_t)x.n0 * P.ldb, P.ldb, P.N - x.n0);
+    const int64_t kb = (int64_t)x.split * P.k_per_split;
+    if constexpr (LA == KMAJ) {
+      x.a = kop4(A + (int64_t)x.m0 * P.lda + kb, P.lda, P.M - x.m0);
+      x.b = kop4(B + (int64_t)x.n0 * P.ldb + kb, P.ldb, P.N - x.n0);
+    } else {
+      const int64_t klen = min<int64_t>(P.K - kb, P.k_per_split);
+      x.a = kop4_mn(A + kb * P.lda + x.m0, P.lda, klen, P.M - x.m0);
+      x.b = kop4_mn(B + kb * P.ldb + x.n0, P.ldb, klen, P.N - x.n0);
+    }
     return x;
   };
   auto opnd = [](const TI& x, int op) { return op == 0 ? x.a : x.b; };
@@ -962,9 +976,30 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
     const int wm = w4_m(), wn = w4_n();
     const int64_t ldc = P.ldc;
     const int mlim = (int)min<int64_t>(P.M - x.m0, 256), nlim = (int)min<int64_t>(P.N - x.n0, 256);
-    T* C = static_cast<T*>(P.C) + (int64_t)x.m0 * ldc + x.n0;
     const int cl = wn * 64 + (lane >> 5) * 4;  // tile column of this lane's group 0, block 0
     auto col = [&](int nb, int g) { return (nb >> 1) * 128 + (nb & 1) * 32 + g * 8; };
+    if constexpr (MODE == GEMM_SPLIT) {
+      float* D = P.C32 + (int64_t)x.split * P.split_stride + (int64_t)x.m0 * ldc + x.n0;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const int mm = wm * 128 + mb * 32 + (lane & 31);
+        float* rp = D + (int64_t)mm * ldc + cl;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
+            const int rem = nlim - (cl + col(nb, g));
+            const int cnt = rem <= 0 ? 0 : (rem >= 4 ? 4 : rem);
+            if (mm < mlim && cnt > 0) store4(rp + col(nb, g), o, cnt == 4, cnt);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      }
+      return;
+    }
+    T* C = static_cast<T*>(P.C) + (int64_t)x.m0 * ldc + x.n0;
     if (mlim == 256 && nlim == 256) {
       // interior tile; for GEMM_ACC_T the reads of C for two row blocks go
       // out before the first add, so one memory latency covers 32 groups
@@ -1032,7 +1067,8 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
         }
     }
   };
-  pipeline4<T, true, true, true>(acc, lds, ntiles, P.K, P.lda, P.ldb, tile_info, opnd, epilogue);
+  pipeline4<T, LA, LB, true, true, true>(acc, lds, ntiles, P.k_per_split, P.lda, P.ldb, tile_info, opnd,
+                                         epilogue);
 }
 
 // out[m][n] = sum over s of part[s][m][n] (fixed order), converted to T.
@@ -1376,9 +1412,18 @@ template <class T, int LA, int LB, int MODE>
 inline void gemm2_go(const GemmParams& P, hipStream_t s) {
   const int64_t total = (int64_t)P.tiles_m * P.tiles_n * P.splits;
   const int grid = (int)(total < persistent_groups() ? total : persistent_groups());
+  // the ring engine (four waves, 160 KiB LDS) for the 16-bit K/K and MN/MN
+  // GEMMs it covers
   if constexpr (sizeof(T) == 2 && LA == KMAJ && LB == KMAJ && (MODE == GEMM_STORE || MODE == GEMM_ACC_T)) {
-    if (P.splits == 1 && P.K > 64) {  // the ring engine (four waves, 160 KiB LDS)
-      hipLaunchKernelGGL((k_gemm4<T, MODE>), dim3(grid), dim3(kThreads4), 0, s, P);
+    if (P.splits == 1 && P.K > 64) {
+      hipLaunchKernelGGL((k_gemm4<T, KMAJ, KMAJ, MODE>), dim3(grid), dim3(kThreads4), 0, s, P);
+      return;
+    }
+  }
+  if constexpr (sizeof(T) == 2 && LA == MNMAJ && LB == MNMAJ && (MODE == GEMM_STORE || MODE == GEMM_SPLIT)) {
+    const int64_t lim = 0x7fffffffll / (int64_t)sizeof(T);
+    if (P.k_per_split > 64 && P.k_per_split * P.lda < lim && P.k_per_split * P.ldb < lim) {
+      hipLaunchKernelGGL((k_gemm4<T, MNMAJ, MNMAJ, MODE>), dim3(grid), dim3(kThreads4), 0, s, P);
       return;
     }
   }
