@@ -316,6 +316,17 @@ def test_schedules_agree_on_a_larger_problem():
         assert (a - b).abs().max().item() <= 2e-2 * scale
 
 
+def test_persistent_workgroups_over_many_tiles():
+    """V = 80000 (313 vocabulary tiles): the scan's workgroups each run three
+    vocabulary tiles back to back and the grad-W GEMM has more tiles than the
+    GPU has CUs, so workgroups move from tile to tile mid-pipeline."""
+    from orda_ce_kernel import KernelConfig
+
+    out, ref, hs, W, teacher = _run("tied", torch.bfloat16, N=512, H=256, V=80000, T=1.0, kl_w=1.0, w_t=1.0,
+                                    config=KernelConfig(chunk_size=128), profile="balanced", seed=5)
+    _check(out, ref, hs, W, torch.bfloat16)
+
+
 def test_grads_in_forward_are_bit_stable():
     o = _orda()
     hs, ht, W, _, y = _make(12, 300, 128, 2000, torch.bfloat16)
@@ -357,3 +368,22 @@ def test_general_gemm_layouts_match_torch(dtype, a_mn, b_mn):
 def test_general_gemm_split_k_matches_torch(dtype):
     for M, N, K, splits in ((264, 272, 5000, 4), (40, 512, 3000, 7), (256, 256, 128, 3)):
         _gemm_case(dtype, 1, 1, M, N, K, splits=splits)
+
+
+@pytest.mark.parametrize("dtype", DTYPES[:2], ids=["bf16", "f16"])
+def test_general_gemm_persistent_many_tiles(dtype):
+    """More output tiles (or split work items) than CUs, ragged edges: each
+    workgroup of the persistent GEMM runs several tiles in one pipeline."""
+    from orda_ce_kernel import _native
+
+    g = torch.Generator().manual_seed(7)
+    for a_mn, b_mn, M, N, K, splits in ((0, 0, 4104, 4104, 264, 1), (1, 1, 4104, 4104, 200, 1),
+                                        (1, 1, 1040, 2056, 9000, 6)):
+        a = torch.randn(M, K, generator=g).to(dtype).cuda()
+        b = torch.randn(N, K, generator=g).to(dtype).cuda()
+        a_in = a.t().contiguous() if a_mn else a
+        b_in = b.t().contiguous() if b_mn else b
+        c = _native.gemm(a_in, b_in, a_mn=a_mn, b_mn=b_mn, splits=splits).float()
+        ref = a.float() @ b.float().t()
+        err = (c - ref).abs().max().item()
+        assert err <= 2e-2 * max(1.0, ref.abs().max().item()), (a_mn, b_mn, M, N, K, splits, err)
