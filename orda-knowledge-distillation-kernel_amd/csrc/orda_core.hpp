@@ -1,22 +1,24 @@
 // orda_core.hpp -- device building blocks shared by every kernel of
-// liborda_ce.so: element traits, the LDS-staged MFMA main loop (CDNA4,
-// gfx950), the XCD-aware workgroup order, and the per-row softmax /
+// liborda_ce.so: element traits, the two-stage LDS-staged MFMA main loop
+// (CDNA4, gfx950; the four-wave ring engine for 16-bit operands is in
+// ring4.hpp), the XCD-aware workgroup order, and the per-row softmax /
 // divergence statistics.
 //
-// Orientation.  Every GEMM here computes C = A * B^T with both operands
-// K-contiguous (row-major [rows x K]).  In the fused loss kernels A is the
-// vocabulary weight W [V x H] and B the hidden states [N x H], so the MFMA
-// output tile is C[v][t]: one lane owns one token column and 16 vocabulary
-// rows per 32x32 block.  Per-token softmax reductions over the vocabulary
-// are therefore in-lane, plus one exchange between lane l and lane l^32 and
-// one between the two waves that split a tile's 256 vocabulary rows.
+// Orientation.  Every GEMM here computes C = A * B^T; each operand is either
+// K-contiguous (row-major [rows x K], "K-major") or MN-contiguous ([K x rows],
+// read through transposed LDS reads).  In the fused loss kernels A is the
+// vocabulary weight W [V x H] and B the hidden states [N x H], both K-major,
+// so the MFMA output tile is C[v][t]: one lane owns one token column and 16
+// vocabulary rows per 32x32 block.  Per-token softmax reductions over the
+// vocabulary are therefore in-lane, plus one exchange between lane l and
+// lane l^32 and one between the waves that split a tile's 256 vocabulary rows.
 //
-// Workgroup tile: 256 A rows x 256 B rows, 8 waves (2 per SIMD) arranged
-// 2 (A) x 4 (B); each wave owns 128 A rows x 64 B rows = 4 x 2 MFMA blocks
-// of 32x32.  B rows come in two 128-row halves; a wave's block 0 is in half 0
-// and block 1 in half 1 at the same offset, so for the loss kernels (half 0 =
-// student tokens, half 1 = teacher rows of the same tokens) a lane holds the
-// student and teacher logits of one token.
+// Two-stage engine tile: 256 A rows x 256 B rows, 8 waves (2 per SIMD)
+// arranged 2 (A) x 4 (B); each wave owns 128 A rows x 64 B rows = 4 x 2 MFMA
+// blocks of 32x32.  B rows come in two 128-row halves; a wave's block 0 is in
+// half 0 and block 1 in half 1 at the same offset, so for the loss kernels
+// (half 0 = student tokens, half 1 = teacher rows of the same tokens) a lane
+// holds the student and teacher logits of one token.
 #pragma once
 
 #include <hip/hip_runtime.h>
