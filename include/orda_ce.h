@@ -80,7 +80,8 @@ enum orda_divergence {
  * accumulated across chunks in the weight dtype (the reference's default,
  * fp32_grad_weight_accumulation=False, ops/tied_teacher.py:354,488-495).
  * orda_backward then only multiplies the gradients by grad_output
- * (ops/tied_teacher.py:531-564).  TIED and SEPARATE modes; not the two-pass
+ * (ops/tied_teacher.py:531-564).  Every mode (a precomputed teacher's logits
+ * are stored beside the student's in the compute dtype); not the two-pass
  * divergences (JSD, skew KLs, TVD): those return ORDA_EUNSUPPORTED. */
 #define ORDA_GRADS_IN_FORWARD (1u << 7)
 

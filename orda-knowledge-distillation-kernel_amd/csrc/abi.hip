@@ -32,6 +32,7 @@ int fail(int code, const char* fmt, ...) {
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t dtype_bytes(int32_t d) { return d == ORDA_F32 ? 4 : 2; }
 
 constexpr size_t kAlign = 256;
 inline size_t carve(size_t& off, size_t bytes) {
@@ -226,7 +227,9 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
   // gradients inside forward: one token chunk of logits at a time
   pl.fused = (f & ORDA_GRADS_IN_FORWARD) != 0;
   if (pl.fused) {
-    if (!tied && !sep) return fail(ORDA_EUNSUPPORTED, "ORDA_GRADS_IN_FORWARD needs the TIED or SEPARATE mode");
+    // precomputed teachers: no teacher gradient; their logits (memory or the
+    // frozen teacher GEMM) are stored next to the student's like a tied
+    // teacher's
     if (pl.two_pass)
       return fail(ORDA_EUNSUPPORTED, "ORDA_GRADS_IN_FORWARD does not support the two-pass divergences");
     pl.store_t = pl.tsrc != TSRC_NONE;
@@ -589,14 +592,18 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     const int64_t nc = (N - r0 < pl.fn) ? N - r0 : pl.fn;
 
     LabelParams Lb{};
-    Lb.hs = hs + r0 * H; Lb.W = W; Lb.ht = ht ? ht + r0 * Ht : nullptr; Lb.Wt = Wt; Lb.Lt = nullptr;
+    // the chunk's rows of precomputed teacher logits [N x V] (logits dtype)
+    const void* Ltc = t->teacher_logits
+                          ? static_cast<const char*>(t->teacher_logits) + r0 * V * dtype_bytes(p->logits_dtype)
+                          : nullptr;
+    Lb.hs = hs + r0 * H; Lb.W = W; Lb.ht = ht ? ht + r0 * Ht : nullptr; Lb.Wt = Wt; Lb.Lt = Ltc;
     Lb.labels = t->labels + r0;
     Lb.N = nc; Lb.V = V; Lb.H = H; Lb.Ht = Ht; Lb.ignore_index = p->ignore_index;
     Lb.tsrc = pl.tsrc; Lb.lt_dtype = p->logits_dtype; Lb.out = labelx;
     { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_label<T>(Lb, s)); }
 
     FusedParams F{};
-    F.W = W; F.hs = hs + r0 * H; F.ht = ht ? ht + r0 * Ht : nullptr; F.Wt = Wt; F.Lt = nullptr;
+    F.W = W; F.hs = hs + r0 * H; F.ht = ht ? ht + r0 * Ht : nullptr; F.Wt = Wt; F.Lt = Ltc;
     F.labels = t->labels + r0;
     F.N = nc; F.V = V; F.H = H; F.Ht = Ht; F.ignore_index = p->ignore_index;
     F.tsrc = pl.tsrc; F.lt_dtype = p->logits_dtype;
@@ -611,7 +618,9 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     F.tiles_per_range = pl.f_tpr; F.n_vtiles = pl.n_vtiles;
     F.partial = part; F.rowp = rowp;
     F.Lout = L; F.ldL = ldL; F.tcolL = nP; F.store_t = pl.store_t;
-    const double scan_flops = 2.0 * (double)nc * (double)V * ((double)H + (pl.store_t ? (double)Ht : 0.0));
+    // teacher logits from memory are no GEMM
+    const bool tgemm = pl.tsrc == TSRC_SHARED || pl.tsrc == TSRC_SEP;
+    const double scan_flops = 2.0 * (double)nc * (double)V * ((double)H + (tgemm ? (double)Ht : 0.0));
     { Timed tm_(ORDA_K_SCAN, s, scan_flops, scan_flops); ORDA_CHECK_LAUNCH(launch_scan_store<T>(F, F.n_ttiles * pl.f_nvr, s)); }
 
     MergeParams M{};

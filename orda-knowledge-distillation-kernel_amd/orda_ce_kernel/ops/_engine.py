@@ -71,10 +71,17 @@ def token_chunk_for(chunk_size) -> int:
 
 
 def grads_in_forward(mode: str, use_fp32_accum, divergence, any_grad: bool) -> bool:
-    """Whether a call takes the gradients-in-forward schedule."""
+    """Whether a call takes the gradients-in-forward schedule.
+
+    Every mode may (precomputed teachers get no gradient; their logits are
+    stored beside the student's for the chunk's dlogits, so the precomputed
+    logits caller checks that their dtype is the compute dtype).
+    """
     from ..divergences import TWO_PASS
 
-    if not any_grad or bool(use_fp32_accum) or mode not in ("tied", "separate"):
+    if not any_grad or bool(use_fp32_accum):
+        return False
+    if mode not in ("tied", "separate", "precomputed_logits", "precomputed_hidden"):
         return False
     return resolve_divergence(divergence).name not in TWO_PASS
 

@@ -19,14 +19,15 @@ from torch.autograd.function import once_differentiable
 from .._runtime import default_compute_dtype
 from ..utils.resolver import DEFAULT_MAX_FUSED_SIZE
 from ._checks import check_common, check_labels_in_range, check_scalars
-from ._engine import FusedCall, cast_to, fused_backward, fused_forward, require_native, vocab_chunk_for
+from ._engine import (FusedCall, cast_to, fused_backward, fused_forward, grads_in_forward, require_native,
+                      token_chunk_for, vocab_chunk_for)
 
 __all__ = ["PrecomputedCEFunction", "precomputed_distillation_loss"]
 
 
 def _forward(ctx, student_hidden, weight, logits_teacher, labels, student_ce_weight, ignore_index, reduction,
              chunk_size, kl_weight, kl_temperature, teacher_ce_weight, max_chunks, max_fused_size, teacher_hidden,
-             teacher_weight, divergence):
+             teacher_weight, divergence, use_fp32_accum=None):
     check_scalars(
         student_ce_weight=student_ce_weight, kl_weight=kl_weight, kl_temperature=kl_temperature,
         max_fused_size=max_fused_size,
@@ -69,6 +70,12 @@ def _forward(ctx, student_hidden, weight, logits_teacher, labels, student_ce_wei
         compute_teacher_ce=float(teacher_ce_weight) != 0.0,
         need_grad_student_hidden=student_hidden.requires_grad,
         need_grad_weight=weight.requires_grad,
+        # gradients inside forward store the teacher's logits in the compute
+        # dtype: only when that loses nothing (given logits of another dtype
+        # take the two-phase schedule, which reads them as given)
+        grads_in_forward=(grads_in_forward(mode, use_fp32_accum, divergence, ctx.compute_grad)
+                          and (logits_teacher is None or logits_teacher.dtype == dtype)),
+        token_chunk=token_chunk_for(chunk_size),
     )
     loss, ce_s, ce_t, kl = fused_forward(ctx, call)
     ctx.mark_non_differentiable(ce_s, ce_t, kl)
@@ -111,7 +118,7 @@ class PrecomputedCEFunction(torch.autograd.Function):
             raise ValueError("PrecomputedCEFunction requires teacher_ce_weight=0.0")
         return _forward(ctx, student_hidden, weight, logits_teacher, labels, student_ce_weight, ignore_index,
                         reduction, chunk_size, kl_weight, kl_temperature, 0.0, max_chunks, max_fused_size,
-                        teacher_hidden, teacher_weight, divergence)
+                        teacher_hidden, teacher_weight, divergence, use_fp32_accum)
 
     @staticmethod
     @once_differentiable
@@ -134,7 +141,7 @@ class PrecomputedTeacherCEFunction(torch.autograd.Function):
             raise ValueError(f"teacher_ce_weight must be >= 0.0, got {teacher_ce_weight}")
         return _forward(ctx, student_hidden, weight, logits_teacher, labels, student_ce_weight, ignore_index,
                         reduction, chunk_size, kl_weight, kl_temperature, float(teacher_ce_weight), max_chunks,
-                        max_fused_size, teacher_hidden, teacher_weight, divergence)
+                        max_fused_size, teacher_hidden, teacher_weight, divergence, use_fp32_accum)
 
     @staticmethod
     @once_differentiable

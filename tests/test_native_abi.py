@@ -182,12 +182,22 @@ def lib_backward_bytes(p):
     return _native.library().orda_backward_workspace_bytes(ctypes.byref(p))
 
 
-@pytest.mark.parametrize("field, value", [("mode", 2), ("mode", 3), ("divergence", 11), ("divergence", 14)])
-def test_grads_in_forward_rejects_unsupported_cases(field, value):
-    p = _problem(flags=0x33 | GIF, div_alpha=0.1, div_beta=0.5, **{field: value})
+@pytest.mark.parametrize("divergence", [11, 14])
+def test_grads_in_forward_rejects_two_pass_divergences(divergence):
+    p = _problem(flags=0x33 | GIF, div_alpha=0.1, div_beta=0.5, divergence=divergence)
     lib = _native.library()
     assert lib.orda_forward_workspace_bytes(ctypes.byref(p)) == 0
     assert b"ORDA_GRADS_IN_FORWARD" in lib.orda_last_error()
+
+
+@pytest.mark.parametrize("mode", [2, 3])
+def test_grads_in_forward_plans_precomputed_teachers(mode):
+    """Precomputed teachers (logits in memory / frozen hidden + W) take the
+    schedule too: one chunk of student and teacher logits, no teacher grads."""
+    p = _problem(mode=mode, flags=0x23 | GIF, teacher_ce_weight=0.0, logits_dtype=0)
+    ws = _native.forward_workspace_bytes(p)
+    assert 1024 * 128256 * 2 * 2 < ws < 900 << 20
+    assert lib_backward_bytes(p) == 0
 
 
 def test_timing_hook_without_launches_reports_zeros():
