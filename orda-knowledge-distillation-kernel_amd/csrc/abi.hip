@@ -70,7 +70,7 @@ struct Plan {
   int64_t NP, ldT, ldh, Vc, nchunks;
   size_t off_hT, off_htT, off_dLT, off_dLNs, off_dLNt, off_WT, off_WtT, off_g32s, off_g32t, bwd_bytes;
   // gradients inside forward (materialised token chunks)
-  bool fused, store_t;
+  bool fused, store_t, f_tl;
   int64_t fn, fnP, fldL, fnchunks;
   int f_nvr, f_tpr, splits_s, splits_t;
   int64_t kps_s, kps_t;
@@ -247,7 +247,13 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.fnP = round_up(n, 8);
     pl.fldL = ncol * pl.fnP;
     pl.fnchunks = cdiv(pl.N, n);
-    const int64_t ntt = cdiv(n, 128);
+    // A separate teacher's logits (its own GEMM) or precomputed logits of the
+    // model dtype are staged into L's teacher columns ahead of the scan, which
+    // then runs the student GEMM alone on the ring engine, 256 tokens per
+    // workgroup (16-bit, K > 64, one-pass non-power divergences).
+    pl.f_tl = pl.eb == 2 && pl.H > 64 && pl.fam != FAM_POW &&
+              ((pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype) || pl.tsrc == TSRC_SEP);
+    const int64_t ntt = cdiv(n, pl.f_tl ? 256 : 128);
     int64_t nvr = cdiv(kFusedScanGroups, ntt);
     if (nvr < 1) nvr = 1;
     if (nvr > pl.n_vtiles) nvr = pl.n_vtiles;
@@ -619,7 +625,21 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     F.partial = part; F.rowp = rowp;
     F.Lout = L; F.ldL = ldL; F.tcolL = nP; F.store_t = pl.store_t;
     // teacher logits from memory are no GEMM
-    const bool tgemm = pl.tsrc == TSRC_SHARED || pl.tsrc == TSRC_SEP;
+    bool tgemm = pl.tsrc == TSRC_SHARED || pl.tsrc == TSRC_SEP;
+    if (pl.f_tl) {
+      // stage the chunk's teacher logits in L[:, nP + t] (vocabulary-major)
+      char* Lt = L + nP * eb;
+      if (pl.tsrc == TSRC_MEM) {
+        Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+        ORDA_CHECK_LAUNCH(launch_transpose<T>(Ltc, V, Lt, ldL, nc, V, s));
+      } else {
+        ORDA_TRY(gemm2<T>(KMAJ, KMAJ, Wt, Ht, ht + r0 * Ht, Ht, nullptr, 0, Ht, Ht, 0, Lt, nullptr, ldL, V, nc, Ht,
+                          GEMM_STORE, 1, 0, s, ORDA_K_SCAN, 2.0 * (double)nc * (double)V * (double)Ht));
+      }
+      F.tsrc = TSRC_L;
+      F.n_ttiles = (int)cdiv(nc, 256);
+      tgemm = false;
+    }
     const double scan_flops = 2.0 * (double)nc * (double)V * ((double)H + (tgemm ? (double)Ht : 0.0));
     { Timed tm_(ORDA_K_SCAN, s, scan_flops, scan_flops); ORDA_CHECK_LAUNCH(launch_scan_store<T>(F, F.n_ttiles * pl.f_nvr, s)); }
 

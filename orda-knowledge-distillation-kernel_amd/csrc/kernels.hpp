@@ -429,9 +429,10 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
 }
 
 // Logits of a ring-engine tile to Lout[v][t] (see store_logits): block
-// acc[mb][nb] holds vocabulary rows wm * 128 + mb * 32 + acc_row and tokens
-// wn * 64 + (nb & 1) * 32 + lane % 32, student for nb < 2, teacher for nb >= 2.
-template <class T>
+// acc[mb][nb] holds vocabulary rows wm * 128 + mb * 32 + acc_row.  Tokens:
+// tied (TL false) wn * 64 + (nb & 1) * 32 + lane % 32, student for nb < 2,
+// teacher for nb >= 2; student-only tiles (TL) col4(nb, wn) + lane % 32.
+template <class T, bool TL>
 __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams& P, int64_t v0, int64_t t0) {
   const int lane = opaque_lane();
   const int wm = w4_m(), wn = w4_n();
@@ -439,11 +440,11 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
   T* L = static_cast<T*>(P.Lout);
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) {
-    if (nb >= 2 && !P.store_t) break;
-    const int64_t tb = t0 + wn * 64 + (nb & 1) * 32 + (lane & 31) - q;  // first token of the quad
+    if (!TL && nb >= 2 && !P.store_t) break;
+    const int64_t tb = t0 + (TL ? col4(nb, wn) : wn * 64 + (nb & 1) * 32) + (lane & 31) - q;  // quad's first token
     const int64_t nt = P.N - tb;
     const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
-    const int64_t col = tb + (nb >= 2 ? P.tcolL : 0);
+    const int64_t col = tb + (!TL && nb >= 2 ? P.tcolL : 0);
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
@@ -459,14 +460,58 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
   }
 }
 
-// k_scan on the four-wave ring engine, for 16-bit operands with the teacher
-// sharing W (TSRC_SHARED): the same workgroup -> (128 tokens, vocabulary
-// range) mapping and partial output.  The fused B operand (student hidden
-// rows t0.., then the teacher's) is fixed per workgroup; the vocabulary tiles
-// of the range run as one persistent ring (pipeline4, MFMAs not swapped), so
-// each lane holds two tokens: j = 0, 1 at blocks (j, j + 2).
-template <class T, int SV, bool STORE>
+// Student-only ring tiles with the teacher logits already in Lout's teacher
+// columns: token nb of the lane reads them with one 8-byte load of the quad's
+// 4 tokens per row group and the in-quad transpose (the inverse of
+// store_logits4).  Rows past V and tokens past N read as 0 (the scan masks
+// rows past V; tokens past N are never merged).
+template <class T>
+__device__ __forceinline__ void load4(const T* p, float (&x)[4], bool full, int n);
+template <class T>
+__device__ __forceinline__ void load_teacher4(f32x16 (&tv)[4], const FusedParams& P, int64_t v0, int64_t t0,
+                                              int nb) {
+  const int lane = opaque_lane();
+  const int wm = w4_m(), wn = w4_n();
+  const int q = lane & 3;
+  const T* L = static_cast<const T*>(P.Lout);
+  const int64_t tb = t0 + col4(nb, wn) + (lane & 31) - q;
+  const int64_t nt = P.N - tb;
+  const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t v = v0 + wm * 128 + acc_row(mb, g * 4, lane) + q;
+      float x[4] = {0.f, 0.f, 0.f, 0.f}, o[4];
+      if (v < P.V && ntok > 0) load4(L + v * P.ldL + P.tcolL + tb, x, ntok == 4, ntok);
+      quad_transpose(x, o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tv[mb][g * 4 + e] = o[e];
+    }
+}
+struct AccPairTL {  // student from accumulator block nb, teacher from registers
+  const Acc4& a;
+  int nb;
+  const f32x16 (&tv)[4];
+  __device__ __forceinline__ float s(int mb, int r) const { return acc_get(a[mb][nb], r); }
+  __device__ __forceinline__ float t(int mb, int r) const { return tv[mb][r]; }
+};
+
+// k_scan on the four-wave ring engine for 16-bit operands: the same
+// workgroup -> (tokens, vocabulary range) mapping and partial output.  The B
+// operand is fixed per workgroup; the vocabulary tiles of the range run as
+// one persistent ring (pipeline4, MFMAs not swapped).
+//  TL false (teacher sharing W, TSRC_SHARED): 128 tokens per workgroup, B =
+//    student hidden rows t0.. then the teacher's; each lane holds two tokens,
+//    j = 0, 1 at blocks (j, j + 2).
+//  TL true (TSRC_L: teacher logits already in Lout's teacher columns): 256
+//    tokens per workgroup, B = 256 student hidden rows; each lane holds four
+//    tokens (blocks 0..3), whose teacher logits come from Lout.
+template <class T, int SV, bool STORE, bool TL>
 __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
+  static_assert(!TL || SV < SV_JSD, "teacher logits from Lout: one-pass divergences");
+  constexpr int NJ = TL ? 4 : 2;       // tokens per lane
+  constexpr int kTok = TL ? 256 : 128;  // tokens per workgroup
   __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
   Acc4 acc;
   zero_acc4(acc);
@@ -475,17 +520,18 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   const int wm = w4_m(), wn = w4_n();
   int tt, vr;
   grouped_tile<4>(xcd_order(blockIdx.x, gridDim.x), P.n_ttiles, P.n_vranges, tt, vr);
-  const int64_t t0 = (int64_t)tt * 128;
+  const int64_t t0 = (int64_t)tt * kTok;
   const int vt_begin = vr * P.tiles_per_range;
   const int ntiles = min(vt_begin + P.tiles_per_range, P.n_vtiles) - vt_begin;
 
-  RowState st[2];
-  int64_t tok[2];
-  float lse_sT[2] = {0.f, 0.f}, lse_tT[2] = {0.f, 0.f};
+  RowState st[NJ];
+  int64_t tok[NJ];
+  float lse_sT[NJ], lse_tT[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     state_init_fam(st[j], kPhase1 ? FAM_NONE : P.fam);
-    tok[j] = t0 + wn * 64 + j * 32 + (lane & 31);
+    tok[j] = t0 + (TL ? col4(j, wn) : wn * 64 + j * 32) + (lane & 31);
+    lse_sT[j] = lse_tT[j] = 0.f;
     if (kPhase1 && tok[j] < P.N) {
       lse_sT[j] = P.rowp[1 * P.N + tok[j]];
       lse_tT[j] = P.rowp[3 * P.N + tok[j]];
@@ -494,7 +540,8 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   const T* W = static_cast<const T*>(P.W);
   const T* hs = static_cast<const T*>(P.hs);
   const T* ht = static_cast<const T*>(P.ht);
-  const KOp4 bop = kop4_split(hs + t0 * P.H, P.N - t0, ht + t0 * P.H, P.N - t0, P.H);
+  const KOp4 bop = TL ? kop4(hs + t0 * P.H, P.H, P.N - t0)
+                      : kop4_split(hs + t0 * P.H, P.N - t0, ht + t0 * P.H, P.N - t0, P.H);
   struct TI {
     int v0;
     KOp4 a;
@@ -507,19 +554,26 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   };
   auto opnd = [&](const TI& x, int op) { return op == 0 ? x.a : bop; };
   auto epilogue = [&](int, const TI& x, Acc4& c) {
-    if constexpr (STORE) store_logits4<T>(c, P, x.v0, t0);
+    if constexpr (STORE) store_logits4<T, TL>(c, P, x.v0, t0);
     const int vlane0 = wm * 128 + (opaque_lane() >> 5) * 4;
     const int64_t vlimit = P.V - x.v0;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      scan_variant<SV>(st[j], AccPair4{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+    static_for<0, NJ>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      if constexpr (TL) {
+        f32x16 tv[4];
+        load_teacher4<T>(tv, P, x.v0, t0, j);
+        scan_variant<SV>(st[j], AccPairTL{c, j, tv}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+      } else {
+        scan_variant<SV>(st[j], AccPair4{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+      }
+    });
   };
   pipeline4<T, KMAJ, KMAJ, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
 
   // combine lane l with l^32 (other vocabulary rows of the same tokens), then
   // the two waves sharing the tokens (wm 0 / 1)
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const RowState o = shfl32(st[j]);
     merge_any<kPhase1>(st[j], o, P);
   }
@@ -527,8 +581,8 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   float* xch = reinterpret_cast<float*>(lds);  // [wn][j][kNStat][32]
   if (wm == 1 && lane < 32) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float* d = xch + ((wn * 2 + j) * kNStat) * 32 + lane;
+    for (int j = 0; j < NJ; ++j) {
+      float* d = xch + ((wn * NJ + j) * kNStat) * 32 + lane;
       const float* sv = reinterpret_cast<const float*>(&st[j]);
 #pragma unroll
       for (int f = 0; f < kNStat; ++f) d[f * 32] = sv[f];
@@ -537,10 +591,10 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   __syncthreads();
   if (wm == 0 && lane < 32) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       RowState o;
       float* od = reinterpret_cast<float*>(&o);
-      const float* sv = xch + ((wn * 2 + j) * kNStat) * 32 + lane;
+      const float* sv = xch + ((wn * NJ + j) * kNStat) * 32 + lane;
 #pragma unroll
       for (int f = 0; f < kNStat; ++f) od[f] = sv[f * 32];
       merge_any<kPhase1>(st[j], o, P);
@@ -1288,7 +1342,7 @@ inline bool scan_on_ring(const FusedParams& P) {
   case SV:                                                                                       \
     if constexpr (sizeof(T) == 2) {                                                              \
       if (scan_on_ring<T>(P)) {                                                                  \
-        hipLaunchKernelGGL((k_scan4<T, SV, false>), dim3(grid), dim3(kThreads4), 0, s, P);       \
+        hipLaunchKernelGGL((k_scan4<T, SV, false, false>), dim3(grid), dim3(kThreads4), 0, s, P);       \
         break;                                                                                   \
       }                                                                                          \
     }                                                                                            \
@@ -1372,8 +1426,15 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
 #define ORDA_SCANST_CASE(T, SV)                                                                  \
   case SV:                                                                                       \
     if constexpr (sizeof(T) == 2) {                                                              \
+      if (P.tsrc == TSRC_L) {                                                                    \
+        if constexpr (SV == SV_STUDENT || SV == SV_POW)                                          \
+          return hipErrorInvalidValue;                                                           \
+        else                                                                                     \
+          hipLaunchKernelGGL((k_scan4<T, SV, true, true>), dim3(grid), dim3(kThreads4), 0, s, P); \
+        break;                                                                                   \
+      }                                                                                          \
       if (scan_on_ring<T>(P)) {                                                                  \
-        hipLaunchKernelGGL((k_scan4<T, SV, true>), dim3(grid), dim3(kThreads4), 0, s, P);        \
+        hipLaunchKernelGGL((k_scan4<T, SV, true, false>), dim3(grid), dim3(kThreads4), 0, s, P); \
         break;                                                                                   \
       }                                                                                          \
     }                                                                                            \
@@ -1382,6 +1443,7 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
 #define ORDA_INSTANTIATE_SCAN_STORE(T)                                                     \
   template <> hipError_t launch_scan_store<T>(const FusedParams& P, int grid, hipStream_t s) { \
     if (P.phase != 0) return hipErrorInvalidValue;                                         \
+    if (P.tsrc == TSRC_L && (sizeof(T) != 2 || P.H <= 64)) return hipErrorInvalidValue;     \
     switch (scan_variant_of(P)) {                                                          \
       ORDA_SCANST_CASE(T, SV_STUDENT)                                                      \
       ORDA_SCANST_CASE(T, SV_TCE_T1)                                                       \

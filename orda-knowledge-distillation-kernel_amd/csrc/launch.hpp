@@ -14,7 +14,9 @@ enum TeacherSource {
   TSRC_NONE = 0,    // no teacher term (student CE only)
   TSRC_SHARED = 1,  // teacher hidden x the student's W (tied mode)
   TSRC_SEP = 2,     // teacher hidden x W_t (separate / precomputed hidden)
-  TSRC_MEM = 3      // precomputed logits [N x V]
+  TSRC_MEM = 3,     // precomputed logits [N x V]
+  TSRC_L = 4        // already in Lout's teacher columns (vocabulary-major; the
+                    // 16-bit ring scan of the gradients-in-forward schedule)
 };
 
 // GEMM epilogues: STORE writes C in T; ACC_FIRST / ACC / ACC_LAST build an

@@ -196,6 +196,17 @@ __device__ __forceinline__ int opaque_lane() {
   return l;
 }
 
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled by construction: a
+// loop body too large for the unroller would otherwise index register arrays
+// (accumulator blocks) dynamically and demote them to scratch.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 __device__ __forceinline__ void zero_acc(f32x16 (&acc)[4][2]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)

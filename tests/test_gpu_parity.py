@@ -327,6 +327,30 @@ def test_persistent_workgroups_over_many_tiles():
     _check(out, ref, hs, W, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("mode", ["separate", "precomputed_logits", "precomputed_hidden"])
+def test_staged_teacher_logits_feed_the_student_scan(dtype, mode):
+    """Separate and precomputed teachers with 16-bit operands and H > 64: the
+    chunk's teacher logits are written into the logits buffer first (teacher
+    GEMM or transpose) and the scan runs the student GEMM alone, 256 tokens
+    per workgroup.  N=600 in 256-token chunks (256 + 256 + 88: a ragged last
+    tile), V=5000 (ragged last vocabulary tile); the power family (hellinger)
+    keeps the two-operand scan."""
+    from orda_ce_kernel import KernelConfig
+
+    grad_teacher = mode == "separate"
+    for div, T in (("forward_kl", 1.0), ("forward_kl", 2.0), ("reverse_kl", 1.0), ("squared_l2", 2.0),
+                   ("hellinger", 1.0)):
+        out, ref, hs, W, teacher = _run(mode, dtype, N=600, H=128, Ht=192, V=5000, T=T, kl_w=0.8,
+                                        w_t=0.4 if grad_teacher else None, div=div, grad_teacher=grad_teacher,
+                                        config=KernelConfig(chunk_size=128), seed=21)
+        _check(out, ref, hs, W, dtype)
+        if grad_teacher:
+            tol = _grad_tol(dtype)
+            _close_grad(teacher.hidden.grad, ref["grad_teacher_hidden"], "grad_teacher_hidden", tol)
+            _close_grad(teacher.weight.grad, ref["grad_teacher_weight"], "grad_teacher_weight", tol)
+
+
 def test_grads_in_forward_are_bit_stable():
     o = _orda()
     hs, ht, W, _, y = _make(12, 300, 128, 2000, torch.bfloat16)
