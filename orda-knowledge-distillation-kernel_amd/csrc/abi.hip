@@ -627,16 +627,21 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     // teacher logits from memory are no GEMM
     bool tgemm = pl.tsrc == TSRC_SHARED || pl.tsrc == TSRC_SEP;
     if (pl.f_tl) {
-      // stage the chunk's teacher logits in L[:, nP + t] (vocabulary-major)
+      // the chunk's teacher logits go to L[:, nP + t] (vocabulary-major) ahead
+      // of the scan (teacher GEMM, transpose) or through it
       char* Lt = L + nP * eb;
-      if (pl.tsrc == TSRC_MEM) {
+      if (pl.tsrc == TSRC_MEM && V % 4 == 0 && reinterpret_cast<uintptr_t>(t->teacher_logits) % 8 == 0) {
+        // read token-major by the scan itself (8-byte loads of 4 rows), which
+        // writes them to L on the way
+        F.tsrc = TSRC_MEM_RING;
+      } else if (pl.tsrc == TSRC_MEM) {
         Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
         ORDA_CHECK_LAUNCH(launch_transpose<T>(Ltc, V, Lt, ldL, nc, V, s));
       } else {
         ORDA_TRY(gemm2<T>(KMAJ, KMAJ, Wt, Ht, ht + r0 * Ht, Ht, nullptr, 0, Ht, Ht, 0, Lt, nullptr, ldL, V, nc, Ht,
                           GEMM_STORE, 1, 0, s, ORDA_K_SCAN, 2.0 * (double)nc * (double)V * (double)Ht));
       }
-      F.tsrc = TSRC_L;
+      if (F.tsrc != TSRC_MEM_RING) F.tsrc = TSRC_L;
       F.n_ttiles = (int)cdiv(nc, 256);
       tgemm = false;
     }

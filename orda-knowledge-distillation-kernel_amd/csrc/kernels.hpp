@@ -460,34 +460,96 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
   }
 }
 
-// Student-only ring tiles with the teacher logits already in Lout's teacher
-// columns: token nb of the lane reads them with one 8-byte load of the quad's
-// 4 tokens per row group and the in-quad transpose (the inverse of
-// store_logits4).  Rows past V and tokens past N read as 0 (the scan masks
-// rows past V; tokens past N are never merged).
+// Teacher logits of the ring scan's student-only tiles (token block nb of the
+// lane: 4 x 16 values, rows as in the accumulator) come in two steps: 16 raw
+// 8-byte loads (issue_teacher4), then unpacking (finish_teacher4), so the
+// next block's loads are in flight while this one is scanned.
+//  TL_FROM_L: Lout's teacher columns (vocabulary-major): one load holds the
+//    quad's 4 tokens of one row; the in-quad transpose (the inverse of
+//    store_logits4) gives the lane its token's 4 rows.
+//  TL_FROM_MEM: precomputed logits [N x V] (token-major, V a multiple of 4):
+//    one load holds the lane's token's 4 consecutive rows directly; the tile
+//    then writes them to Lout's teacher columns for the dlogits pass.
+// Rows past V and tokens past N read as 0 (the scan masks rows past V;
+// tokens past N are never merged).
+enum { TL_NONE = 0, TL_FROM_L = 1, TL_FROM_MEM = 2 };
+
 template <class T>
-__device__ __forceinline__ void load4(const T* p, float (&x)[4], bool full, int n);
+__device__ __forceinline__ uint2 load_raw4(const T* p, int n) {  // n in 1..4 16-bit elements
+  if (n >= 4) return *reinterpret_cast<const uint2*>(p);
+  const unsigned short* h = reinterpret_cast<const unsigned short*>(p);
+  const unsigned a = h[0];
+  const unsigned b = n > 1 ? (unsigned)h[1] : 0u;
+  const unsigned c = n > 2 ? (unsigned)h[2] : 0u;
+  return make_uint2(a | (b << 16), c);
+}
 template <class T>
-__device__ __forceinline__ void load_teacher4(f32x16 (&tv)[4], const FusedParams& P, int64_t v0, int64_t t0,
-                                              int nb) {
+__device__ __forceinline__ void unpack_raw4(uint2 r, float (&x)[4]) {
+  union { uint2 u; T e[4]; } v;
+  v.u = r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = to_f32(v.e[i]);
+}
+
+template <class T, int TL>
+__device__ __forceinline__ void issue_teacher4(uint2 (&raw)[16], const FusedParams& P, int64_t v0, int64_t t0,
+                                               int nb) {
+  const int lane = opaque_lane();
+  const int wm = w4_m(), wn = w4_n();
+  if constexpr (TL == TL_FROM_L) {
+    const int q = lane & 3;
+    const T* L = static_cast<const T*>(P.Lout);
+    const int64_t tb = t0 + col4(nb, wn) + (lane & 31) - q;  // quad's first token
+    const int64_t nt = P.N - tb;
+    const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane) + q;
+      raw[i] = (v < P.V && ntok > 0) ? load_raw4(L + v * P.ldL + P.tcolL + tb, ntok) : make_uint2(0u, 0u);
+    }
+  } else {
+    const T* Lt = static_cast<const T*>(P.Lt);
+    const int64_t tok = t0 + col4(nb, wn) + (lane & 31);
+    const bool live = tok < P.N;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane);  // rows v .. v + 3
+      raw[i] = (live && v < P.V) ? *reinterpret_cast<const uint2*>(Lt + tok * P.V + v) : make_uint2(0u, 0u);
+    }
+  }
+}
+template <class T, int TL>
+__device__ __forceinline__ void finish_teacher4(const uint2 (&raw)[16], f32x16 (&tv)[4]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float x[4], o[4];
+    unpack_raw4<T>(raw[i], x);
+    if constexpr (TL == TL_FROM_L) quad_transpose(x, o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tv[i >> 2][(i & 3) * 4 + e] = TL == TL_FROM_L ? o[e] : x[e];
+  }
+}
+// Token block nb's teacher logits (registers, accumulator layout) to Lout's
+// teacher columns, as store_logits4 writes a tied teacher's.
+template <class T>
+__device__ __forceinline__ void store_teacher4(const f32x16 (&tv)[4], const FusedParams& P, int64_t v0, int64_t t0,
+                                               int nb) {
   const int lane = opaque_lane();
   const int wm = w4_m(), wn = w4_n();
   const int q = lane & 3;
-  const T* L = static_cast<const T*>(P.Lout);
+  T* L = static_cast<T*>(P.Lout);
   const int64_t tb = t0 + col4(nb, wn) + (lane & 31) - q;
   const int64_t nt = P.N - tb;
   const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int i = 0; i < 16; ++i) {
+    const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane) + q;
+    float x[4], o[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int64_t v = v0 + wm * 128 + acc_row(mb, g * 4, lane) + q;
-      float x[4] = {0.f, 0.f, 0.f, 0.f}, o[4];
-      if (v < P.V && ntok > 0) load4(L + v * P.ldL + P.tcolL + tb, x, ntok == 4, ntok);
-      quad_transpose(x, o);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) tv[mb][g * 4 + e] = o[e];
-    }
+    for (int e = 0; e < 4; ++e) x[e] = tv[i >> 2][(i & 3) * 4 + e];
+    quad_transpose(x, o);
+    if (v < P.V && ntok > 0) store4(L + v * P.ldL + P.tcolL + tb, o, ntok == 4, ntok);
+  }
 }
 struct AccPairTL {  // student from accumulator block nb, teacher from registers
   const Acc4& a;
@@ -504,13 +566,13 @@ struct AccPairTL {  // student from accumulator block nb, teacher from registers
 //  TL false (teacher sharing W, TSRC_SHARED): 128 tokens per workgroup, B =
 //    student hidden rows t0.. then the teacher's; each lane holds two tokens,
 //    j = 0, 1 at blocks (j, j + 2).
-//  TL true (TSRC_L: teacher logits already in Lout's teacher columns): 256
-//    tokens per workgroup, B = 256 student hidden rows; each lane holds four
-//    tokens (blocks 0..3), whose teacher logits come from Lout.
-template <class T, int SV, bool STORE, bool TL>
+//  TL_FROM_L / TL_FROM_MEM (teacher logits from memory, see
+//    issue_teacher4): 256 tokens per workgroup, B = 256 student hidden rows;
+//    each lane holds four tokens (blocks 0..3).
+template <class T, int SV, bool STORE, int TL>
 __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
-  static_assert(!TL || SV < SV_JSD, "teacher logits from Lout: one-pass divergences");
-  constexpr int NJ = TL ? 4 : 2;       // tokens per lane
+  static_assert(TL == TL_NONE || (SV < SV_JSD && STORE), "teacher logits from memory: one-pass, stored");
+  constexpr int NJ = TL ? 4 : 2;        // tokens per lane
   constexpr int kTok = TL ? 256 : 128;  // tokens per workgroup
   __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
   Acc4 acc;
@@ -554,19 +616,27 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   };
   auto opnd = [&](const TI& x, int op) { return op == 0 ? x.a : bop; };
   auto epilogue = [&](int, const TI& x, Acc4& c) {
-    if constexpr (STORE) store_logits4<T, TL>(c, P, x.v0, t0);
     const int vlane0 = wm * 128 + (opaque_lane() >> 5) * 4;
     const int64_t vlimit = P.V - x.v0;
-    static_for<0, NJ>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      if constexpr (TL) {
+    if constexpr (TL != TL_NONE) {
+      uint2 raw[2][16];
+      issue_teacher4<T, TL>(raw[0], P, x.v0, t0, 0);
+      store_logits4<T, true>(c, P, x.v0, t0);
+      static_for<0, NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j + 1 < NJ) issue_teacher4<T, TL>(raw[(j + 1) & 1], P, x.v0, t0, j + 1);
         f32x16 tv[4];
-        load_teacher4<T>(tv, P, x.v0, t0, j);
+        finish_teacher4<T, TL>(raw[j & 1], tv);
+        if constexpr (TL == TL_FROM_MEM) store_teacher4<T>(tv, P, x.v0, t0, j);
         scan_variant<SV>(st[j], AccPairTL{c, j, tv}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
-      } else {
+      });
+    } else {
+      if constexpr (STORE) store_logits4<T, false>(c, P, x.v0, t0);
+      static_for<0, NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
         scan_variant<SV>(st[j], AccPair4{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
-      }
-    });
+      });
+    }
   };
   pipeline4<T, KMAJ, KMAJ, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
 
@@ -1342,7 +1412,7 @@ inline bool scan_on_ring(const FusedParams& P) {
   case SV:                                                                                       \
     if constexpr (sizeof(T) == 2) {                                                              \
       if (scan_on_ring<T>(P)) {                                                                  \
-        hipLaunchKernelGGL((k_scan4<T, SV, false, false>), dim3(grid), dim3(kThreads4), 0, s, P);       \
+        hipLaunchKernelGGL((k_scan4<T, SV, false, TL_NONE>), dim3(grid), dim3(kThreads4), 0, s, P);       \
         break;                                                                                   \
       }                                                                                          \
     }                                                                                            \
@@ -1426,15 +1496,17 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
 #define ORDA_SCANST_CASE(T, SV)                                                                  \
   case SV:                                                                                       \
     if constexpr (sizeof(T) == 2) {                                                              \
-      if (P.tsrc == TSRC_L) {                                                                    \
+      if (P.tsrc == TSRC_L || P.tsrc == TSRC_MEM_RING) {                                         \
         if constexpr (SV == SV_STUDENT || SV == SV_POW)                                          \
           return hipErrorInvalidValue;                                                           \
+        else if (P.tsrc == TSRC_L)                                                               \
+          hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_L>), dim3(grid), dim3(kThreads4), 0, s, P); \
         else                                                                                     \
-          hipLaunchKernelGGL((k_scan4<T, SV, true, true>), dim3(grid), dim3(kThreads4), 0, s, P); \
+          hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_MEM>), dim3(grid), dim3(kThreads4), 0, s, P); \
         break;                                                                                   \
       }                                                                                          \
       if (scan_on_ring<T>(P)) {                                                                  \
-        hipLaunchKernelGGL((k_scan4<T, SV, true, false>), dim3(grid), dim3(kThreads4), 0, s, P); \
+        hipLaunchKernelGGL((k_scan4<T, SV, true, TL_NONE>), dim3(grid), dim3(kThreads4), 0, s, P); \
         break;                                                                                   \
       }                                                                                          \
     }                                                                                            \
@@ -1443,7 +1515,9 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
 #define ORDA_INSTANTIATE_SCAN_STORE(T)                                                     \
   template <> hipError_t launch_scan_store<T>(const FusedParams& P, int grid, hipStream_t s) { \
     if (P.phase != 0) return hipErrorInvalidValue;                                         \
-    if (P.tsrc == TSRC_L && (sizeof(T) != 2 || P.H <= 64)) return hipErrorInvalidValue;     \
+    if ((P.tsrc == TSRC_L || P.tsrc == TSRC_MEM_RING) && (sizeof(T) != 2 || P.H <= 64))    \
+      return hipErrorInvalidValue;                                                         \
+    if (P.tsrc == TSRC_MEM_RING && P.V % 4 != 0) return hipErrorInvalidValue;              \
     switch (scan_variant_of(P)) {                                                          \
       ORDA_SCANST_CASE(T, SV_STUDENT)                                                      \
       ORDA_SCANST_CASE(T, SV_TCE_T1)                                                       \

@@ -15,8 +15,11 @@ enum TeacherSource {
   TSRC_SHARED = 1,  // teacher hidden x the student's W (tied mode)
   TSRC_SEP = 2,     // teacher hidden x W_t (separate / precomputed hidden)
   TSRC_MEM = 3,     // precomputed logits [N x V]
-  TSRC_L = 4        // already in Lout's teacher columns (vocabulary-major; the
+  TSRC_L = 4,       // already in Lout's teacher columns (vocabulary-major; the
                     // 16-bit ring scan of the gradients-in-forward schedule)
+  TSRC_MEM_RING = 5  // precomputed logits [N x V] of the compute dtype, read by
+                     // the 16-bit ring scan, which also writes them to Lout's
+                     // teacher columns (V a multiple of 4)
 };
 
 // GEMM epilogues: STORE writes C in T; ACC_FIRST / ACC / ACC_LAST build an

@@ -335,13 +335,18 @@ def test_staged_teacher_logits_feed_the_student_scan(dtype, mode):
     GEMM or transpose) and the scan runs the student GEMM alone, 256 tokens
     per workgroup.  N=600 in 256-token chunks (256 + 256 + 88: a ragged last
     tile), V=5000 (ragged last vocabulary tile); the power family (hellinger)
-    keeps the two-operand scan."""
+    keeps the two-operand scan.  Precomputed logits are read token-major by
+    the scan when V is a multiple of 4 (V=5000) and transposed into the
+    buffer first otherwise (V=4998)."""
     from orda_ce_kernel import KernelConfig
 
     grad_teacher = mode == "separate"
-    for div, T in (("forward_kl", 1.0), ("forward_kl", 2.0), ("reverse_kl", 1.0), ("squared_l2", 2.0),
-                   ("hellinger", 1.0)):
-        out, ref, hs, W, teacher = _run(mode, dtype, N=600, H=128, Ht=192, V=5000, T=T, kl_w=0.8,
+    cases = [("forward_kl", 1.0, 5000), ("forward_kl", 2.0, 5000), ("reverse_kl", 1.0, 5000),
+             ("squared_l2", 2.0, 5000), ("hellinger", 1.0, 5000)]
+    if mode == "precomputed_logits":
+        cases += [("forward_kl", 1.0, 4998), ("reverse_kl", 2.0, 4998)]
+    for div, T, V in cases:
+        out, ref, hs, W, teacher = _run(mode, dtype, N=600, H=128, Ht=192, V=V, T=T, kl_w=0.8,
                                         w_t=0.4 if grad_teacher else None, div=div, grad_teacher=grad_teacher,
                                         config=KernelConfig(chunk_size=128), seed=21)
         _check(out, ref, hs, W, dtype)
