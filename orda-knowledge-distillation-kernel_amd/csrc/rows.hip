@@ -5,25 +5,37 @@
 
 namespace orda {
 
-// One thread per token: merge the per-vocabulary-range partial states in a
-// fixed order (bit-stable), then form the row losses and the parameters the
+// 32 tokens per workgroup, 8 threads per token: thread (slice, token) merges
+// the partial states of vocabulary ranges slice, slice + 8, ... in order, and
+// the slice-0 thread then merges the 8 slice states in slice order (a fixed
+// order: bit-stable), then forms the row losses and the parameters the
 // dlogits kernel needs.  The final combination runs in fp64 to limit the
 // cancellation in lse_s - lse_t + (cross term).
-__global__ __launch_bounds__(256) void k_merge(MergeParams P) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= P.N) return;
+constexpr int kMergeSlices = 8;
+constexpr int kMergeTok = 32;
+__global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams P) {
+  __shared__ float xch[kMergeSlices - 1][kNStat][kMergeTok];
+  __shared__ double xch1[kMergeSlices - 1][2][kMergeTok];
+  const int tl = threadIdx.x % kMergeTok, slice = threadIdx.x / kMergeTok;
+  const int64_t t = (int64_t)blockIdx.x * kMergeTok + tl;
+  const bool live = t < P.N;
   const int64_t N = P.N;
-  const int64_t y = P.labels[t];
-  const bool ignored = (y == P.ignore_index);
-  const double T = P.temperature, invT = P.invT;
 
   if (P.phase == 1) {
     double x0 = 0.0, x1 = 0.0;
-    for (int vr = 0; vr < P.n_vranges; ++vr) {
-      const float* s = P.partial + (int64_t)vr * kNStat * N + t;
-      x0 += s[6 * N];
-      x1 += s[7 * N];
-    }
+    if (live)
+      for (int vr = slice; vr < P.n_vranges; vr += kMergeSlices) {
+        const float* s = P.partial + (int64_t)vr * kNStat * N + t;
+        x0 += s[6 * N];
+        x1 += s[7 * N];
+      }
+    if (slice > 0) { xch1[slice - 1][0][tl] = x0; xch1[slice - 1][1][tl] = x1; }
+    __syncthreads();
+    if (slice > 0 || !live) return;
+    for (int k = 0; k < kMergeSlices - 1; ++k) { x0 += xch1[k][0][tl]; x1 += xch1[k][1][tl]; }
+    const int64_t y = P.labels[t];
+    const bool ignored = (y == P.ignore_index);
+    const double T = P.temperature;
     double D = 0.0, c0 = 0.0, c1 = 0.0;
     switch (P.div) {
       case DIV_JSD: D = P.beta * x0 + (1.0 - P.beta) * x1; c1 = x1; break;
@@ -38,18 +50,30 @@ __global__ __launch_bounds__(256) void k_merge(MergeParams P) {
   }
 
   RowState S;
-  {
-    const float* s = P.partial + t;
-    float* d = reinterpret_cast<float*>(&S);
-    for (int f = 0; f < kNStat; ++f) d[f] = s[(int64_t)f * N];
+  state_init_fam(S, P.fam);
+  if (live)
+    for (int vr = slice; vr < P.n_vranges; vr += kMergeSlices) {
+      RowState o;
+      const float* s = P.partial + (int64_t)vr * kNStat * N + t;
+      float* d = reinterpret_cast<float*>(&o);
+      for (int f = 0; f < kNStat; ++f) d[f] = s[(int64_t)f * N];
+      state_merge(S, o, P.fam, P.t_is_one != 0, P.invT);
+    }
+  if (slice > 0) {
+    const float* d = reinterpret_cast<const float*>(&S);
+    for (int f = 0; f < kNStat; ++f) xch[slice - 1][f][tl] = d[f];
   }
-  for (int vr = 1; vr < P.n_vranges; ++vr) {
+  __syncthreads();
+  if (slice > 0 || !live) return;
+  for (int k = 0; k < kMergeSlices - 1; ++k) {
     RowState o;
-    const float* s = P.partial + (int64_t)vr * kNStat * N + t;
     float* d = reinterpret_cast<float*>(&o);
-    for (int f = 0; f < kNStat; ++f) d[f] = s[(int64_t)f * N];
+    for (int f = 0; f < kNStat; ++f) d[f] = xch[k][f][tl];
     state_merge(S, o, P.fam, P.t_is_one != 0, P.invT);
   }
+  const int64_t y = P.labels[t];
+  const bool ignored = (y == P.ignore_index);
+  const double T = P.temperature, invT = P.invT;
   const bool t1 = P.t_is_one != 0;
   const double lse_s = (double)S.ms + log((double)S.ss);
   const double lse_sT = t1 ? lse_s : (double)S.ms * invT + log((double)S.sst);
@@ -182,8 +206,8 @@ __global__ void k_zero2d(char* out, int64_t ld_bytes, int64_t R, int64_t c0_byte
 }
 
 hipError_t launch_merge(const MergeParams& P, hipStream_t s) {
-  const int grid = (int)((P.N + 255) / 256);
-  hipLaunchKernelGGL(k_merge, dim3(grid), dim3(256), 0, s, P);
+  const int grid = (int)((P.N + kMergeTok - 1) / kMergeTok);
+  hipLaunchKernelGGL(k_merge, dim3(grid), dim3(kMergeSlices * kMergeTok), 0, s, P);
   return hipGetLastError();
 }
 
