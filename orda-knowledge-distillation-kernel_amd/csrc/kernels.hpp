@@ -193,28 +193,35 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
     }
   }
 
-  // accumulate this tile
+  // accumulate this tile.  exp(x - m) = 2^(x log2e - m log2e): one fma forms
+  // the exponent; the teacher's log-ratio sum (x[2]) is taken in that base-2
+  // exponent and scaled by ln 2 once per tile.
+  const float ms2 = nms * kLog2e, mt2 = nmt * kLog2e;
+  const float cT = invT * kLog2e, msT2 = nms * cT, mtT2 = nmt * cT;
+  float lx2 = 0.f;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
       const float xs = acc.s(mb, r);
-      const float es = fexp(xs - nms);
+      const float es = __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, -ms2));
       S.ss += es;
-      const float esT = T1 ? es : fexp((xs - nms) * invT);
+      const float esT = T1 ? es : __builtin_amdgcn_exp2f(fmaf(xs, cT, -msT2));
       if (!T1) S.sst += esT;
       if (HAS_T) {
         const float xt = acc.t(mb, r);
-        const float et = fexp(xt - nmt);
+        const float at = fmaf(xt, kLog2e, -mt2);
+        const float et = __builtin_amdgcn_exp2f(at);
         S.st += et;
-        const float etT = T1 ? et : fexp((xt - nmt) * invT);
+        const float atT = T1 ? at : fmaf(xt, cT, -mtT2);
+        const float etT = T1 ? et : __builtin_amdgcn_exp2f(atT);
         if (!T1) S.stt += etT;
         if (FAM == FAM_LIN) {
-          const float zd = (xt - xs) * invT;
+          const float zd = T1 ? xt - xs : (xt - xs) * invT;
           S.x[0] += etT * zd;
           S.x[1] -= esT * zd;
-          S.x[2] += etT * ((xt - nmt) * invT);
+          lx2 += etT * atT;
         }
         if (FAM == FAM_POW) {
           S.x[1] += fexp((P.pa[0] * xt + P.pb[0] * xs) * invT - nmu0);
@@ -223,6 +230,7 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
         }
       }
     }
+  if (HAS_T && FAM == FAM_LIN) S.x[2] += lx2 * kLn2;
 }
 
 // Phase 1 (two-pass divergences): sums of terms of the normalised
@@ -1045,10 +1053,10 @@ __global__ __launch_bounds__(kThreads) void k_gemm2(GemmParams P) {
 }
 
 // C[M x N] (mode) A B^T for 16-bit operands on the four-wave ring engine
-// (pipeline4): A and B both K-major (MODE GEMM_STORE: C = in T, GEMM_ACC_T:
-// C += in T, the fp32 sum rounded once; one split), or both MN-major (GEMM_STORE,
-// or GEMM_SPLIT: split s covers K rows [s * k_per_split, ...) and writes its
-// fp32 partial).  Persistent: workgroup b (in XCD order) owns work items b,
+// (pipeline4): A K-major and B K-major or MN-major (one segment; MODE
+// GEMM_STORE: C = in T, GEMM_ACC_T: C += in T, the fp32 sum rounded once; one
+// split), or both MN-major (GEMM_STORE, or GEMM_SPLIT: split s covers K rows
+// [s * k_per_split, ...) and writes its fp32 partial).  Persistent: workgroup b (in XCD order) owns work items b,
 // b + grid, ... (split-major, tiles in band order, 8 row tiles wide).  The
 // MFMAs run swapped (B x A^T), so each lane holds four consecutive columns of
 // one C row and stores them with one 8-byte (16-byte for fp32) store.
@@ -1056,7 +1064,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm2(GemmParams P) {
 // k_per_split * ld * sizeof(T) < 2^31.
 template <class T, int LA, int LB, int MODE>
 __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
-  static_assert(LA == LB, "both operands K-major or both MN-major");
+  static_assert(LA == LB || (LA == KMAJ && LB == MNMAJ), "K/K, K/MN or MN/MN");
   __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
   Acc4 acc;
   zero_acc4(acc);
@@ -1084,9 +1092,12 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
     x.m0 = (first_m + rem % gm) * 256;
     x.n0 = (rem / gm) * 256;
     const int64_t kb = (int64_t)x.split * P.k_per_split;
-    if constexpr (LA == KMAJ) {
+    if constexpr (LA == KMAJ && LB == KMAJ) {
       x.a = kop4(A + (int64_t)x.m0 * P.lda + kb, P.lda, P.M - x.m0);
       x.b = kop4(B + (int64_t)x.n0 * P.ldb + kb, P.ldb, P.N - x.n0);
+    } else if constexpr (LA == KMAJ) {
+      x.a = kop4(A + (int64_t)x.m0 * P.lda, P.lda, P.M - x.m0);
+      x.b = kop4_mn(B + x.n0, P.ldb, P.b_kval0, P.N - x.n0);
     } else {
       const int64_t klen = min<int64_t>(P.K - kb, P.k_per_split);
       x.a = kop4_mn(A + kb * P.lda + x.m0, P.lda, klen, P.M - x.m0);
@@ -1571,6 +1582,13 @@ inline void gemm2_go(const GemmParams& P, hipStream_t s) {
   if constexpr (sizeof(T) == 2 && LA == KMAJ && LB == KMAJ && (MODE == GEMM_STORE || MODE == GEMM_ACC_T)) {
     if (P.splits == 1 && P.K > 64) {
       hipLaunchKernelGGL((k_gemm4<T, KMAJ, KMAJ, MODE>), dim3(grid), dim3(kThreads4), 0, s, P);
+      return;
+    }
+  }
+  if constexpr (sizeof(T) == 2 && LA == KMAJ && LB == MNMAJ && (MODE == GEMM_STORE || MODE == GEMM_ACC_T)) {
+    const int64_t lim = 0x7fffffffll / (int64_t)sizeof(T);
+    if (P.splits == 1 && P.K > 64 && !P.B1 && P.b_kval0 * P.ldb < lim) {
+      hipLaunchKernelGGL((k_gemm4<T, KMAJ, MNMAJ, MODE>), dim3(grid), dim3(kThreads4), 0, s, P);
       return;
     }
   }

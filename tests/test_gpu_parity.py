@@ -406,8 +406,8 @@ def test_general_gemm_persistent_many_tiles(dtype):
     from orda_ce_kernel import _native
 
     g = torch.Generator().manual_seed(7)
-    for a_mn, b_mn, M, N, K, splits in ((0, 0, 4104, 4104, 264, 1), (1, 1, 4104, 4104, 200, 1),
-                                        (1, 1, 1040, 2056, 9000, 6)):
+    for a_mn, b_mn, M, N, K, splits in ((0, 0, 4104, 4104, 264, 1), (0, 1, 4104, 4104, 264, 1),
+                                        (1, 1, 4104, 4104, 200, 1), (1, 1, 1040, 2056, 9000, 6)):
         a = torch.randn(M, K, generator=g).to(dtype).cuda()
         b = torch.randn(N, K, generator=g).to(dtype).cuda()
         a_in = a.t().contiguous() if a_mn else a
