@@ -440,6 +440,11 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
 // acc[mb][nb] holds vocabulary rows wm * 128 + mb * 32 + acc_row.  Tokens:
 // tied (TL false) wn * 64 + (nb & 1) * 32 + lane % 32, student for nb < 2,
 // teacher for nb >= 2; student-only tiles (TL) col4(nb, wn) + lane % 32.
+// Every store is a full 8-byte one, made by each quad whose first token is
+// below N: a quad straddling N writes into the padding columns [N, nP) of its
+// half, which the caller zeroes before anything reads them.  (Partial stores
+// in the same loop make the compiler split every full store into a 4-byte
+// and two 2-byte ones under divergent branches.)
 template <class T, bool TL>
 __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams& P, int64_t v0, int64_t t0) {
   const int lane = opaque_lane();
@@ -450,8 +455,7 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
   for (int nb = 0; nb < 4; ++nb) {
     if (!TL && nb >= 2 && !P.store_t) break;
     const int64_t tb = t0 + (TL ? col4(nb, wn) : wn * 64 + (nb & 1) * 32) + (lane & 31) - q;  // quad's first token
-    const int64_t nt = P.N - tb;
-    const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
+    const bool tok_ok = tb < P.N;
     const int64_t col = tb + (!TL && nb >= 2 ? P.tcolL : 0);
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
@@ -462,7 +466,7 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 #pragma unroll
         for (int e = 0; e < 4; ++e) x[e] = acc_get(acc[mb][nb], g * 4 + e);
         quad_transpose(x, o);
-        if (v < P.V && ntok > 0) store4(L + v * P.ldL + col, o, ntok == 4, ntok);
+        if (v < P.V && tok_ok) store4(L + v * P.ldL + col, o, true, 4);
         __builtin_amdgcn_sched_barrier(0);
       }
   }
@@ -483,15 +487,6 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 enum { TL_NONE = 0, TL_FROM_L = 1, TL_FROM_MEM = 2 };
 
 template <class T>
-__device__ __forceinline__ uint2 load_raw4(const T* p, int n) {  // n in 1..4 16-bit elements
-  if (n >= 4) return *reinterpret_cast<const uint2*>(p);
-  const unsigned short* h = reinterpret_cast<const unsigned short*>(p);
-  const unsigned a = h[0];
-  const unsigned b = n > 1 ? (unsigned)h[1] : 0u;
-  const unsigned c = n > 2 ? (unsigned)h[2] : 0u;
-  return make_uint2(a | (b << 16), c);
-}
-template <class T>
 __device__ __forceinline__ void unpack_raw4(uint2 r, float (&x)[4]) {
   union { uint2 u; T e[4]; } v;
   v.u = r;
@@ -508,12 +503,12 @@ __device__ __forceinline__ void issue_teacher4(uint2 (&raw)[16], const FusedPara
     const int q = lane & 3;
     const T* L = static_cast<const T*>(P.Lout);
     const int64_t tb = t0 + col4(nb, wn) + (lane & 31) - q;  // quad's first token
-    const int64_t nt = P.N - tb;
-    const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
+    const bool tok_ok = tb < P.N;  // full loads: tokens past N are never merged
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane) + q;
-      raw[i] = (v < P.V && ntok > 0) ? load_raw4(L + v * P.ldL + P.tcolL + tb, ntok) : make_uint2(0u, 0u);
+      raw[i] = (v < P.V && tok_ok) ? *reinterpret_cast<const uint2*>(L + v * P.ldL + P.tcolL + tb)
+                                   : make_uint2(0u, 0u);
     }
   } else {
     const T* Lt = static_cast<const T*>(P.Lt);
@@ -547,8 +542,7 @@ __device__ __forceinline__ void store_teacher4(const f32x16 (&tv)[4], const Fuse
   const int q = lane & 3;
   T* L = static_cast<T*>(P.Lout);
   const int64_t tb = t0 + col4(nb, wn) + (lane & 31) - q;
-  const int64_t nt = P.N - tb;
-  const int ntok = nt <= 0 ? 0 : (nt >= 4 ? 4 : (int)nt);
+  const bool tok_ok = tb < P.N;  // full stores, as in store_logits4
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane) + q;
@@ -556,7 +550,7 @@ __device__ __forceinline__ void store_teacher4(const f32x16 (&tv)[4], const Fuse
 #pragma unroll
     for (int e = 0; e < 4; ++e) x[e] = tv[i >> 2][(i & 3) * 4 + e];
     quad_transpose(x, o);
-    if (v < P.V && ntok > 0) store4(L + v * P.ldL + P.tcolL + tb, o, ntok == 4, ntok);
+    if (v < P.V && tok_ok) store4(L + v * P.ldL + P.tcolL + tb, o, true, 4);
   }
 }
 struct AccPairTL {  // student from accumulator block nb, teacher from registers
@@ -623,7 +617,7 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
     return x;
   };
   auto opnd = [&](const TI& x, int op) { return op == 0 ? x.a : bop; };
-  auto epilogue = [&](int, const TI& x, Acc4& c) {
+  auto epilogue = [&](int, const TI& x, Acc4& c) __attribute__((always_inline)) {
     const int vlane0 = wm * 128 + (opaque_lane() >> 5) * 4;
     const int64_t vlimit = P.V - x.v0;
     if constexpr (TL != TL_NONE) {
@@ -1106,7 +1100,7 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
     return x;
   };
   auto opnd = [](const TI& x, int op) { return op == 0 ? x.a : x.b; };
-  auto epilogue = [&](int, const TI& x, Acc4& c) {
+  auto epilogue = [&](int, const TI& x, Acc4& c) __attribute__((always_inline)) {
     const int lane = opaque_lane();
     const int wm = w4_m(), wn = w4_n();
     const int64_t ldc = P.ldc;
@@ -1115,23 +1109,35 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
     auto col = [&](int nb, int g) { return (nb >> 1) * 128 + (nb & 1) * 32 + g * 8; };
     if constexpr (MODE == GEMM_SPLIT) {
       float* D = P.C32 + (int64_t)x.split * P.split_stride + (int64_t)x.m0 * ldc + x.n0;
+      // interior tiles take a path with only full 16-byte stores: in one loop
+      // with the ragged-edge stores the compiler merges the two and splits
+      // every full store into narrower ones under divergent branches
+      auto part = [&](auto edge) __attribute__((always_inline)) {
+        constexpr bool E = decltype(edge)::value;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const int mm = wm * 128 + mb * 32 + (lane & 31);
-        float* rp = D + (int64_t)mm * ldc + cl;
+        for (int mb = 0; mb < 4; ++mb) {
+          const int mm = wm * 128 + mb * 32 + (lane & 31);
+          float* rp = D + (int64_t)mm * ldc + cl;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+          for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float o[4];
+            for (int g = 0; g < 4; ++g) {
+              float o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
-            const int rem = nlim - (cl + col(nb, g));
-            const int cnt = rem <= 0 ? 0 : (rem >= 4 ? 4 : rem);
-            if (mm < mlim && cnt > 0) store4(rp + col(nb, g), o, cnt == 4, cnt);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-      }
+              for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
+              if (!E) {
+                store4(rp + col(nb, g), o, true, 4);
+              } else {
+                const int rem = nlim - (cl + col(nb, g));
+                const int cnt = rem <= 0 ? 0 : (rem >= 4 ? 4 : rem);
+                if (mm < mlim && cnt > 0) store4(rp + col(nb, g), o, cnt == 4, cnt);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+      };
+      if (mlim == 256 && nlim == 256) part(std::false_type{});
+      else part(std::true_type{});
       return;
     }
     T* C = static_cast<T*>(P.C) + (int64_t)x.m0 * ldc + x.n0;
