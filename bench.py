@@ -48,13 +48,16 @@ CONFIGS = {
     "c4": ("precomputed", 8192, 4096, 4096, 128256, "bfloat16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
     "c5": ("tied", 32768, 5120, 5120, 152064, "bfloat16", "forward_kl", 1.0, 0.7, None, 0.3, 0.20),
 }
+# config 5: teacher rows scaled by c / tau_n, tau_n ~ U[0.5, 4]; c puts the teacher logit spread at
+# ~6.4 standard deviations for tau = 0.5 (entropy of a few nats) and ~0.8 for tau = 4 (near uniform)
+ROW_TEMPERATURE = {"c5": (0.5, 4.0, 6.4 * 0.5 / (0.02 * 5120 ** 0.5))}
 
 
 def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_inputs(cfg, device, seed):
+def make_inputs(cfg, device, seed, row_tau=None):
     import torch
 
     mode, N, H, Ht, V, dtype_name, *_rest, ignore_frac = cfg
@@ -62,7 +65,11 @@ def make_inputs(cfg, device, seed):
     g = torch.Generator(device=device).manual_seed(seed)
     hs = torch.randn(N, H, generator=g, device=device).to(dtype)
     if mode == "tied":
-        ht = torch.randn(N, H, generator=g, device=device).to(dtype)
+        ht = torch.randn(N, H, generator=g, device=device)
+        if row_tau is not None:
+            lo, hi, c = row_tau
+            ht *= (c / (lo + (hi - lo) * torch.rand(N, generator=g, device=device)))[:, None]
+        ht = ht.to(dtype)
         Wt = None
     else:
         ht = torch.randn(N, Ht, generator=g, device=device).to(dtype)
@@ -96,7 +103,7 @@ def algorithmic_flops(cfg) -> float:
     return 3 * G(H)
 
 
-def run_gpu(cfg, steps, warmup, seed, timing):
+def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None):
     import torch
 
     import orda_ce_kernel as orda
@@ -104,7 +111,7 @@ def run_gpu(cfg, steps, warmup, seed, timing):
 
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, _ = cfg
     device = "cuda"
-    hs, ht, W, Wt, lt, y = make_inputs(cfg, device, seed)
+    hs, ht, W, Wt, lt, y = make_inputs(cfg, device, seed, row_tau)
     hs.requires_grad_(True)
     W.requires_grad_(True)
     if mode == "tied":
@@ -171,7 +178,7 @@ def kernel_report(kern, steps, peak_tflops):
     return rows
 
 
-def cpu_baseline(cfg, seed, budget_s):
+def cpu_baseline(cfg, seed, budget_s, row_tau=None):
     """Time the oracle's unfused torch restatement (fp32) on a token sample."""
     import torch
 
@@ -180,7 +187,7 @@ def cpu_baseline(cfg, seed, budget_s):
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, _ = cfg
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    hs, ht, W, _, _, y = make_inputs(cfg, "cuda", seed)
+    hs, ht, W, _, _, y = make_inputs(cfg, "cuda", seed, row_tau)
     Wc = W.float().cpu()
     hs_c, ht_c, y_c = hs.float().cpu(), ht.float().cpu(), y.cpu()
     del hs, ht, W
@@ -259,6 +266,29 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+SWEEP_DIVERGENCES = ("forward_kl", "reverse_kl", "symmetric_kl", "soft_target_ce", "hellinger", "bhattacharyya",
+                     "renyi", "amari_alpha", "chi_squared", "squared_l2", "ab", "jsd", "skew_forward_kl",
+                     "skew_reverse_kl", "tvd")
+
+
+def sweep(cfg, args, row_tau) -> int:
+    """ms per fwd+bwd step for every divergence at T = 1 and 4 (default
+    alpha/beta: skew 0.1, JSD 0.5), with the kernel-class split."""
+    mode, N, H, Ht, V, dtype_name = cfg[:6]
+    for T in (1.0, 4.0):
+        for div in SWEEP_DIVERGENCES:
+            c = cfg[:6] + (div, T) + cfg[8:]
+            ms, peak_extra, loss, kern = run_gpu(c, args.steps, args.warmup, args.seed, True, row_tau)
+            rows = kernel_report(kern, args.steps, PEAK_BF16_TFLOPS)
+            print(json.dumps({
+                "config": args.config, "divergence": div, "temperature": T, "ms_per_step": ms,
+                "tokens_per_s": N / (ms / 1e3), "step_tflops": algorithmic_flops(c) / (ms / 1e3) / 1e12,
+                "peak_extra_hbm_gb": peak_extra / 1e9, "loss": loss,
+                "ms_per_step_by_class": {k: round(r["ms_per_step"], 4) for k, r in rows.items()},
+            }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -266,6 +296,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--seed", type=int, default=1002)
+    ap.add_argument("--divergence", default=None, help="override the config's divergence (config 4 sweep)")
+    ap.add_argument("--temperature", type=float, default=None, help="override the config's temperature")
+    ap.add_argument("--sweep", action="store_true",
+                    help="instead of the one-line benchmark, time every divergence at T=1 and T=4 on --config "
+                         "(one json line per case; config 4's divergence sweep)")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true")
@@ -285,8 +320,14 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     cfg = CONFIGS[args.config]
+    if args.divergence is not None or args.temperature is not None:
+        cfg = cfg[:6] + (args.divergence or cfg[6], cfg[7] if args.temperature is None else args.temperature) + cfg[8:]
+    row_tau = ROW_TEMPERATURE.get(args.config)
+    if args.sweep:
+        return sweep(cfg, args, row_tau)
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, ignore_frac = cfg
-    ms_step, peak_extra, loss_val, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, not args.no_timing)
+    ms_step, peak_extra, loss_val, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, not args.no_timing,
+                                                 row_tau)
     peak = PEAK_FP32_TFLOPS if dtype_name == "float32" else PEAK_BF16_TFLOPS
     alg = algorithmic_flops(cfg)
     step_tflops = alg / (ms_step / 1e3) / 1e12
@@ -335,9 +376,24 @@ def main() -> int:
         }
         if traffic is not None:
             result["roofline"]["traffic_source"] = f"profiles/{source} (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)"
+        if "dlogits" in kern and kern["dlogits"]["launches"] > 0:
+            # the HBM-bound streaming pass over the materialised logits: student logits read and
+            # dlogits written in place, teacher logits read when the divergence or the teacher CE
+            # needs them, teacher dlogits written when the teacher CE has a gradient
+            es = 4 if dtype_name == "float32" else 2
+            w_t_eff = (1.0 if mode == "tied" else 0.0) if w_t is None else w_t
+            tgrad = w_t_eff != 0.0
+            passes = 2 + (1 if (kl_w != 0.0 or tgrad) else 0) + (1 if tgrad else 0)
+            d = kern["dlogits"]
+            gbs = passes * N * V * es * args.steps / (d["ms"] / 1e3) / 1e9  # every launch of the timed steps
+            result["stream"] = {
+                "bound": "hbm", "kernel": "dlogits", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": gbs / PEAK_HBM_GBS, "algorithmic_bytes_per_step": passes * N * V * es,
+                "mean_launch_ms": d["ms"] / d["launches"],
+            }
     if not args.no_cpu_baseline and mode == "tied":
         _log("[bench] CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(cfg, args.seed, args.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline(cfg, args.seed, args.cpu_budget, row_tau)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -658,6 +658,11 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     M.invT = F.invT; M.temperature = p->temperature; M.alpha = p->div_alpha; M.beta = p->div_beta;
     for (int i = 0; i < 3; ++i) { M.pa[i] = pl.pa[i]; M.pb[i] = pl.pb[i]; }
     M.npow = pl.npow; M.rowp = rowp; M.rowv = rowv + r0; M.ldv = N;
+    // logits the scan computed in fp32 and stored rounded: the student's, and
+    // the teacher's when its GEMM ran inside the scan
+    const int round_code = std::is_same<T, bf16>::value ? 1 : std::is_same<T, f16>::value ? 2 : 0;
+    M.round_s = round_code;
+    M.round_t = tgemm ? round_code : 0;
     { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
 
     if (!any_grad) continue;

@@ -135,6 +135,11 @@ struct MergeParams {
   float* rowp;  // [kNRowP][N]
   float* rowv;  // [3][ldv]: student CE, teacher CE, T^2 * divergence
   int64_t ldv;
+  // dtype the dlogits pass reads the student's / teacher's logits in when the
+  // scan stored them rounded from the fp32 values its statistics came from:
+  // 0 none (fp32, recomputed, or teacher logits read back from memory),
+  // 1 bf16, 2 fp16
+  int round_s, round_t;
 };
 hipError_t launch_merge(const MergeParams& P, hipStream_t s);
 

@@ -11,6 +11,12 @@ namespace orda {
 // order: bit-stable), then forms the row losses and the parameters the
 // dlogits kernel needs.  The final combination runs in fp64 to limit the
 // cancellation in lse_s - lse_t + (cross term).
+// x rounded to nearest-even in bf16 (code 1) or fp16 (code 2), as the
+// logits stores convert it.
+__device__ inline float round_to(float x, int code) {
+  return code == 1 ? (float)(bf16)x : (float)(f16)x;
+}
+
 constexpr int kMergeSlices = 8;
 constexpr int kMergeTok = 32;
 __global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams P) {
@@ -123,10 +129,28 @@ __global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams 
       else c[0] = lp[0];
     }
   }
-  P.rowp[0 * N + t] = (float)lse_s;
-  P.rowp[1 * N + t] = (float)lse_sT;
-  P.rowp[2 * N + t] = (float)lse_t;
-  P.rowp[3 * N + t] = (float)lse_tT;
+  // Normalisers for the dlogits pass.  When it reads logits stored rounded to
+  // 16 bits while lse_* come from the fp32 values, a peaked row's largest
+  // logit carries a rounding error d (|d| up to 2^-9 |x| in bf16) that scales
+  // its probability by e^d, so the row's probabilities stop summing to one
+  // (by up to ~6% at |x| ~ 30).  Adding d * p_max to the normaliser restores
+  // the sum to first order; what remains is the error of a softmax over the
+  // rounded logits.  The losses keep the fp32 normalisers.
+  double g_s = lse_s, g_sT = lse_sT, g_t = lse_t, g_tT = lse_tT;
+  if (P.round_s && S.ms > -kInf) {
+    const double d = (double)round_to(S.ms, P.round_s) - (double)S.ms;
+    g_s += d * exp((double)S.ms - lse_s);
+    g_sT = t1 ? g_s : g_sT + d * invT * exp((double)S.ms * invT - lse_sT);
+  }
+  if (P.round_t && P.has_t && S.mt > -kInf) {
+    const double d = (double)round_to(S.mt, P.round_t) - (double)S.mt;
+    g_t += d * exp((double)S.mt - lse_t);
+    g_tT = t1 ? g_t : g_tT + d * invT * exp((double)S.mt * invT - lse_tT);
+  }
+  P.rowp[0 * N + t] = (float)g_s;
+  P.rowp[1 * N + t] = (float)g_sT;
+  P.rowp[2 * N + t] = (float)g_t;
+  P.rowp[3 * N + t] = (float)g_tT;
   for (int i = 0; i < 4; ++i) P.rowp[(4 + i) * N + t] = (float)c[i];
   P.rowv[0 * P.ldv + t] = (float)ce_s;
   P.rowv[1 * P.ldv + t] = (float)ce_t;

@@ -416,3 +416,31 @@ def test_general_gemm_persistent_many_tiles(dtype):
         ref = a.float() @ b.float().t()
         err = (c - ref).abs().max().item()
         assert err <= 2e-2 * max(1.0, ref.abs().max().item()), (a_mn, b_mn, M, N, K, splits, err)
+
+
+def test_peaked_rows_dlogits_sum_to_zero_within_rounding():
+    """Softmax dlogits of a row sum to zero (shift invariance), so with a
+    constant column in W the gradient along that column vanishes.  Peaked
+    teacher rows with logits up to ~33 (bf16 ulp 0.25) stress the normaliser
+    the dlogits pass uses: it must describe the logits as stored (rounded to
+    bf16), not the fp32 values the statistics came from.  Emulation of this
+    case: with fp32 normalisers the column reaches ~12% of the largest
+    gradient entry; with the max-element correction ~4.4% (the rest is the
+    rounding of the other logits)."""
+    o = _orda()
+    g = torch.Generator().manual_seed(21)
+    N, H, V = 128, 64, 4000
+    W = torch.randn(V, H, generator=g) / H ** 0.5
+    W[:, 0] = 1.0
+    ht = torch.randn(N, H, generator=g) * 6.4
+    hs = torch.randn(N, H, generator=g) * 3.0
+    y = torch.randint(0, V, (N,), generator=g)
+    hs_d, ht_d, W_d = (x.bfloat16().cuda().requires_grad_(True) for x in (hs, ht, W))
+    out = o.distillation_loss(hs_d, W_d, y.cuda(), o.TiedTeacher(ht_d), kl_weight=1.0, backend="triton")
+    out.loss.backward()
+    torch.cuda.synchronize()
+    for name, gr in (("grad_teacher_hidden", ht_d.grad), ("grad_student_hidden", hs_d.grad)):
+        gr = gr.float()
+        ratio = float(gr[:, 0].abs().max() / gr[:, 1:].abs().max())
+        print(f"{name}: max |column 0| / max |other columns| = {ratio:.4f}")
+        assert ratio < 0.08, (name, ratio)
