@@ -260,10 +260,25 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.f_tpr = (int)cdiv(pl.n_vtiles, nvr);
     pl.f_nvr = (int)cdiv(pl.n_vtiles, pl.f_tpr);
     auto split_plan = [&](int64_t cols, int& splits, int64_t& kps) {
+      // The persistent GEMM runs its tiles x splits equal work items in
+      // rounds of kFusedScanGroups workgroups, so its time goes as
+      // ceil(items / groups) / splits: pick the split count (1..16) that
+      // minimises it (a partial last round idles CUs: 80 tiles x 7 splits is
+      // 3 rounds at 73% fill, x 16 is 5 full ones), the one nearest
+      // kSplitTargetGroups / tiles among equals.
       const int64_t tiles = cdiv(n, 256) * cdiv(cols, 256);
-      int64_t sp = cdiv(kSplitTargetGroups, tiles);
-      if (sp > 16) sp = 16;
-      if (sp < 1) sp = 1;
+      int64_t want = cdiv(kSplitTargetGroups, tiles);
+      if (want > 16) want = 16;
+      int64_t sp = 1;
+      double best = 1e30;
+      for (int64_t c = 1; c <= 16; ++c) {
+        const double cost = (double)cdiv(tiles * c, kFusedScanGroups) / (double)c;
+        const bool nearer = std::llabs(c - want) < std::llabs(sp - want);
+        if (cost < best * (1.0 - 1e-9) || (cost <= best * (1.0 + 1e-9) && nearer)) {
+          best = cost;
+          sp = c;
+        }
+      }
       kps = round_up(cdiv(pl.V, sp), 64);
       splits = (int)cdiv(pl.V, kps);
     };
