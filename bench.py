@@ -266,6 +266,7 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+TWO_PASS = ("jsd", "skew_forward_kl", "skew_reverse_kl", "tvd")
 SWEEP_DIVERGENCES = ("forward_kl", "reverse_kl", "symmetric_kl", "soft_target_ce", "hellinger", "bhattacharyya",
                      "renyi", "amari_alpha", "chi_squared", "squared_l2", "ab", "jsd", "skew_forward_kl",
                      "skew_reverse_kl", "tvd")
@@ -384,6 +385,8 @@ def main() -> int:
             w_t_eff = (1.0 if mode == "tied" else 0.0) if w_t is None else w_t
             tgrad = w_t_eff != 0.0
             passes = 2 + (1 if (kl_w != 0.0 or tgrad) else 0) + (1 if tgrad else 0)
+            if kl_w != 0.0 and div in TWO_PASS:
+                passes += 2  # the second pass of the two-pass divergences reads both halves again
             d = kern["dlogits"]
             gbs = passes * N * V * es * args.steps / (d["ms"] / 1e3) / 1e9  # every launch of the timed steps
             result["stream"] = {

@@ -81,8 +81,9 @@ enum orda_divergence {
  * fp32_grad_weight_accumulation=False, ops/tied_teacher.py:354,488-495).
  * orda_backward then only multiplies the gradients by grad_output
  * (ops/tied_teacher.py:531-564).  Every mode (a precomputed teacher's logits
- * are stored beside the student's in the compute dtype); not the two-pass
- * divergences (JSD, skew KLs, TVD): those return ORDA_EUNSUPPORTED. */
+ * are stored beside the student's in the compute dtype) and every divergence
+ * (the two-pass ones, JSD, skew KLs and TVD, take their second pass over the
+ * chunk's stored logits). */
 #define ORDA_GRADS_IN_FORWARD (1u << 7)
 
 /* Error codes. */

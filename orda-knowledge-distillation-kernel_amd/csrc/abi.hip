@@ -230,8 +230,6 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // precomputed teachers: no teacher gradient; their logits (memory or the
     // frozen teacher GEMM) are stored next to the student's like a tied
     // teacher's
-    if (pl.two_pass)
-      return fail(ORDA_EUNSUPPORTED, "ORDA_GRADS_IN_FORWARD does not support the two-pass divergences");
     pl.store_t = pl.tsrc != TSRC_NONE;
     const int64_t ncol = pl.store_t ? 2 : 1;
     const int64_t Nr = round_up(pl.N, 8);
@@ -679,6 +677,19 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     M.round_s = round_code;
     M.round_t = tgemm ? round_code : 0;
     { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
+    if (pl.two_pass) {
+      // the two-pass divergences' row sums over the stored logits, then the
+      // merge of their partial states into D and the dlogits row constants
+      TwoParams Q{};
+      Q.L = L; Q.ldL = ldL; Q.tcol = nP; Q.rowp = rowp; Q.partial = part;
+      Q.N = nc; Q.V = V; Q.rows_per_range = (int64_t)pl.f_tpr * 256; Q.n_ranges = pl.f_nvr; Q.div = pl.div;
+      Q.invT = F.invT;
+      Q.lw = pl.div == DIV_JSD ? F.log_beta : F.log_alpha;
+      Q.l1mw = pl.div == DIV_JSD ? F.log_1m_beta : F.log_1m_alpha;
+      { Timed tm_(ORDA_K_DLOGITS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_two<T>(Q, s)); }
+      M.phase = 1;
+      { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
+    }
 
     if (!any_grad) continue;
 

@@ -235,6 +235,34 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
 
 // Phase 1 (two-pass divergences): sums of terms of the normalised
 // probabilities, given the row log-normalisers from phase 0.
+// One vocabulary row's terms of the two-pass divergences' row sums (x0, x1),
+// from normalised log-probabilities at temperature T.  lw, l1mw: log w and
+// log(1 - w) of the mixture weight (beta for JSD, alpha for the skew KLs).
+//   JSD:    x0 += p_t (l_t - l_m), x1 += p_s (l_s - l_m), m = b p_t + (1-b) p_s
+//   skew-F: x0 += p_t (l_t - l_m), x1 += p_s p_t / m,     m = a p_t + (1-a) p_s
+//   skew-R: x0 += p_s (l_s - l_m), x1 += p_s p_s / m,     m = a p_s + (1-a) p_t
+//   TVD:    x0 += |p_t - p_s|,     x1 += p_s sign(p_s - p_t)
+template <int DIV>
+__device__ __forceinline__ void two_term(float lps, float lpt, float lw, float l1mw, float& s0, float& s1) {
+  const float ps = fexp(lps), pt = fexp(lpt);
+  if constexpr (DIV == DIV_JSD) {
+    const float lm = logaddexp(lw + lpt, l1mw + lps);
+    s0 += pt * (lpt - lm);
+    s1 += ps * (lps - lm);
+  } else if constexpr (DIV == DIV_SKEW_F) {
+    const float lm = logaddexp(lw + lpt, l1mw + lps);
+    s0 += pt * (lpt - lm);
+    s1 += ps * fexp(lpt - lm);
+  } else if constexpr (DIV == DIV_SKEW_R) {
+    const float lm = logaddexp(lw + lps, l1mw + lpt);
+    s0 += ps * (lps - lm);
+    s1 += ps * fexp(lps - lm);
+  } else {  // TVD
+    s0 += fabsf(pt - ps);
+    s1 += (ps > pt) ? ps : ((ps < pt) ? -ps : 0.f);
+  }
+}
+
 template <int DIV, bool MASK, class AP>
 __device__ __forceinline__ void rowsum_tile(RowState& S, const AP& acc, int vlane0, int64_t vlimit,
                                             float lse_sT, float lse_tT, const FusedParams& P) {
@@ -247,23 +275,8 @@ __device__ __forceinline__ void rowsum_tile(RowState& S, const AP& acc, int vlan
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
       const float lps = acc.s(mb, r) * invT - lse_sT;
       const float lpt = acc.t(mb, r) * invT - lse_tT;
-      const float ps = fexp(lps), pt = fexp(lpt);
-      if constexpr (DIV == DIV_JSD) {
-        const float lm = logaddexp(P.log_beta + lpt, P.log_1m_beta + lps);
-        s0 += pt * (lpt - lm);
-        s1 += ps * (lps - lm);
-      } else if constexpr (DIV == DIV_SKEW_F) {
-        const float lm = logaddexp(P.log_alpha + lpt, P.log_1m_alpha + lps);
-        s0 += pt * (lpt - lm);
-        s1 += ps * fexp(lpt - lm);
-      } else if constexpr (DIV == DIV_SKEW_R) {
-        const float lm = logaddexp(P.log_alpha + lps, P.log_1m_alpha + lpt);
-        s0 += ps * (lps - lm);
-        s1 += ps * fexp(lps - lm);
-      } else {  // TVD
-        s0 += fabsf(pt - ps);
-        s1 += (ps > pt) ? ps : ((ps < pt) ? -ps : 0.f);
-      }
+      two_term<DIV>(lps, lpt, DIV == DIV_JSD ? P.log_beta : P.log_alpha,
+                    DIV == DIV_JSD ? P.log_1m_beta : P.log_1m_alpha, s0, s1);
     }
   S.x[0] += s0;
   S.x[1] += s1;
@@ -1245,6 +1258,89 @@ __global__ __launch_bounds__(256) void k_scale(T* __restrict__ x, int64_t n, con
   }
 }
 
+// ------------------------------------- two-pass row sums on stored logits
+// Phase 1 of the two-pass divergences (JSD, skew KLs, TVD) for the
+// gradients-in-forward schedule: the row sums x0, x1 over a token chunk's
+// stored logits L[v][t] (student columns [0, N), teacher columns
+// [tcol, tcol + N)), normalised with phase 0's log-sum-exps (rowp rows 1
+// and 3), with the same per-row terms as the two-phase scan (two_term).
+// One partial state (slots x0, x1) per (vocabulary range, token) for
+// k_merge's phase 1.  Block: 16 token quads x 64 row lanes (1024 threads:
+// enough waves in flight for a latency-bound stream), grid: (groups of 64
+// tokens, vocabulary ranges); a thread reads 4 tokens of every 64th row of
+// its range (8-byte loads for 16-bit logits; a wave covers 4 rows x 128
+// contiguous bytes), 4 rows in flight, and the 64 row lanes' sums are added
+// in a fixed order (bit-stable).
+constexpr int kTwoLanes = 64;
+template <class T, int DIV>
+__global__ __launch_bounds__(16 * kTwoLanes) void k_two_rows(TwoParams P) {
+  __shared__ float xch[2][kTwoLanes][64];
+  const int tq = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int64_t tb = (int64_t)blockIdx.x * 64 + tq * 4;
+  const int64_t v0 = (int64_t)blockIdx.y * P.rows_per_range;
+  const int64_t v1 = min<int64_t>(P.V, v0 + P.rows_per_range);
+  const int64_t rem = P.N - tb;
+  const int nt = rem <= 0 ? 0 : (rem >= 4 ? 4 : (int)rem);
+  const float invT = P.invT;
+  float lse_sT[4], lse_tT[4], s0[4], s1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t t = i < nt ? tb + i : 0;
+    lse_sT[i] = P.rowp[1 * P.N + t];
+    lse_tT[i] = P.rowp[3 * P.N + t];
+    s0[i] = 0.f;
+    s1[i] = 0.f;
+  }
+  const T* Ls = static_cast<const T*>(P.L) + (nt > 0 ? tb : 0);
+  const T* Lt = Ls + P.tcol;
+  auto rows = [&](const float (&xs)[4], const float (&xt)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      two_term<DIV>(xs[i] * invT - lse_sT[i], xt[i] * invT - lse_tT[i], P.lw, P.l1mw, s0[i], s1[i]);
+  };
+  if (nt > 0) {
+    int64_t v = v0 + rl;
+    constexpr int R = 4;
+    for (; v + kTwoLanes * (R - 1) < v1; v += kTwoLanes * R) {
+      float xs[R][4], xt[R][4];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        load4(Ls + (v + kTwoLanes * r) * P.ldL, xs[r], nt == 4, nt);
+        load4(Lt + (v + kTwoLanes * r) * P.ldL, xt[r], nt == 4, nt);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) rows(xs[r], xt[r]);
+    }
+    for (; v < v1; v += kTwoLanes) {
+      float xs[4], xt[4];
+      load4(Ls + v * P.ldL, xs, nt == 4, nt);
+      load4(Lt + v * P.ldL, xt, nt == 4, nt);
+      rows(xs, xt);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xch[0][rl][tq * 4 + i] = s0[i];
+    xch[1][rl][tq * 4 + i] = s1[i];
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int tk = threadIdx.x;
+    const int64_t t = (int64_t)blockIdx.x * 64 + tk;
+    float a = 0.f, b = 0.f;
+#pragma unroll 8
+    for (int r = 0; r < kTwoLanes; ++r) {
+      a += xch[0][r][tk];
+      b += xch[1][r][tk];
+    }
+    if (t < P.N) {
+      float* dst = P.partial + (int64_t)blockIdx.y * kNStat * P.N + t;
+      dst[6 * P.N] = a;  // RowState x[0]
+      dst[7 * P.N] = b;  // RowState x[1]
+    }
+  }
+}
+
 // ------------------------------------------------- materialised dlogits
 // In place on the logits L[v][t] of one token chunk (vocabulary-major,
 // student columns [0, N), teacher columns [tcol, tcol + N)): student
@@ -1647,6 +1743,21 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
       ORDA_DLM_CASE(T, DIV_CHI2)                                                           \
       ORDA_DLM_CASE(T, DIV_L2)                                                             \
       ORDA_DLM_CASE(T, DIV_AB)                                                             \
+      ORDA_DLM_CASE(T, DIV_JSD)                                                            \
+      ORDA_DLM_CASE(T, DIV_SKEW_F)                                                         \
+      ORDA_DLM_CASE(T, DIV_SKEW_R)                                                         \
+      ORDA_DLM_CASE(T, DIV_TVD)                                                            \
+      default: return hipErrorInvalidValue;                                                \
+    }                                                                                      \
+    return hipGetLastError();                                                              \
+  }                                                                                        \
+  template <> hipError_t launch_two<T>(const TwoParams& P, hipStream_t s) {                \
+    const dim3 grid((unsigned)((P.N + 63) / 64), (unsigned)P.n_ranges);                   \
+    switch (P.div) {                                                                       \
+      case DIV_JSD: hipLaunchKernelGGL((k_two_rows<T, DIV_JSD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+      case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_F>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+      case DIV_SKEW_R: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_R>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+      case DIV_TVD: hipLaunchKernelGGL((k_two_rows<T, DIV_TVD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
       default: return hipErrorInvalidValue;                                                \
     }                                                                                      \
     return hipGetLastError();                                                              \

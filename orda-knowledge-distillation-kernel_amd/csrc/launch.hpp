@@ -94,6 +94,17 @@ struct DlmParams {
   float invT, temperature, alpha, beta, w_s, w_t, w_kl;
 };
 
+// Phase-1 row sums of the two-pass divergences over stored logits (k_two_rows).
+struct TwoParams {
+  const void* L;  // [V][ldL]; student columns [0, N), teacher columns [tcol, tcol + N)
+  int64_t ldL, tcol;
+  const float* rowp;  // [kNRowP][N]: rows 1 and 3 = log-sum-exps at T
+  float* partial;     // [n_ranges][kNStat][N]: slots 6, 7 written
+  int64_t N, V, rows_per_range;
+  int n_ranges, div;
+  float invT, lw, l1mw;  // log w, log(1 - w) of the mixture weight
+};
+
 struct LabelParams {
   const void* hs;
   const void* W;
@@ -113,6 +124,7 @@ template <class T> hipError_t launch_label(const LabelParams& P, hipStream_t s);
 template <class T> hipError_t launch_scan_store(const FusedParams& P, int grid, hipStream_t s);
 template <class T> hipError_t launch_gemm2(const GemmParams& P, hipStream_t s);
 template <class T> hipError_t launch_dlm(const DlmParams& P, hipStream_t s);
+template <class T> hipError_t launch_two(const TwoParams& P, hipStream_t s);
 template <class T>
 hipError_t launch_splitk_reduce(const float* part, int splits, int64_t stride, void* out, int64_t ldo, int64_t M,
                                 int64_t N, hipStream_t s);

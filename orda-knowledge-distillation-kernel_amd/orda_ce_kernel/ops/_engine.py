@@ -9,8 +9,9 @@ Two schedules, chosen per call by :func:`grads_in_forward`:
   turns them into dlogits in place and multiplies them into the gradients,
   accumulating grad W across chunks in the weight dtype as the reference's
   ``addmm_`` does; backward only multiplies by ``grad_output``;
-* two-phase (``fp32_grad_weight_accumulation=True``, precomputed teachers,
-  the two-pass divergences, and forward-only calls): ``orda_forward``
+* two-phase (``fp32_grad_weight_accumulation=True``, precomputed logits
+  in another dtype than the compute dtype, and forward-only calls):
+  ``orda_forward``
   computes the losses with an online-softmax scan (no logits stored) and
   ``orda_backward`` recomputes the logits per vocabulary chunk, so every
   grad W element is one fp32-accumulated GEMM rounded once.
@@ -77,13 +78,9 @@ def grads_in_forward(mode: str, use_fp32_accum, divergence, any_grad: bool) -> b
     stored beside the student's for the chunk's dlogits, so the precomputed
     logits caller checks that their dtype is the compute dtype).
     """
-    from ..divergences import TWO_PASS
-
     if not any_grad or bool(use_fp32_accum):
         return False
-    if mode not in ("tied", "separate", "precomputed_logits", "precomputed_hidden"):
-        return False
-    return resolve_divergence(divergence).name not in TWO_PASS
+    return mode in ("tied", "separate", "precomputed_logits", "precomputed_hidden")
 
 
 def _kelems(dtype: torch.dtype) -> int:

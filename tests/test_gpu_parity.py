@@ -290,7 +290,8 @@ def test_grads_in_forward_over_ragged_token_chunks(dtype, mode):
     ragged (zeroed padding columns), grad W accumulated across chunks."""
     from orda_ce_kernel import KernelConfig
 
-    for div in ("forward_kl", "reverse_kl", "hellinger", "squared_l2"):
+    for div in ("forward_kl", "reverse_kl", "hellinger", "squared_l2", "jsd", "skew_forward_kl", "skew_reverse_kl",
+                "tvd"):
         out, ref, hs, W, teacher = _run(mode, dtype, Ht=72 if mode == "separate" else None, T=1.3, kl_w=0.6,
                                         w_t=0.5, div=div, config=KernelConfig(chunk_size=20))
         _check(out, ref, hs, W, dtype)
@@ -300,15 +301,18 @@ def test_grads_in_forward_over_ragged_token_chunks(dtype, mode):
             _close_grad(teacher.weight.grad, ref["grad_teacher_weight"], "grad_teacher_weight", tol)
 
 
-def test_schedules_agree_on_a_larger_problem():
+@pytest.mark.parametrize("div, T", [("forward_kl", 1.0), ("jsd", 2.0), ("skew_reverse_kl", 1.0)])
+def test_schedules_agree_on_a_larger_problem(div, T):
     """N=600 tokens, V=5000, H=256 (several vocabulary tiles, split-K grad
-    hidden, 3 token chunks): balanced vs debug gradients."""
+    hidden, 3 token chunks): balanced vs debug gradients, for a one-pass
+    divergence and two two-pass ones (second pass over the stored logits vs
+    over recomputed ones)."""
     from orda_ce_kernel import KernelConfig
 
     res = {}
     for profile, cfg in (("balanced", KernelConfig(chunk_size=128)), ("debug", None)):
-        out, ref, hs, W, teacher = _run("tied", torch.bfloat16, N=600, H=256, V=5000, T=1.0, kl_w=1.0, w_t=1.0,
-                                        config=cfg, profile=profile, seed=3)
+        out, ref, hs, W, teacher = _run("tied", torch.bfloat16, N=600, H=256, V=5000, T=T, kl_w=1.0, w_t=1.0,
+                                        config=cfg, profile=profile, seed=3, div=div)
         _check(out, ref, hs, W, torch.bfloat16)
         res[profile] = (hs.grad.float(), W.grad.float(), teacher.hidden.grad.float())
     for a, b in zip(res["balanced"], res["debug"]):
@@ -342,9 +346,9 @@ def test_staged_teacher_logits_feed_the_student_scan(dtype, mode):
 
     grad_teacher = mode == "separate"
     cases = [("forward_kl", 1.0, 5000), ("forward_kl", 2.0, 5000), ("reverse_kl", 1.0, 5000),
-             ("squared_l2", 2.0, 5000), ("hellinger", 1.0, 5000)]
+             ("squared_l2", 2.0, 5000), ("hellinger", 1.0, 5000), ("jsd", 2.0, 5000), ("skew_reverse_kl", 1.0, 5000)]
     if mode == "precomputed_logits":
-        cases += [("forward_kl", 1.0, 4998), ("reverse_kl", 2.0, 4998)]
+        cases += [("forward_kl", 1.0, 4998), ("reverse_kl", 2.0, 4998), ("skew_forward_kl", 2.0, 4998)]
     for div, T, V in cases:
         out, ref, hs, W, teacher = _run(mode, dtype, N=600, H=128, Ht=192, V=V, T=T, kl_w=0.8,
                                         w_t=0.4 if grad_teacher else None, div=div, grad_teacher=grad_teacher,
