@@ -70,7 +70,7 @@ struct Plan {
   int64_t NP, ldT, ldh, Vc, nchunks;
   size_t off_hT, off_htT, off_dLT, off_dLNs, off_dLNt, off_WT, off_WtT, off_g32s, off_g32t, bwd_bytes;
   // gradients inside forward (materialised token chunks)
-  bool fused, store_t, f_tl;
+  bool fused, store_t, f_tl, f_tmem;
   int64_t fn, fnP, fldL, fnchunks;
   int f_nvr, f_tpr, splits_s, splits_t;
   int64_t kps_s, kps_t;
@@ -81,6 +81,7 @@ struct Plan {
 constexpr int kScalFloats = 64;  // scalars at the head of the saved buffer
 
 int make_plan(const orda_problem_t* p, Plan& pl) {
+  pl = Plan{};
   if (!p) return fail(ORDA_EINVAL, "problem is NULL");
   if (p->abi_version != ORDA_ABI_VERSION)
     return fail(ORDA_EINVAL, "abi_version %d does not match library version %d", p->abi_version,
@@ -230,12 +231,24 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // precomputed teachers: no teacher gradient; their logits (memory or the
     // frozen teacher GEMM) are stored next to the student's like a tied
     // teacher's
-    pl.store_t = pl.tsrc != TSRC_NONE;
+    // A separate teacher's logits (its own GEMM) or precomputed logits of the
+    // model dtype are staged into L's teacher columns ahead of the scan, which
+    // then runs the student GEMM alone on the ring engine, 256 tokens per
+    // workgroup (16-bit, K > 64, one-pass non-power divergences).
+    pl.f_tl = pl.eb == 2 && pl.H > 64 && pl.fam != FAM_POW &&
+              ((pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype) || pl.tsrc == TSRC_SEP);
+    // Precomputed logits with V a multiple of 8 are not staged at all: the
+    // scan and the dlogits pass both read them in place, token-major (16-byte
+    // aligned rows), so L holds only the student's logits and a chunk holds
+    // twice the tokens in the same memory (grad W then runs half as many
+    // read-modify-write passes with twice the K).
+    pl.f_tmem = pl.f_tl && pl.tsrc == TSRC_MEM && pl.V % 8 == 0 && !pl.two_pass;
+    pl.store_t = pl.tsrc != TSRC_NONE && !pl.f_tmem;
     const int64_t ncol = pl.store_t ? 2 : 1;
     const int64_t Nr = round_up(pl.N, 8);
     int64_t n = p->token_chunk;
     if (n > 0) {
-      n = round_up(n, 8);
+      n = round_up(n * (pl.f_tmem ? 2 : 1), 8);
     } else {
       n = kFusedLogitsBytes / (pl.V * ncol * pl.eb) / 128 * 128;
       if (n < 128) n = 128;
@@ -245,12 +258,6 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.fnP = round_up(n, 8);
     pl.fldL = ncol * pl.fnP;
     pl.fnchunks = cdiv(pl.N, n);
-    // A separate teacher's logits (its own GEMM) or precomputed logits of the
-    // model dtype are staged into L's teacher columns ahead of the scan, which
-    // then runs the student GEMM alone on the ring engine, 256 tokens per
-    // workgroup (16-bit, K > 64, one-pass non-power divergences).
-    pl.f_tl = pl.eb == 2 && pl.H > 64 && pl.fam != FAM_POW &&
-              ((pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype) || pl.tsrc == TSRC_SEP);
     const int64_t ntt = cdiv(n, pl.f_tl ? 256 : 128);
     int64_t nvr = cdiv(kFusedScanGroups, ntt);
     if (nvr < 1) nvr = 1;
@@ -606,6 +613,8 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
   const T* W = static_cast<const T*>(t->weight);
   const T* Wt = static_cast<const T*>(t->teacher_weight);
 
+  if (pl.f_tmem && reinterpret_cast<uintptr_t>(t->teacher_logits) % 16 != 0)
+    return fail(ORDA_EINVAL, "precomputed teacher logits must be 16-byte aligned when the vocabulary is a multiple of 8");
   // mean scale first: the chunks' dlogits need it before the loss rows exist
   { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_count(t->labels, N, p->ignore_index, reduction_sum, scal, s)); }
 
@@ -646,7 +655,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       // the chunk's teacher logits go to L[:, nP + t] (vocabulary-major) ahead
       // of the scan (teacher GEMM, transpose) or through it
       char* Lt = L + nP * eb;
-      if (pl.tsrc == TSRC_MEM && V % 4 == 0 && reinterpret_cast<uintptr_t>(t->teacher_logits) % 8 == 0) {
+      if (pl.f_tmem || (pl.tsrc == TSRC_MEM && V % 4 == 0 && reinterpret_cast<uintptr_t>(t->teacher_logits) % 8 == 0)) {
         // read token-major by the scan itself (8-byte loads of 4 rows), which
         // writes them to L on the way
         F.tsrc = TSRC_MEM_RING;
@@ -697,7 +706,9 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     D.L = L; D.ldL = ldL; D.tcol = nP; D.labels = t->labels + r0; D.rowp = rowp; D.mean_scale = scal;
     D.N = nc; D.V = V; D.ignore_index = p->ignore_index;
     D.div = pl.div; D.t_is_one = pl.t1; D.tgrad = tgrad;
-    D.rows_per_block = (int)std::max<int64_t>(64, cdiv(V, 65535));  // grid.y stays <= 65535
+    D.rows_per_block = (int)round_up(std::max<int64_t>(64, cdiv(V, 65535)), 8);  // grid.y stays <= 65535
+    D.Ltm = pl.f_tmem ? Ltc : nullptr;
+    D.ldtm = V;
     D.invT = F.invT; D.temperature = p->temperature; D.alpha = p->div_alpha; D.beta = p->div_beta;
     D.w_s = p->student_ce_weight; D.w_t = p->teacher_ce_weight; D.w_kl = pl.div_on ? p->kl_weight : 0.f;
     { Timed tm_(ORDA_K_DLOGITS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_dlm<T>(D, s)); }

@@ -642,7 +642,9 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
         if constexpr (j + 1 < NJ) issue_teacher4<T, TL>(raw[(j + 1) & 1], P, x.v0, t0, j + 1);
         f32x16 tv[4];
         finish_teacher4<T, TL>(raw[j & 1], tv);
-        if constexpr (TL == TL_FROM_MEM) store_teacher4<T>(tv, P, x.v0, t0, j);
+        if constexpr (TL == TL_FROM_MEM) {
+          if (P.store_t) store_teacher4<T>(tv, P, x.v0, t0, j);  // else the dlogits pass reads them in place
+        }
         scan_variant<SV>(st[j], AccPairTL{c, j, tv}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
       });
     } else {
@@ -1342,45 +1344,41 @@ __global__ __launch_bounds__(16 * kTwoLanes) void k_two_rows(TwoParams P) {
 }
 
 // ------------------------------------------------- materialised dlogits
-// In place on the logits L[v][t] of one token chunk (vocabulary-major,
-// student columns [0, N), teacher columns [tcol, tcol + N)): student
-// dlogits w_s (p_s - 1_y) + w_kl T dD/dz_s and teacher dlogits
+// Row parameters of 4 consecutive tokens and their dlogits for one
+// vocabulary row: student w_s (p_s - 1_y) + w_kl T dD/dz_s, teacher
 // w_t (p_t - 1_y), times mean_scale (the caller's grad_output is applied
-// later).  Ignored rows give 0.  Thread: 4 consecutive tokens x
-// rows_per_block vocabulary rows; block: 256 threads = 1024 tokens.
-template <class T, int DIV, bool T1>
-__global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
-  const int64_t t0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (t0 >= P.N) return;
-  const int nt = (int)min<int64_t>(P.N - t0, 4);
-  const int64_t v0 = (int64_t)blockIdx.y * P.rows_per_block;
-  const int64_t v1 = min<int64_t>(P.V, v0 + P.rows_per_block);
-  const float scale = P.mean_scale[0];
-  const float invT = P.invT;
+// later); ignored tokens (and tokens past the quad's nt) give 0.
+template <int DIV, bool T1>
+struct DlmQuad {
   int64_t yeff[4];
   float lse_s[4], lse_sT[4], lse_t[4], lse_tT[4], c[4][4], sc_s[4], sc_t[4], sc_d[4];
+  float invT, alpha, beta;
+
+  __device__ __forceinline__ void init(const DlmParams& P, int64_t t0, int nt) {
+    const float scale = P.mean_scale[0];
+    invT = P.invT;
+    alpha = P.alpha;
+    beta = P.beta;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bool ok = i < nt;
-    const int64_t t = t0 + (ok ? i : 0);
-    const int64_t y = P.labels[t];
-    const bool ign = !ok || y == P.ignore_index;
-    yeff[i] = (y >= 0 && y < P.V) ? y : 0;
-    lse_s[i] = P.rowp[0 * P.N + t];
-    lse_sT[i] = P.rowp[1 * P.N + t];
-    lse_t[i] = P.rowp[2 * P.N + t];
-    lse_tT[i] = P.rowp[3 * P.N + t];
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = i < nt;
+      const int64_t t = t0 + (ok ? i : 0);
+      const int64_t y = P.labels[t];
+      const bool ign = !ok || y == P.ignore_index;
+      yeff[i] = (y >= 0 && y < P.V) ? y : 0;
+      lse_s[i] = P.rowp[0 * P.N + t];
+      lse_sT[i] = P.rowp[1 * P.N + t];
+      lse_t[i] = P.rowp[2 * P.N + t];
+      lse_tT[i] = P.rowp[3 * P.N + t];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) c[i][k] = P.rowp[(4 + k) * P.N + t];
-    sc_s[i] = ign ? 0.f : scale * P.w_s;
-    sc_t[i] = ign ? 0.f : scale * P.w_t;
-    sc_d[i] = ign ? 0.f : scale * P.w_kl * P.temperature;
+      for (int k = 0; k < 4; ++k) c[i][k] = P.rowp[(4 + k) * P.N + t];
+      sc_s[i] = ign ? 0.f : scale * P.w_s;
+      sc_t[i] = ign ? 0.f : scale * P.w_t;
+      sc_d[i] = ign ? 0.f : scale * P.w_kl * P.temperature;
+    }
   }
-  T* Ls = static_cast<T*>(P.L) + t0;
-  T* Lt = Ls + P.tcol;
-  const bool need_t = DIV >= 0 || P.tgrad;
-  // dlogits of one row from its loaded logits (4 tokens)
-  auto row = [&](int64_t v, const float (&xs)[4], const float (&xt)[4], float (&ds)[4], float (&dt)[4]) {
+  __device__ __forceinline__ void row(int64_t v, const float (&xs)[4], const float (&xt)[4], float (&ds)[4],
+                                      float (&dt)[4]) const {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float onehot = (v == yeff[i]) ? 1.f : 0.f;
@@ -1391,12 +1389,30 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
         const float lpt = xt[i] * invT - lse_tT[i];
         const float psT = T1 ? ps1 : fexp(lps);
         const float ptT = fexp(lpt);
-        d += sc_d[i] * div_grad<DIV>(lps, lpt, psT, ptT, c[i], P.alpha, P.beta);
+        d += sc_d[i] * div_grad<DIV>(lps, lpt, psT, ptT, c[i], alpha, beta);
       }
       ds[i] = d;
       dt[i] = sc_t[i] * (fexp(xt[i] - lse_t[i]) - onehot);
     }
-  };
+  }
+};
+
+// In place on the logits L[v][t] of one token chunk (vocabulary-major,
+// student columns [0, N), teacher columns [tcol, tcol + N)): the dlogits of
+// DlmQuad.  Thread: 4 consecutive tokens x rows_per_block vocabulary rows;
+// block: 256 threads = 1024 tokens.
+template <class T, int DIV, bool T1>
+__global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
+  const int64_t t0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (t0 >= P.N) return;
+  const int nt = (int)min<int64_t>(P.N - t0, 4);
+  const int64_t v0 = (int64_t)blockIdx.y * P.rows_per_block;
+  const int64_t v1 = min<int64_t>(P.V, v0 + P.rows_per_block);
+  DlmQuad<DIV, T1> q;
+  q.init(P, t0, nt);
+  T* Ls = static_cast<T*>(P.L) + t0;
+  T* Lt = Ls + P.tcol;
+  const bool need_t = DIV >= 0 || P.tgrad;
   int64_t v = v0;
   if (nt == 4) {
     // interior: R rows per iteration, every load issued before any use
@@ -1415,7 +1431,7 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float ds[4], dt[4];
-        row(v + r, xs[r], xt[r], ds, dt);
+        q.row(v + r, xs[r], xt[r], ds, dt);
         store4(Ls + (v + r) * P.ldL, ds, true, 4);
         if (P.tgrad) store4(Lt + (v + r) * P.ldL, dt, true, 4);
       }
@@ -1426,12 +1442,71 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
     float xs[4], xt[4] = {0.f, 0.f, 0.f, 0.f}, ds[4], dt[4];
     load4(Ls + v * P.ldL, xs, nt == 4, nt);
     if (need_t) load4(Lt + v * P.ldL, xt, nt == 4, nt);
-    row(v, xs, xt, ds, dt);
+    q.row(v, xs, xt, ds, dt);
     store4(Ls + v * P.ldL, ds, nt == 4, nt);
     if (P.tgrad) store4(Lt + v * P.ldL, dt, nt == 4, nt);
   }
 }
 
+// The same dlogits with the teacher's logits read in place from the caller's
+// precomputed [N x ldtm] tensor (token-major; no teacher gradient): a block
+// takes 64 tokens and walks kDlmTmTiles tiles of 64 vocabulary rows.  Per
+// tile, the teacher's 64 x 64 block is loaded with 32-byte loads, 4 lanes per
+// token covering its 128 contiguous bytes, and put in LDS; each thread then
+// takes 4 tokens x 4 rows of it transposed, beside the student's 8-byte
+// loads of 4 tokens per row from L (16 lanes per row), which are issued
+// together with the teacher's.  Requires ldtm a multiple of 8 and 16-byte
+// aligned rows.
+constexpr int kDlmTmTok = 64, kDlmTmRows = 64, kDlmTmTiles = 8;
+template <class T, int DIV, bool T1>
+__global__ __launch_bounds__(256) void k_dlm_tm(DlmParams P) {
+  __shared__ T tt[kDlmTmTok][kDlmTmRows + 8];  // rows of 144 B
+  const int tid = threadIdx.x;
+  const int64_t tb = (int64_t)blockIdx.x * kDlmTmTok;
+  const int64_t vb = (int64_t)blockIdx.y * (kDlmTmRows * kDlmTmTiles);
+  const int64_t vend = min<int64_t>(P.V, vb + kDlmTmRows * kDlmTmTiles);
+  const T* Tm = static_cast<const T*>(P.Ltm);
+  // teacher load: thread -> token tk, rows rc .. rc + 15 of the tile
+  const int tk = tid >> 2, rc = (tid & 3) * 16;
+  const bool tk_ok = tb + tk < P.N;
+  const T* tsrc = Tm + (tk_ok ? tb + tk : 0) * P.ldtm;
+  // compute: thread -> token quad tq, rows rg * 4 .. + 3 of the tile
+  const int tq = tid & 15, rg = tid >> 4;
+  const int64_t t0 = tb + tq * 4;
+  const bool live = t0 < P.N;
+  const int nt = live ? (int)min<int64_t>(P.N - t0, 4) : 0;
+  DlmQuad<DIV, T1> q;
+  q.init(P, live ? t0 : 0, nt);
+  T* Ls = static_cast<T*>(P.L) + (live ? t0 : 0);
+  for (int64_t v0 = vb; v0 < vend; v0 += kDlmTmRows) {
+    union { T e[8]; uint4 u; } w0, w1;
+    w0.u = make_uint4(0u, 0u, 0u, 0u);
+    w1.u = make_uint4(0u, 0u, 0u, 0u);
+    if (tk_ok && v0 + rc < P.V) w0.u = *reinterpret_cast<const uint4*>(tsrc + v0 + rc);
+    if (tk_ok && v0 + rc + 8 < P.V) w1.u = *reinterpret_cast<const uint4*>(tsrc + v0 + rc + 8);
+    float xs[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t v = v0 + rg * 4 + r;
+      if (live && v < P.V) load4(Ls + v * P.ldL, xs[r], nt == 4, nt);
+    }
+    __syncthreads();  // the previous tile's LDS reads are done
+    *reinterpret_cast<uint4*>(&tt[tk][rc]) = w0.u;
+    *reinterpret_cast<uint4*>(&tt[tk][rc + 8]) = w1.u;
+    __syncthreads();
+    if (!live) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t v = v0 + rg * 4 + r;
+      if (v >= P.V) break;
+      float xt[4], ds[4], dt[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xt[i] = to_f32(tt[tq * 4 + i][rg * 4 + r]);
+      q.row(v, xs[r], xt, ds, dt);
+      store4(Ls + v * P.ldL, ds, nt == 4, nt);
+    }
+  }
+}
 
 // ---------------------------------------------------------------- transpose
 // out[c * ldo + r] = in[r * ldi + c] for r < R, c < C (64 x 64 LDS tiles).
@@ -1722,6 +1797,12 @@ inline void gemm2_go(const GemmParams& P, hipStream_t s) {
 // In-place dlogits variants (the divergences of families LIN and POW).
 template <class T, int DIV, bool T1>
 inline void dlm_go(const DlmParams& P, hipStream_t s) {
+  if (P.Ltm) {
+    const int64_t rows = kDlmTmRows * kDlmTmTiles;
+    const dim3 grid((unsigned)((P.N + kDlmTmTok - 1) / kDlmTmTok), (unsigned)((P.V + rows - 1) / rows));
+    hipLaunchKernelGGL((k_dlm_tm<T, DIV, T1>), grid, dim3(256), 0, s, P);
+    return;
+  }
   const dim3 grid((unsigned)((P.N + 1023) / 1024), (unsigned)((P.V + P.rows_per_block - 1) / P.rows_per_block));
   hipLaunchKernelGGL((k_dlm<T, DIV, T1>), grid, dim3(256), 0, s, P);
 }

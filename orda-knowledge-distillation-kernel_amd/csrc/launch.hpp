@@ -92,6 +92,11 @@ struct DlmParams {
   int64_t N, V, ignore_index;
   int div, t_is_one, tgrad, rows_per_block;
   float invT, temperature, alpha, beta, w_s, w_t, w_kl;
+  // precomputed teacher logits read in place, token-major [N][ldtm] (16-byte
+  // aligned rows, ldtm a multiple of 8, rows_per_block a multiple of 8), when
+  // they are not staged in L's teacher columns; else null
+  const void* Ltm;
+  int64_t ldtm;
 };
 
 // Phase-1 row sums of the two-pass divergences over stored logits (k_two_rows).

@@ -200,6 +200,8 @@ def fused_forward(ctx, call: FusedCall):
         lt = call.teacher_logits.contiguous()
         if lt.dtype not in _native.DTYPE:
             lt = lt.float()
+        if lt.data_ptr() % 16 != 0:  # the kernels read 16-byte rows in place
+            lt = lt.clone()
     labels = call.labels.contiguous()
     Hp = hs.shape[1]
     Htp = ht.shape[1] if (ht is not None and call.mode != "tied") else Hp

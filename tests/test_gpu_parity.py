@@ -448,3 +448,38 @@ def test_peaked_rows_dlogits_sum_to_zero_within_rounding():
         ratio = float(gr[:, 0].abs().max() / gr[:, 1:].abs().max())
         print(f"{name}: max |column 0| / max |other columns| = {ratio:.4f}")
         assert ratio < 0.08, (name, ratio)
+
+
+@pytest.mark.parametrize("V", [2000, 1998], ids=["in_place", "staged"])
+def test_precomputed_logits_read_in_place_partial_quads(V):
+    """Precomputed logits of the compute dtype with V a multiple of 8 are read
+    in place, token-major, by the scan and the dlogits pass (no copy into the
+    chunk buffer; chunks of twice the tokens); V = 1998 takes the staged path.
+    N = 203 in 128-token chunks (128 + 75): the last token quad is partial."""
+    from orda_ce_kernel import KernelConfig
+
+    for div, T in (("forward_kl", 1.0), ("reverse_kl", 2.0), ("hellinger", 1.0)):
+        out, ref, hs, W, _ = _run("precomputed_logits", torch.bfloat16, N=203, H=128, Ht=96, V=V, T=T, kl_w=0.9,
+                                  div=div, config=KernelConfig(chunk_size=32), seed=31, grad_teacher=False)
+        _check(out, ref, hs, W, torch.bfloat16)
+
+
+def test_precomputed_logits_misaligned_view_matches_aligned():
+    """A contiguous logits tensor that starts 2 bytes past a 16-byte boundary
+    (a view into a larger buffer) gives the same result as an aligned copy."""
+    o = _orda()
+    hs, ht, W, Wt, y = _make(41, 96, 128, 1000, torch.bfloat16, Ht=64)
+    lt = (ht.float() @ Wt.float().t()).bfloat16()
+    buf = torch.empty(lt.numel() + 8, dtype=torch.bfloat16, device="cuda")
+    lt_mis = buf[1:1 + lt.numel()].view(lt.shape)
+    lt_mis.copy_(lt.cuda())
+    assert lt_mis.data_ptr() % 16 != 0
+    res = []
+    for src in (lt.cuda(), lt_mis):
+        hs_d, W_d = hs.cuda().requires_grad_(True), W.cuda().requires_grad_(True)
+        out = o.distillation_loss(hs_d, W_d, y.cuda(), o.PrecomputedTeacher(logits=src), kl_weight=1.0,
+                                  backend="triton")
+        out.loss.backward()
+        res.append((out.loss.detach(), hs_d.grad, W_d.grad))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
