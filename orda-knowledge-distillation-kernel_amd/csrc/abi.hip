@@ -242,7 +242,7 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // aligned rows), so L holds only the student's logits and a chunk holds
     // twice the tokens in the same memory (grad W then runs half as many
     // read-modify-write passes with twice the K).
-    pl.f_tmem = pl.f_tl && pl.tsrc == TSRC_MEM && pl.V % 8 == 0 && !pl.two_pass;
+    pl.f_tmem = pl.f_tl && pl.tsrc == TSRC_MEM && pl.V % 8 == 0;
     pl.store_t = pl.tsrc != TSRC_NONE && !pl.f_tmem;
     const int64_t ncol = pl.store_t ? 2 : 1;
     const int64_t Nr = round_up(pl.N, 8);
@@ -695,6 +695,8 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       Q.invT = F.invT;
       Q.lw = pl.div == DIV_JSD ? F.log_beta : F.log_alpha;
       Q.l1mw = pl.div == DIV_JSD ? F.log_1m_beta : F.log_1m_alpha;
+      Q.Ltm = pl.f_tmem ? Ltc : nullptr;
+      Q.ldtm = V;
       { Timed tm_(ORDA_K_DLOGITS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_two<T>(Q, s)); }
       M.phase = 1;
       { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }

@@ -1343,6 +1343,90 @@ __global__ __launch_bounds__(16 * kTwoLanes) void k_two_rows(TwoParams P) {
   }
 }
 
+// k_two_rows with the teacher's logits read in place from the caller's
+// precomputed [N x ldtm] tensor (token-major): per iteration the block loads
+// the teacher's 64 tokens x 256 rows with 32-byte loads (16 lanes per
+// token's 512 contiguous bytes) into LDS, and each row lane takes rows
+// rl, rl + 64, rl + 128, rl + 192 of it for its 4 tokens, beside the
+// student's 8-byte loads from L issued in the same iteration.  Same partial
+// states and fixed-order reduction as k_two_rows.
+template <class T, int DIV>
+__global__ __launch_bounds__(16 * kTwoLanes) void k_two_rows_tm(TwoParams P) {
+  constexpr int kIt = 4 * kTwoLanes;            // rows per iteration
+  __shared__ T tt[64][kIt + 8];                 // 64 tokens x 264 (rows of 528 B)
+  __shared__ float xch[2][kTwoLanes][64];
+  const int tid = threadIdx.x;
+  const int tq = tid & 15, rl = tid >> 4;
+  const int64_t tb = (int64_t)blockIdx.x * 64 + tq * 4;
+  const int64_t v0 = (int64_t)blockIdx.y * P.rows_per_range;
+  const int64_t v1 = min<int64_t>(P.V, v0 + P.rows_per_range);
+  const int64_t rem = P.N - tb;
+  const int nt = rem <= 0 ? 0 : (rem >= 4 ? 4 : (int)rem);
+  const float invT = P.invT;
+  float lse_sT[4], lse_tT[4], s0[4], s1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t t = i < nt ? tb + i : 0;
+    lse_sT[i] = P.rowp[1 * P.N + t];
+    lse_tT[i] = P.rowp[3 * P.N + t];
+    s0[i] = 0.f;
+    s1[i] = 0.f;
+  }
+  const T* Ls = static_cast<const T*>(P.L) + (nt > 0 ? tb : 0);
+  // teacher load: thread -> token tk, rows pr .. pr + 15 of the iteration
+  const int tk = tid >> 4, pr = (tid & 15) * 16;
+  const int64_t tglob = (int64_t)blockIdx.x * 64 + tk;
+  const bool tk_ok = tglob < P.N;
+  const T* tsrc = static_cast<const T*>(P.Ltm) + (tk_ok ? tglob : 0) * P.ldtm;
+  for (int64_t vb = v0; vb < v1; vb += kIt) {
+    union { T e[8]; uint4 u; } w0, w1;
+    w0.u = make_uint4(0u, 0u, 0u, 0u);
+    w1.u = make_uint4(0u, 0u, 0u, 0u);
+    if (tk_ok && vb + pr < P.V) w0.u = *reinterpret_cast<const uint4*>(tsrc + vb + pr);
+    if (tk_ok && vb + pr + 8 < P.V) w1.u = *reinterpret_cast<const uint4*>(tsrc + vb + pr + 8);
+    float xs[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t v = vb + rl + r * kTwoLanes;
+      if (nt > 0 && v < v1) load4(Ls + v * P.ldL, xs[r], nt == 4, nt);
+    }
+    __syncthreads();  // the previous iteration's LDS reads are done
+    *reinterpret_cast<uint4*>(&tt[tk][pr]) = w0.u;
+    *reinterpret_cast<uint4*>(&tt[tk][pr + 8]) = w1.u;
+    __syncthreads();
+    if (nt == 0) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t v = vb + rl + r * kTwoLanes;
+      if (v >= v1) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        two_term<DIV>(xs[r][i] * invT - lse_sT[i], to_f32(tt[tq * 4 + i][rl + r * kTwoLanes]) * invT - lse_tT[i],
+                      P.lw, P.l1mw, s0[i], s1[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xch[0][rl][tq * 4 + i] = s0[i];
+    xch[1][rl][tq * 4 + i] = s1[i];
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int64_t t = (int64_t)blockIdx.x * 64 + tid;
+    float a = 0.f, b = 0.f;
+#pragma unroll 8
+    for (int r = 0; r < kTwoLanes; ++r) {
+      a += xch[0][r][tid];
+      b += xch[1][r][tid];
+    }
+    if (t < P.N) {
+      float* dst = P.partial + (int64_t)blockIdx.y * kNStat * P.N + t;
+      dst[6 * P.N] = a;  // RowState x[0]
+      dst[7 * P.N] = b;  // RowState x[1]
+    }
+  }
+}
+
 // ------------------------------------------------- materialised dlogits
 // Row parameters of 4 consecutive tokens and their dlogits for one
 // vocabulary row: student w_s (p_s - 1_y) + w_kl T dD/dz_s, teacher
@@ -1834,6 +1918,16 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
   }                                                                                        \
   template <> hipError_t launch_two<T>(const TwoParams& P, hipStream_t s) {                \
     const dim3 grid((unsigned)((P.N + 63) / 64), (unsigned)P.n_ranges);                   \
+    if (P.Ltm) {                                                                           \
+      switch (P.div) {                                                                     \
+        case DIV_JSD: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_JSD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+        case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_SKEW_F>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+        case DIV_SKEW_R: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_SKEW_R>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+        case DIV_TVD: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_TVD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+        default: return hipErrorInvalidValue;                                              \
+      }                                                                                    \
+      return hipGetLastError();                                                            \
+    }                                                                                      \
     switch (P.div) {                                                                       \
       case DIV_JSD: hipLaunchKernelGGL((k_two_rows<T, DIV_JSD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
       case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_F>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \

@@ -108,6 +108,11 @@ struct TwoParams {
   int64_t N, V, rows_per_range;
   int n_ranges, div;
   float invT, lw, l1mw;  // log w, log(1 - w) of the mixture weight
+  // precomputed teacher logits read in place, token-major [N][ldtm] (16-byte
+  // aligned rows, ldtm and rows_per_range multiples of 8); else null: the
+  // teacher's logits are L's teacher columns
+  const void* Ltm;
+  int64_t ldtm;
 };
 
 struct LabelParams {

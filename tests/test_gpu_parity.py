@@ -453,12 +453,14 @@ def test_peaked_rows_dlogits_sum_to_zero_within_rounding():
 @pytest.mark.parametrize("V", [2000, 1998], ids=["in_place", "staged"])
 def test_precomputed_logits_read_in_place_partial_quads(V):
     """Precomputed logits of the compute dtype with V a multiple of 8 are read
-    in place, token-major, by the scan and the dlogits pass (no copy into the
-    chunk buffer; chunks of twice the tokens); V = 1998 takes the staged path.
+    in place, token-major, by the scan, the two-pass divergences' second pass
+    and the dlogits pass (no copy into the chunk buffer; chunks of twice the
+    tokens); V = 1998 takes the staged path.
     N = 203 in 128-token chunks (128 + 75): the last token quad is partial."""
     from orda_ce_kernel import KernelConfig
 
-    for div, T in (("forward_kl", 1.0), ("reverse_kl", 2.0), ("hellinger", 1.0)):
+    for div, T in (("forward_kl", 1.0), ("reverse_kl", 2.0), ("hellinger", 1.0), ("jsd", 2.0), ("skew_forward_kl", 1.0),
+                   ("tvd", 1.0)):
         out, ref, hs, W, _ = _run("precomputed_logits", torch.bfloat16, N=203, H=128, Ht=96, V=V, T=T, kl_w=0.9,
                                   div=div, config=KernelConfig(chunk_size=32), seed=31, grad_teacher=False)
         _check(out, ref, hs, W, torch.bfloat16)
