@@ -237,12 +237,13 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // workgroup (16-bit, K > 64, one-pass non-power divergences).
     pl.f_tl = pl.eb == 2 && pl.H > 64 && pl.fam != FAM_POW &&
               ((pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype) || pl.tsrc == TSRC_SEP);
-    // Precomputed logits with V a multiple of 8 are not staged at all: the
-    // scan and the dlogits pass both read them in place, token-major (16-byte
-    // aligned rows), so L holds only the student's logits and a chunk holds
-    // twice the tokens in the same memory (grad W then runs half as many
-    // read-modify-write passes with twice the K).
-    pl.f_tmem = pl.f_tl && pl.tsrc == TSRC_MEM && pl.V % 8 == 0;
+    // Precomputed 16-bit logits of the compute dtype with V a multiple of 8
+    // are not staged at all: the scan (either engine), the two-pass
+    // divergences' second pass and the dlogits pass all read them in place,
+    // token-major (16-byte aligned rows), so L holds only the student's
+    // logits and a chunk holds twice the tokens in the same memory (grad W
+    // then runs half as many read-modify-write passes with twice the K).
+    pl.f_tmem = pl.eb == 2 && pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype && pl.V % 8 == 0;
     pl.store_t = pl.tsrc != TSRC_NONE && !pl.f_tmem;
     const int64_t ncol = pl.store_t ? 2 : 1;
     const int64_t Nr = round_up(pl.N, 8);
