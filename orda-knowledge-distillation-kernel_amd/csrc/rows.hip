@@ -62,11 +62,13 @@ __global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams 
       RowState o;
       const float* s = P.partial + (int64_t)vr * kNStat * N + t;
       float* d = reinterpret_cast<float*>(&o);
+#pragma unroll
       for (int f = 0; f < kNStat; ++f) d[f] = s[(int64_t)f * N];
       state_merge(S, o, P.fam, P.t_is_one != 0, P.invT);
     }
   if (slice > 0) {
     const float* d = reinterpret_cast<const float*>(&S);
+#pragma unroll
     for (int f = 0; f < kNStat; ++f) xch[slice - 1][f][tl] = d[f];
   }
   __syncthreads();
@@ -74,6 +76,7 @@ __global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams 
   for (int k = 0; k < kMergeSlices - 1; ++k) {
     RowState o;
     float* d = reinterpret_cast<float*>(&o);
+#pragma unroll
     for (int f = 0; f < kNStat; ++f) d[f] = xch[k][f][tl];
     state_merge(S, o, P.fam, P.t_is_one != 0, P.invT);
   }
@@ -108,9 +111,11 @@ __global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams 
       }
     } else {  // FAM_POW: log P_i = LSE(u_i) - a_i lse_t^T - b_i lse_s^T
       double lp[3] = {0.0, 0.0, 0.0};
-      for (int i = 0; i < P.npow; ++i)
-        lp[i] = (double)S.x[2 * i] + log((double)S.x[2 * i + 1]) - (double)P.pa[i] * lse_tT -
-                (double)P.pb[i] * lse_sT;
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        if (i < P.npow)
+          lp[i] = (double)S.x[2 * i] + log((double)S.x[2 * i + 1]) - (double)P.pa[i] * lse_tT -
+                  (double)P.pb[i] * lse_sT;
       const double a = P.alpha, b = P.beta;
       switch (P.div) {
         case DIV_HELL: D = 1.0 - exp(lp[0]); break;
