@@ -124,7 +124,11 @@ typedef struct orda_tensors {
   const void* weight;          /* [V x H]   dtype                            */
   const void* teacher_hidden;  /* [N x Ht]  dtype (TIED: Ht == H)            */
   const void* teacher_weight;  /* [V x Ht]  dtype (SEPARATE / PRE_HIDDEN)    */
-  const void* teacher_logits;  /* [N x V]   logits_dtype (PRE_LOGITS)        */
+  const void* teacher_logits;  /* [N x V]   logits_dtype (PRE_LOGITS); with
+                                * ORDA_GRADS_IN_FORWARD, a 16-bit compute dtype
+                                * and V a multiple of 8 they are read in place
+                                * and must be 16-byte aligned (else
+                                * ORDA_EINVAL)                                */
   const int64_t* labels;       /* [N]                                        */
   /* forward outputs: fp32 scalars */
   float* out_loss;
