@@ -1176,22 +1176,59 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
         for (int j = 0; j < 2; ++j) {
           const int mb = 2 * hh + j;
           T* rp = C + (int64_t)(wm * 128 + mb * 32 + (lane & 31)) * ldc + cl;
+          auto group = [&](int nb, int g, float (&o)[4]) __attribute__((always_inline)) {
 #pragma unroll
-          for (int nb = 0; nb < 4; ++nb)
+            for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
+            if constexpr (MODE == GEMM_ACC_T) {
+              union { T e[4]; uint2 u; } v;
+              v.u = cv[j][nb][g];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              float o[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
-              if constexpr (MODE == GEMM_ACC_T) {
-                union { T e[4]; uint2 u; } v;
-                v.u = cv[j][nb][g];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
-              }
-              store4(rp + col(nb, g), o, true, 4);
-              __builtin_amdgcn_sched_barrier(0);
+              for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
             }
+          };
+          // 16-byte stores need 16-byte aligned rows (uniform test: the
+          // library's own outputs always pass; the general entry may not)
+          const bool wide = sizeof(T) == 2 && ldc % 8 == 0 && reinterpret_cast<uintptr_t>(P.C) % 16 == 0;
+          if (wide) {
+            // lanes l and l + 32 hold the two 4-column halves of each 8-column
+            // group of the same row: exchanging one group of each pair (g,
+            // g + 1) gives lane l group g whole and lane l + 32 group g + 1
+            // whole, one 16-byte store each instead of two 8-byte stores
+            const bool hi = lane >= 32;
+            T* rq = rp - (hi ? 4 : 0);  // the row's 8-column group base
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+              for (int g = 0; g < 4; g += 2) {
+                float oa[4], ob[4];
+                group(nb, g, oa);
+                group(nb, g + 1, ob);
+                union { T e[4]; uint2 u; } pa, pb;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  pa.e[e] = from_f32<T>(oa[e]);
+                  pb.e[e] = from_f32<T>(ob[e]);
+                }
+                const uint2 send = hi ? pa.u : pb.u;
+                uint2 recv;
+                recv.x = __shfl_xor(send.x, 32);
+                recv.y = __shfl_xor(send.y, 32);
+                const uint4 out = hi ? make_uint4(recv.x, recv.y, pb.u.x, pb.u.y)
+                                     : make_uint4(pa.u.x, pa.u.y, recv.x, recv.y);
+                *reinterpret_cast<uint4*>(rq + col(nb, hi ? g + 1 : g)) = out;
+                __builtin_amdgcn_sched_barrier(0);
+              }
+          } else {
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                float o[4];
+                group(nb, g, o);
+                store4(rp + col(nb, g), o, true, 4);
+                __builtin_amdgcn_sched_barrier(0);
+              }
+          }
         }
       }
       return;
