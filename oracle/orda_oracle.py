@@ -23,6 +23,11 @@ relative to ``src/orda_ce_kernel/``):
   ``kl_weight == 0`` (the Triton kernels skip it: ``COMPUTE_KL``,
   ``ops/tied_teacher.py:143,188``); the torch backend reports it
   (``api.py:317-331``);
+* with ``grad_logits_dtype="bfloat16"`` / ``"float16"`` the dlogits are
+  formed from the logits rounded to that dtype, as the reference's kernels
+  form them: the chunk's logits are a matmul output in the compute dtype
+  (``ops/tied_teacher.py:444-445``) that the row kernel loads and widens to
+  fp32 (``:145-147``); loss values still come from the unrounded logits;
 * gradients in closed form: student dlogits
   ``s [w_s (p_s - 1_y) + w_kl T dD/dz_s]`` and teacher dlogits
   ``s w_t (p_t - 1_y)`` (``ops/tied_teacher.py:153-186``), with
@@ -43,7 +48,23 @@ from __future__ import annotations
 
 import numpy as np
 
-__all__ = ["DIVERGENCE_DEFS", "divergence_value_and_grad", "distillation_loss_oracle", "log_softmax"]
+__all__ = ["DIVERGENCE_DEFS", "divergence_value_and_grad", "distillation_loss_oracle", "log_softmax", "round_to"]
+
+
+def round_to(x: np.ndarray, dtype: str | None) -> np.ndarray:
+    """``x`` rounded to float32, then to ``dtype`` ("bfloat16" / "float16",
+    round to nearest even; None: unchanged), returned as float64.  The GPU
+    kernels round an fp32 accumulator, so the float32 step is part of it."""
+    if dtype is None:
+        return np.asarray(x, dtype=np.float64)
+    f = np.asarray(x, dtype=np.float32)
+    if dtype == "float16":
+        return f.astype(np.float16).astype(np.float64)
+    if dtype != "bfloat16":
+        raise ValueError(f"unknown dtype {dtype!r}")
+    u = f.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
 
 
 def log_softmax(x: np.ndarray) -> np.ndarray:
@@ -198,6 +219,7 @@ def distillation_loss_oracle(
     kernel_semantics: bool = True,
     grad_output: float = 1.0,
     teacher_grads: bool = True,
+    grad_logits_dtype: str | None = None,
 ) -> dict:
     """Loss components and gradients, float64.
 
@@ -249,6 +271,13 @@ def distillation_loss_oracle(
 
     g = grad_output * scale
     keep = (~ignored)[:, None].astype(np.float64)
+    if grad_logits_dtype is not None:
+        x_s = round_to(x_s, grad_logits_dtype)
+        if ht is not None:  # given teacher logits are used as they come
+            x_t = round_to(x_t, grad_logits_dtype)
+        lse_s = np.log(np.exp(x_s - x_s.max(1, keepdims=True)).sum(1)) + x_s.max(1)
+        lse_t = np.log(np.exp(x_t - x_t.max(1, keepdims=True)).sum(1)) + x_t.max(1)
+        _, dz = divergence_value_and_grad(x_t / T, x_s / T, divergence, alpha, beta)
     p_s = np.exp(x_s - lse_s[:, None])
     p_t = np.exp(x_t - lse_t[:, None])
     dl_s = g * keep * (student_ce_weight * (p_s - onehot) + kl_weight * T * dz)

@@ -329,9 +329,9 @@ def distillation_loss(
         )
     if not _supports_native(student_hidden):
         raise RuntimeError(
-            f"backend={backend!r} requires the HIP extension liborda_ce.so and CUDA/HIP tensors "
-            f"(device={student_hidden.device}, library: {native_error() or 'loaded'}); use backend='auto' "
-            "or backend='torch' for fallback execution"
+            f"backend={backend!r} on {student_hidden.device} tensors requires the HIP extension liborda_ce.so "
+            f"({native_error() or 'loaded'}); on a HIP device this build never falls back silently, pass "
+            "backend='torch' to run the unfused PyTorch formulation explicitly"
         )
 
     common = dict(

@@ -8,7 +8,9 @@ Two schedules, chosen per call by :func:`grads_in_forward`:
   walks token chunks, materialises each chunk's logits in a workspace,
   turns them into dlogits in place and multiplies them into the gradients,
   accumulating grad W across chunks in the weight dtype as the reference's
-  ``addmm_`` does; backward only multiplies by ``grad_output``;
+  ``addmm_`` does; backward only multiplies by ``grad_output`` (in place,
+  once: a second backward through a retained graph recomputes the
+  gradients rather than rescale tensors already handed out);
 * two-phase (``fp32_grad_weight_accumulation=True``, precomputed logits
   in another dtype than the compute dtype, and forward-only calls):
   ``orda_forward``
@@ -208,28 +210,35 @@ def fused_forward(ctx, call: FusedCall):
     problem = _problem(call, Hp, Htp, lt.dtype if lt is not None else None)
 
     saved = torch.empty(_native.saved_bytes(problem), dtype=torch.uint8, device=dev)
-    ws = torch.empty(_native.forward_workspace_bytes(problem), dtype=torch.uint8, device=dev)
     outs = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(4)]
+    grads = _alloc_grads(problem.flags, hs, w, ht, wt) if call.grads_in_forward else (None,) * 4
+    _run_forward(problem, (hs, w, ht, wt, lt, labels), saved, outs, grads)
+
+    ctx.orda_problem = problem
+    ctx.orda_shapes = (H, Ht)
+    ctx.orda_mode = call.mode
+    ctx.save_for_backward(hs, w, ht, wt, lt, labels, saved)
+    # Gradients computed in forward: the first backward scales them in place
+    # and hands them to autograd, dropping this reference (so autograd can
+    # keep the buffers as .grad without a copy); a later backward through a
+    # retained graph recomputes them, so no returned tensor is ever scaled
+    # twice.
+    ctx.orda_grads = grads if call.grads_in_forward else None
+    return tuple(outs)
+
+
+def _run_forward(problem, inputs, saved, outs, grads) -> None:
+    """One orda_forward call with a fresh workspace (freed on return)."""
+    hs, w, ht, wt, lt, labels = inputs
+    ws = torch.empty(_native.forward_workspace_bytes(problem), dtype=torch.uint8, device=hs.device)
     t = _native.Tensors()
     t.student_hidden, t.weight, t.labels = _ptr(hs), _ptr(w), _ptr(labels)
     t.teacher_hidden, t.teacher_weight, t.teacher_logits = _ptr(ht), _ptr(wt), _ptr(lt)
     t.out_loss, t.out_student_ce, t.out_teacher_ce, t.out_kl = (o.data_ptr() for o in outs)
     t.saved = saved.data_ptr()
-    grads = (None, None, None, None)
-    if call.grads_in_forward:
-        grads = _alloc_grads(problem.flags, hs, w, ht, wt)
-        t.grad_student_hidden, t.grad_weight, t.grad_teacher_hidden, t.grad_teacher_weight = (_ptr(g) for g in grads)
+    t.grad_student_hidden, t.grad_weight, t.grad_teacher_hidden, t.grad_teacher_weight = (_ptr(g) for g in grads)
     _native.forward(problem, t, ws)
     del ws
-
-    ctx.orda_problem = problem
-    ctx.orda_shapes = (H, Ht)
-    ctx.orda_mode = call.mode
-    if call.grads_in_forward:
-        ctx.save_for_backward(hs, w, ht, wt, lt, labels, saved, *grads)
-    else:
-        ctx.save_for_backward(hs, w, ht, wt, lt, labels, saved)
-    return tuple(outs)
 
 
 def _alloc_grads(flags: int, hs, w, ht, wt):
@@ -244,14 +253,18 @@ def _alloc_grads(flags: int, hs, w, ht, wt):
 def fused_backward(ctx, grad_output: torch.Tensor):
     """Gradients ``(d_student_hidden, d_weight, d_teacher_hidden,
     d_teacher_weight)`` in the compute dtype, unpadded; None where not needed."""
-    saved_tensors = ctx.saved_tensors
-    hs, w, ht, wt, lt, labels, saved = saved_tensors[:7]
+    hs, w, ht, wt, lt, labels, saved = ctx.saved_tensors
     problem = ctx.orda_problem
     H, Ht = ctx.orda_shapes
     flags = problem.flags
     dev = hs.device
     if flags & _native.FLAG["grads_in_forward"]:
-        g_hs, g_w, g_ht, g_wt = saved_tensors[7:]
+        grads, ctx.orda_grads = ctx.orda_grads, None
+        if grads is None:  # a second backward through a retained graph
+            grads = _alloc_grads(flags, hs, w, ht, wt)
+            outs = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(4)]
+            _run_forward(problem, (hs, w, ht, wt, lt, labels), torch.empty_like(saved), outs, grads)
+        g_hs, g_w, g_ht, g_wt = grads
     else:
         g_hs, g_w, g_ht, g_wt = _alloc_grads(flags, hs, w, ht, wt)
     go = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()

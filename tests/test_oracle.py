@@ -24,7 +24,7 @@ import torch.nn.functional as F
 from scipy.spatial.distance import jensenshannon
 from scipy.stats import entropy
 
-from oracle.orda_oracle import DIVERGENCE_DEFS, distillation_loss_oracle, divergence_value_and_grad
+from oracle.orda_oracle import DIVERGENCE_DEFS, distillation_loss_oracle, divergence_value_and_grad, round_to
 
 DIVS = sorted(DIVERGENCE_DEFS)
 
@@ -333,3 +333,60 @@ def test_loss_gradient_matches_finite_differences_with_temperature():
     out_p = distillation_loss_oracle("precomputed", hs, W, y, **kw_p)
     num = _fd(lambda: distillation_loss_oracle("precomputed", hs, W, y, **kw_p)["loss"], W)
     np.testing.assert_allclose(out_p["grad_weight"], num, rtol=1e-5, atol=1e-8)
+
+
+# ------------------------------------------------ dlogits from rounded logits
+def test_round_to_matches_torch_conversions():
+    """round_to's bfloat16 / float16 rounding is torch's (round to nearest
+    even), exact ties and the fp32 step included."""
+    r = _rng(5)
+    x = np.concatenate([r.standard_normal(20000) * 10.0 ** r.integers(-6, 6, 20000),
+                        [0.0, -0.0, 1.0, -3.5, 65504.0, 1e-30]])
+    # exact bf16 ties: fp32 patterns whose low 16 bits are 0x8000
+    ties = (r.integers(0x3F000000, 0x43000000, 2000, dtype=np.uint32) & 0xFFFF0000) | 0x8000
+    x = np.concatenate([x, ties.view(np.float32).astype(np.float64)])
+    xt = torch.tensor(x, dtype=torch.float64).float()
+    np.testing.assert_array_equal(round_to(x, "bfloat16"), xt.bfloat16().double().numpy())
+    small = x[np.abs(x) < 60000]
+    np.testing.assert_array_equal(round_to(small, "float16"),
+                                  torch.tensor(small).float().half().double().numpy())
+    np.testing.assert_array_equal(round_to(x, None), x)
+
+
+def test_rounded_logits_option_is_a_no_op_on_representable_logits():
+    """With one-hot student and teacher hidden rows the logits are columns of
+    a bf16 W, which bfloat16 holds exactly: the option must change nothing."""
+    r = _rng(6)
+    N, H, V = 12, 12, 40
+    W = round_to(r.standard_normal((V, H)) * 2.0, "bfloat16")
+    hs = np.eye(N, H)
+    ht = np.roll(np.eye(N, H), 3, axis=1)
+    y = r.integers(0, V, N)
+    y[::5] = -100
+    for div in ("forward_kl", "jsd", "hellinger"):
+        kw = dict(teacher_hidden=ht, kl_weight=0.6, kl_temperature=2.0, teacher_ce_weight=0.4, divergence=div)
+        a = distillation_loss_oracle("tied", hs, W, y, **kw)
+        b = distillation_loss_oracle("tied", hs, W, y, grad_logits_dtype="bfloat16", **kw)
+        for k in ("grad_student_hidden", "grad_weight", "grad_teacher_hidden"):
+            np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+
+
+def test_rounded_logits_option_rounds_the_logits_the_dlogits_see():
+    """Against a direct restatement: softmax dlogits of the rounded student
+    logits (the student CE part only: w_t = kl = 0), and the row-sum
+    invariant (softmax dlogits sum to zero per row) still holds."""
+    hs, ht, W, _, y = _inputs(7, N=6, H=5, V=30)
+    hs, W = hs * 3.0, W * 3.0
+    out = distillation_loss_oracle("tied", hs, W, y, teacher_hidden=ht, teacher_ce_weight=0.0,
+                                   grad_logits_dtype="bfloat16")
+    x = round_to(hs @ W.T, "bfloat16")
+    p = np.exp(x - x.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    keep = y != -100
+    p[np.arange(len(y))[keep], y[keep]] -= 1.0
+    p[~keep] = 0.0
+    want = p / keep.sum()
+    np.testing.assert_allclose(out["dlogits_student"], want, rtol=1e-12, atol=1e-15)
+    assert np.abs(out["dlogits_student"].sum(1)).max() < 1e-15
+    plain = distillation_loss_oracle("tied", hs, W, y, teacher_hidden=ht, teacher_ce_weight=0.0)
+    assert np.abs(plain["dlogits_student"] - want).max() > 1e-6  # the rounding is visible at this scale
