@@ -179,6 +179,25 @@ size_t orda_backward_workspace_bytes(const orda_problem_t* p);
 int orda_forward(const orda_problem_t* p, const orda_tensors_t* t,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the static scratch behind orda_forward_static (64 MiB). */
+#define ORDA_STATIC_SCRATCH_BYTES (64ull << 20)
+
+/* orda_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, whose
+ * Functions allocate their chunk buffers with torch (ops/tied_teacher.py:
+ * 356-358).  The scratch is a file-scope device array of
+ * ORDA_STATIC_SCRATCH_BYTES on each device the library runs on, held until
+ * the process ends; this entry point calls no hipMalloc/hipFree.  Problems
+ * whose orda_forward_workspace_bytes() exceed it are rejected with
+ * ORDA_EWORKSPACE (a smaller token_chunk shrinks the gradients-in-forward
+ * workspace: at V = 128256, H = 4096 a 64-token chunk fits).  Every call on a
+ * device shares that device's scratch: calls that overlap on one device
+ * (different streams, different host threads) race and must be serialised by
+ * the caller.  The stream must belong to the current device.  Same outputs
+ * as orda_forward. */
+int orda_forward_static(const orda_problem_t* p, const orda_tensors_t* t, void* stream);
+
 /* Backward: all requested gradients, already multiplied by
  * grad_output * mean_scale.  Replaces the gradient GEMMs computed inside
  * forward (ops/tied_teacher.py:468-495, separate_teacher.py:660-674,

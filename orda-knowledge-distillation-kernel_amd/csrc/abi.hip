@@ -821,6 +821,63 @@ int check_operands(const Plan& pl, const orda_tensors_t* t) {
   return ORDA_OK;
 }
 
+// Scratch of orda_forward_static, the entry point for callers that cannot
+// allocate (code under HIP graph capture, serving loops, harnesses that forbid
+// hipMalloc).  One array per device, created with the library's code object
+// on that device and held until the process ends; every call on a device
+// shares it, so calls that overlap on one device race.  Host code never uses
+// the array's name as an address: the device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t kStaticScratchBytes = ORDA_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch.
+int static_scratch(char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(ORDA_ELAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(ORDA_EUNSUPPORTED, "device index %d is out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(ORDA_ELAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<char*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return ORDA_OK;
+}
+
+// orda_forward's work once the plan and the workspace are settled.
+int forward_with(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  ORDA_TRY(check_operands(pl, t));
+  if (!t->out_loss || !t->out_student_ce || !t->out_teacher_ce || !t->out_kl)
+    return fail(ORDA_EINVAL, "forward outputs are required");
+  if (!workspace || workspace_bytes < pl.fwd_bytes)
+    return fail(ORDA_EWORKSPACE, "forward workspace too small: need %zu bytes, got %zu", pl.fwd_bytes, workspace_bytes);
+  char* ws = aligned_base(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.fused) {
+    ORDA_TRY(check_grads(pl, t));
+    switch (pl.dtype) {
+      case ORDA_BF16: return run_fused<bf16>(pl, p, t, ws, s);
+      case ORDA_F16: return run_fused<f16>(pl, p, t, ws, s);
+      default: return run_fused<float>(pl, p, t, ws, s);
+    }
+  }
+  switch (pl.dtype) {
+    case ORDA_BF16: return run_forward<bf16>(pl, p, t, ws, s);
+    case ORDA_F16: return run_forward<f16>(pl, p, t, ws, s);
+    default: return run_forward<float>(pl, p, t, ws, s);
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -852,26 +909,21 @@ int orda_forward(const orda_problem_t* p, const orda_tensors_t* t, void* workspa
   g_err.clear();
   Plan pl;
   ORDA_TRY(make_plan(p, pl));
-  ORDA_TRY(check_operands(pl, t));
-  if (!t->out_loss || !t->out_student_ce || !t->out_teacher_ce || !t->out_kl)
-    return fail(ORDA_EINVAL, "forward outputs are required");
-  if (!workspace || workspace_bytes < pl.fwd_bytes)
-    return fail(ORDA_EWORKSPACE, "forward workspace too small: need %zu bytes, got %zu", pl.fwd_bytes, workspace_bytes);
-  char* ws = aligned_base(workspace);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (pl.fused) {
-    ORDA_TRY(check_grads(pl, t));
-    switch (pl.dtype) {
-      case ORDA_BF16: return run_fused<bf16>(pl, p, t, ws, s);
-      case ORDA_F16: return run_fused<f16>(pl, p, t, ws, s);
-      default: return run_fused<float>(pl, p, t, ws, s);
-    }
-  }
-  switch (pl.dtype) {
-    case ORDA_BF16: return run_forward<bf16>(pl, p, t, ws, s);
-    case ORDA_F16: return run_forward<f16>(pl, p, t, ws, s);
-    default: return run_forward<float>(pl, p, t, ws, s);
-  }
+  return forward_with(pl, p, t, workspace, workspace_bytes, stream);
+}
+
+int orda_forward_static(const orda_problem_t* p, const orda_tensors_t* t, void* stream) {
+  g_err.clear();
+  Plan pl;
+  ORDA_TRY(make_plan(p, pl));
+  if (pl.fwd_bytes > kStaticScratchBytes)
+    return fail(ORDA_EWORKSPACE,
+                "orda_forward_static: this problem needs %zu bytes of scratch, more than the %zu of the static "
+                "scratch; use orda_forward with a workspace, or a smaller token_chunk",
+                pl.fwd_bytes, kStaticScratchBytes);
+  char* ws = nullptr;
+  ORDA_TRY(static_scratch(&ws));
+  return forward_with(pl, p, t, ws, kStaticScratchBytes, stream);
 }
 
 int orda_backward(const orda_problem_t* p, const orda_tensors_t* t, void* workspace, size_t workspace_bytes,

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 __all__ = [
-    "ABI_VERSION", "Problem", "Tensors", "library", "library_path", "forward", "backward",
+    "ABI_VERSION", "Problem", "Tensors", "library", "library_path", "forward", "forward_static", "backward",
     "saved_bytes", "forward_workspace_bytes", "backward_workspace_bytes", "gemm_abt", "gemm",
     "MODE", "DTYPE", "FLAG", "KERNEL_CLASSES", "timing_enable", "timing_collect",
 ]
@@ -127,6 +127,8 @@ def library() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [P, T, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.orda_forward_static.restype = ctypes.c_int
+        lib.orda_forward_static.argtypes = [P, T, ctypes.c_void_p]
         lib.orda_gemm_abt.restype = ctypes.c_int
         lib.orda_gemm_abt.argtypes = [
             ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
@@ -186,6 +188,17 @@ def forward(problem: Problem, tensors: Tensors, workspace: torch.Tensor) -> None
         _stream(workspace.device),
     )
     _check(rc, "orda_forward")
+
+
+def forward_static(problem: Problem, tensors: Tensors, device: torch.device) -> None:
+    """orda_forward on the library's static scratch (no workspace, no
+    allocation); raises RuntimeError when the problem does not fit it."""
+    with torch.cuda.device(device):
+        rc = library().orda_forward_static(ctypes.byref(problem), ctypes.byref(tensors), _stream(device))
+    _check(rc, "orda_forward_static")
+
+
+STATIC_SCRATCH_BYTES = 64 << 20  # ORDA_STATIC_SCRATCH_BYTES
 
 
 def backward(problem: Problem, tensors: Tensors, workspace: torch.Tensor | None, device: torch.device) -> None:
