@@ -103,11 +103,16 @@ def algorithmic_flops(cfg) -> float:
     return 3 * G(H)
 
 
-def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None):
+def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=None):
     import torch
 
     import orda_ce_kernel as orda
     from orda_ce_kernel import _native
+    from orda_ce_kernel.ops import _engine
+
+    # launch-table sweeps: an explicit requested chunk and grad-hidden split count
+    config = orda.KernelConfig(chunk_size=chunk) if chunk else None
+    _engine.LAUNCH_OVERRIDES["grad_hidden_splits"] = splits
 
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, _ = cfg
     device = "cuda"
@@ -123,7 +128,8 @@ def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None):
 
     def step():
         out = orda.distillation_loss(hs, W, y, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t,
-                                     kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div)
+                                     kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div,
+                                     config=config)
         out.loss.backward()
         hs.grad = None
         W.grad = None
@@ -161,6 +167,40 @@ def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None):
     return ms_step, peak_extra, loss_val, kern
 
 
+def launch_plan_of(cfg, chunk, splits):
+    """The library's launch plan for the benchmark call (gfx950 launch
+    table row, token chunk, grad-hidden split count)."""
+    from orda_ce_kernel import _native
+
+    mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, _ = cfg
+    p = _native.Problem()
+    p.abi_version = _native.ABI_VERSION
+    p.mode = {"tied": 0, "separate": 1, "precomputed": 2}[mode]
+    p.dtype = p.logits_dtype = {"bfloat16": 0, "float16": 1, "float32": 2}[dtype_name]
+    p.n_rows, p.vocab, p.hidden, p.teacher_hidden = N, V, H, Ht
+    p.ignore_index = -100
+    w_t_eff = (1.0 if mode == "tied" else 0.0) if w_t is None else w_t
+    f = _native.FLAG
+    p.flags = f["need_grad_student_hidden"] | f["need_grad_weight"] | f["grads_in_forward"]
+    if w_t_eff != 0.0:
+        p.flags |= f["compute_teacher_ce"]
+    if kl_w != 0.0:
+        p.flags |= f["compute_divergence"]
+    from orda_ce_kernel.divergences import resolve_divergence
+
+    d = resolve_divergence(div)
+    p.divergence = d.code
+    p.div_alpha = d.alpha or 0.0
+    p.div_beta = d.beta or 0.0
+    p.temperature = T
+    p.student_ce_weight, p.teacher_ce_weight, p.kl_weight = w_s, w_t_eff, kl_w
+    p.token_chunk = chunk or 512  # the dispatcher's auto chunk at these sizes
+    p.grad_hidden_splits = splits or 0
+    info = _native.plan_info(p)
+    return {k: info[k] for k in ("table_entry", "token_chunk", "n_token_chunks", "grad_hidden_splits",
+                                 "scan_workgroups", "scan_engine")}
+
+
 def kernel_report(kern, steps, peak_tflops):
     rows = {}
     for name, k in kern.items():
@@ -185,7 +225,7 @@ def cpu_baseline(cfg, seed, budget_s, row_tau=None):
     from oracle.torch_unfused import tied_forward_kl_loss
 
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, _ = cfg
-    threads = min(16, os.cpu_count() or 1)
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     hs, ht, W, _, _, y = make_inputs(cfg, "cuda", seed, row_tau)
     Wc = W.float().cpu()
@@ -208,9 +248,11 @@ def cpu_baseline(cfg, seed, budget_s, row_tau=None):
     probe = 64
     t_probe = run(probe)
     per_tok = t_probe / probe
-    n = int(max(probe, min(N, (budget_s / 3.0) / per_tok)))
+    # one warm-up run of the sample size, then the median of 3: about budget_s in all
+    n = int(max(probe, min(N, (budget_s / 4.0) / per_tok)))
     n = max(probe, (n // 64) * 64)
-    times = [run(n) for _ in range(2)]
+    run(n)
+    times = [run(n) for _ in range(3)]
     t = statistics.median(times)
     cpu_name = platform.processor() or platform.machine()
     try:
@@ -227,8 +269,9 @@ def cpu_baseline(cfg, seed, budget_s, row_tau=None):
         "cores": threads,
         "kind": "port",
         "sample": (f"{n} of {N} tokens of the same workload (full V={V}, H={H}), fp32 unfused torch restatement "
-                   f"of the reference loss (oracle/torch_unfused.py), fwd+bwd, median of {len(times)} runs; "
-                   f"os.cpu_count()={os.cpu_count()}, {cpu_name}"),
+                   f"of the reference loss (oracle/torch_unfused.py), fwd+bwd, median of {len(times)} runs after "
+                   f"1 warm-up; torch threads {torch.get_num_threads()} = os.cpu_count()={os.cpu_count()}, "
+                   f"{cpu_name}"),
     }
 
 
@@ -290,6 +333,39 @@ def sweep(cfg, args, row_tau) -> int:
     return 0
 
 
+# Launch-table sweep: (requested chunk, grad-hidden split count) per config;
+# the chunk is the dispatcher's chunk_size, which the library scales by the
+# table's chunk_scale (so 512 -> 1024 tokens at scale 2).
+TABLE_SWEEP = {
+    "c2": [(c, s) for c in (256, 512) for s in (4, 8, 12, 16)],
+    "c3": [(c, s) for c in (512, 1024) for s in (4, 8, 16)],
+    "c4": [(c, s) for c in (256, 512) for s in (2, 4, 8)],
+    "c5": [(c, s) for c in (512, 1024) for s in (8, 16)],
+}
+
+
+def table_sweep(args) -> int:
+    """ms per step for each launch-table candidate of every configuration
+    (one json line each); the rows behind csrc/launch_table.hpp."""
+    import torch
+
+    for name, cases in TABLE_SWEEP.items():
+        cfg = CONFIGS[name]
+        row_tau = ROW_TEMPERATURE.get(name)
+        for chunk, splits in cases:
+            ms, peak_extra, _, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, True, row_tau, chunk=chunk,
+                                              splits=splits)
+            rows = kernel_report(kern, args.steps, PEAK_BF16_TFLOPS)
+            plan = launch_plan_of(cfg, chunk, splits)
+            print(json.dumps({
+                "config": name, "chunk": chunk, "splits": splits, "token_chunk": plan["token_chunk"],
+                "ms_per_step": round(ms, 3), "peak_extra_hbm_gb": round(peak_extra / 1e9, 3),
+                "ms_per_step_by_class": {k: round(r["ms_per_step"], 3) for k, r in rows.items()},
+            }), flush=True)
+            torch.cuda.empty_cache()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -302,7 +378,15 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true",
                     help="instead of the one-line benchmark, time every divergence at T=1 and T=4 on --config "
                          "(one json line per case; config 4's divergence sweep)")
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work")
+    ap.add_argument("--chunk", type=int, default=None,
+                    help="requested token chunk (KernelConfig.chunk_size; the library scales it by the launch "
+                         "table's chunk_scale), for launch-table sweeps")
+    ap.add_argument("--splits", type=int, default=None,
+                    help="grad-hidden split-K count instead of the launch table's, for launch-table sweeps")
+    ap.add_argument("--table-sweep", action="store_true",
+                    help="instead of the one-line benchmark, time the launch-table candidates (requested chunk x "
+                         "grad-hidden splits) of configs 2-5, one json line each")
+    ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -326,9 +410,11 @@ def main() -> int:
     row_tau = ROW_TEMPERATURE.get(args.config)
     if args.sweep:
         return sweep(cfg, args, row_tau)
+    if args.table_sweep:
+        return table_sweep(args)
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, ignore_frac = cfg
     ms_step, peak_extra, loss_val, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, not args.no_timing,
-                                                 row_tau)
+                                                 row_tau, chunk=args.chunk, splits=args.splits)
     peak = PEAK_FP32_TFLOPS if dtype_name == "float32" else PEAK_BF16_TFLOPS
     alg = algorithmic_flops(cfg)
     step_tflops = alg / (ms_step / 1e3) / 1e12
@@ -353,6 +439,7 @@ def main() -> int:
             "tokens": N, "hidden": H, "vocab": V, "teacher": mode, "divergence": div, "temperature": T,
             "student_ce_weight": w_s, "teacher_ce_weight": w_t, "kl_weight": kl_w, "ignore_frac": ignore_frac,
         },
+        "launch_plan": launch_plan_of(cfg, args.chunk, args.splits),
         "peak_extra_hbm_gb": peak_extra / 1e9,
         "loss": loss_val,
         "step_roofline": {

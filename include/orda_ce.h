@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define ORDA_ABI_VERSION 2
+#define ORDA_ABI_VERSION 3
 
 /* Teacher modes (reference api.py:21-52, ops/separate_teacher.py:1102). */
 enum orda_mode {
@@ -113,8 +113,17 @@ typedef struct orda_problem {
   float kl_weight;
   float div_alpha;        /* alpha of renyi, amari_alpha, ab, skew_*_kl       */
   float div_beta;         /* beta of jsd and ab                               */
-  int32_t reserved;
-  int64_t token_chunk;    /* tokens per chunk with ORDA_GRADS_IN_FORWARD;
+  int32_t grad_hidden_splits; /* ORDA_GRADS_IN_FORWARD: split-K count of the
+                             grad-hidden GEMM (contraction over V), 1..64;
+                             0 = the gfx950 launch table (rule-based for
+                             shapes it does not list).  Raised when needed
+                             so each split's K range of its MN-major operands
+                             stays below 2^31 bytes (one buffer resource)  */
+  int64_t token_chunk;    /* ORDA_GRADS_IN_FORWARD: requested tokens per
+                             chunk, the reference's chunk_size; the library's
+                             chunk is this times the launch table's
+                             chunk_scale (2; 4 when precomputed logits are
+                             read in place), at most 2^21 tokens.
                              0 = library choice (chunk logits <= 512 MiB)     */
 } orda_problem_t;
 
@@ -165,6 +174,31 @@ size_t orda_forward_workspace_bytes(const orda_problem_t* p);
 /* Scratch bytes orda_backward needs for p->vocab_chunk (0: library choice).
  * Bounded by O(vocab_chunk x N + N x H): no [N x V] tensor is ever formed. */
 size_t orda_backward_workspace_bytes(const orda_problem_t* p);
+
+/* The launch plan orda_forward would use for p (host-side, no device work).
+ * Replaces the reference's launch-config lookup (utils/_autotune.py:94-106
+ * default_config, :255-340 select_config): the fixed gfx950 table of
+ * launch_table.hpp for measured shapes, a rule for others. */
+typedef struct orda_plan_info {
+  int32_t grads_in_forward;      /* 1: gradients-in-forward schedule          */
+  int32_t table_entry;           /* launch-table row used, -1 = rule          */
+  int32_t teacher_class;         /* 0 tied, 1 staged, 2 in place, 3 other     */
+  int32_t scan_engine;           /* 0 two-stage (8 waves), 1 ring (4 waves)   */
+  int64_t token_chunk;           /* tokens per chunk                          */
+  int64_t n_token_chunks;
+  int32_t chunk_scale;           /* token_chunk / requested chunk             */
+  int32_t scan_tokens_per_tile;  /* tokens of one scan workgroup tile         */
+  int32_t scan_workgroups;       /* workgroups of one chunk's scan            */
+  int32_t grad_hidden_splits;    /* student grad hidden split-K               */
+  int32_t grad_teacher_hidden_splits;
+  int32_t reserved;
+  int64_t vocab_rows_per_split;  /* K rows of one grad-hidden split           */
+  int64_t vocab_chunk;           /* two-phase backward vocabulary chunk       */
+  uint64_t forward_workspace_bytes;
+  uint64_t backward_workspace_bytes;
+} orda_plan_info_t;
+
+int orda_plan_info(const orda_problem_t* p, orda_plan_info_t* out);
 
 /* Forward: losses and per-row statistics.  Replaces the chunk loop of
  * TiedCEFunction.forward (ops/tied_teacher.py:366-516),

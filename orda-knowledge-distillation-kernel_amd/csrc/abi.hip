@@ -12,6 +12,7 @@
 
 #include "../../include/orda_ce.h"
 #include "launch.hpp"
+#include "launch_table.hpp"
 #include "orda_core.hpp"
 
 using namespace orda;
@@ -47,11 +48,20 @@ constexpr int64_t kDefaultStagingBytes = 512ll << 20;
 constexpr int64_t kScanTargetGroups = 2048;
 // Default size of one token chunk's materialised logits (ORDA_GRADS_IN_FORWARD).
 constexpr int64_t kFusedLogitsBytes = 512ll << 20;
-// Workgroups of one chunk's scan: one per CU of an MI355X (256 CUs, one
-// 144 KiB-LDS workgroup each), so each walks a long run of vocabulary tiles.
-constexpr int64_t kFusedScanGroups = 256;
-// Target number of workgroups of a split-K grad-hidden GEMM.
+// Workgroups of one chunk's scan and of the persistent GEMMs: one per CU of
+// an MI355X (256 CUs, one 160 KiB-LDS workgroup each), so each walks a long
+// run of tiles.
+constexpr int64_t kPersistentGroups = 256;
+// Target number of workgroups of a split-K grad-hidden GEMM (rule for shapes
+// outside the launch table).
 constexpr int64_t kSplitTargetGroups = 512;
+// The ring engine addresses an MN-major operand's K range of one split as one
+// buffer resource whose record count is a 32-bit byte count.
+constexpr int64_t kRsrcBytes = 0x7fffffffll;
+// Largest hidden size (K-major rows of 128 x hidden x 4 bytes stay below 2^31)
+// and largest tokens per chunk (the chunk buffer's rows, 2 x chunk columns).
+constexpr int64_t kMaxHidden = 1ll << 22;
+constexpr int64_t kMaxChunkTokens = 1ll << 21;
 
 struct Plan {
   int mode, dtype, eb, kelems;
@@ -71,6 +81,7 @@ struct Plan {
   size_t off_hT, off_htT, off_dLT, off_dLNs, off_dLNt, off_WT, off_WtT, off_g32s, off_g32t, bwd_bytes;
   // gradients inside forward (materialised token chunks)
   bool fused, store_t, f_tl, f_tmem;
+  int tclass, table_entry, chunk_scale, scan_groups;
   int64_t fn, fnP, fldL, fnchunks;
   int f_nvr, f_tpr, splits_s, splits_t;
   int64_t kps_s, kps_t;
@@ -79,6 +90,12 @@ struct Plan {
 };
 
 constexpr int kScalFloats = 64;  // scalars at the head of the saved buffer
+
+#define ORDA_TRY_PLAN(expr)         \
+  do {                              \
+    int rc_ = (expr);               \
+    if (rc_ != ORDA_OK) return rc_; \
+  } while (0)
 
 int make_plan(const orda_problem_t* p, Plan& pl) {
   pl = Plan{};
@@ -92,8 +109,11 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
   if (p->n_rows <= 0 || p->vocab <= 0 || p->hidden <= 0)
     return fail(ORDA_EINVAL, "n_rows, vocab and hidden must be > 0 (got %lld, %lld, %lld)",
                 (long long)p->n_rows, (long long)p->vocab, (long long)p->hidden);
-  if (p->n_rows > (1ll << 30) || p->vocab > (1ll << 30) || p->hidden > (1ll << 24))
-    return fail(ORDA_EINVAL, "shape too large");
+  if (p->n_rows > (1ll << 30) || p->vocab > (1ll << 30) || p->hidden > kMaxHidden ||
+      (p->mode != ORDA_MODE_TIED && p->teacher_hidden > kMaxHidden))
+    return fail(ORDA_EINVAL, "shape too large (n_rows and vocab <= 2^30, hidden <= 2^22)");
+  if (p->grad_hidden_splits < 0 || p->grad_hidden_splits > 64)
+    return fail(ORDA_EINVAL, "grad_hidden_splits must be in [0, 64], got %d", p->grad_hidden_splits);
   if (!(p->temperature > 0.f) || !std::isfinite(p->temperature))
     return fail(ORDA_EINVAL, "temperature must be > 0, got %g", (double)p->temperature);
   if (p->student_ce_weight < 0.f || p->teacher_ce_weight < 0.f || p->kl_weight < 0.f)
@@ -166,7 +186,7 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
   // forward plan
   pl.n_ttiles = (int)cdiv(pl.N, 128);
   pl.n_vtiles = (int)cdiv(pl.V, 256);
-  int64_t nvr = cdiv(kScanTargetGroups, pl.n_ttiles);
+  int64_t nvr = cdiv(kScanTargetGroups, pl.n_ttiles);  // two-phase scan
   if (nvr < 1) nvr = 1;
   if (nvr > pl.n_vtiles) nvr = pl.n_vtiles;
   pl.tiles_per_range = (int)cdiv(pl.n_vtiles, nvr);
@@ -247,49 +267,77 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.store_t = pl.tsrc != TSRC_NONE && !pl.f_tmem;
     const int64_t ncol = pl.store_t ? 2 : 1;
     const int64_t Nr = round_up(pl.N, 8);
+    // launch geometry: the gfx950 table for measured shapes, else the rule
+    pl.tclass = pl.f_tmem                                           ? TC_INPLACE
+                : pl.f_tl                                           ? TC_STAGED
+                : (pl.tsrc == TSRC_SHARED && pl.eb == 2 && pl.H > 64) ? TC_TIED
+                                                                    : TC_OTHER;
+    pl.table_entry = find_launch_entry(pl.tclass, pl.dtype, pl.V, pl.H);
+    const LaunchEntry* te = pl.table_entry >= 0 ? &kLaunchTable[pl.table_entry] : nullptr;
+    pl.chunk_scale = te ? te->chunk_scale : (pl.f_tmem ? 4 : 2);
+    pl.scan_groups = te ? te->scan_groups : (int)kPersistentGroups;
     int64_t n = p->token_chunk;
     if (n > 0) {
-      n = round_up(n * (pl.f_tmem ? 2 : 1), 8);
+      n = round_up(n * pl.chunk_scale, 8);
     } else {
       n = kFusedLogitsBytes / (pl.V * ncol * pl.eb) / 128 * 128;
       if (n < 128) n = 128;
     }
     if (n > Nr) n = Nr;
+    if (n > kMaxChunkTokens) n = kMaxChunkTokens;
     pl.fn = n;
     pl.fnP = round_up(n, 8);
     pl.fldL = ncol * pl.fnP;
     pl.fnchunks = cdiv(pl.N, n);
     const int64_t ntt = cdiv(n, pl.f_tl ? 256 : 128);
-    int64_t nvr = cdiv(kFusedScanGroups, ntt);
+    int64_t nvr = cdiv(pl.scan_groups, ntt);
     if (nvr < 1) nvr = 1;
     if (nvr > pl.n_vtiles) nvr = pl.n_vtiles;
     pl.f_tpr = (int)cdiv(pl.n_vtiles, nvr);
     pl.f_nvr = (int)cdiv(pl.n_vtiles, pl.f_tpr);
-    auto split_plan = [&](int64_t cols, int& splits, int64_t& kps) {
-      // The persistent GEMM runs its tiles x splits equal work items in
-      // rounds of kFusedScanGroups workgroups, so its time goes as
-      // ceil(items / groups) / splits: pick the split count (1..16) that
-      // minimises it (a partial last round idles CUs: 80 tiles x 7 splits is
-      // 3 rounds at 73% fill, x 16 is 5 full ones), the one nearest
-      // kSplitTargetGroups / tiles among equals.
-      const int64_t tiles = cdiv(n, 256) * cdiv(cols, 256);
-      int64_t want = cdiv(kSplitTargetGroups, tiles);
-      if (want > 16) want = 16;
+    // the table's split count is measured for the student's hidden size (the
+    // tied teacher's too); a separate teacher's own grad hidden takes the rule
+    auto split_plan = [&](int64_t cols, int& splits, int64_t& kps) -> int {
       int64_t sp = 1;
-      double best = 1e30;
-      for (int64_t c = 1; c <= 16; ++c) {
-        const double cost = (double)cdiv(tiles * c, kFusedScanGroups) / (double)c;
-        const bool nearer = std::llabs(c - want) < std::llabs(sp - want);
-        if (cost < best * (1.0 - 1e-9) || (cost <= best * (1.0 + 1e-9) && nearer)) {
-          best = cost;
-          sp = c;
+      if (p->grad_hidden_splits > 0) {
+        sp = p->grad_hidden_splits;
+      } else if (te && cols == pl.H) {
+        sp = te->splits_h;
+      } else {
+        // Rule: the persistent GEMM runs its tiles x splits equal work items
+        // in rounds of kPersistentGroups workgroups, so its time goes as
+        // ceil(items / groups) / splits: pick the split count (1..16) that
+        // minimises it (a partial last round idles CUs: 80 tiles x 7 splits
+        // is 3 rounds at 73% fill, x 16 is 5 full ones), the one nearest
+        // kSplitTargetGroups / tiles among equals.
+        const int64_t tiles = cdiv(n, 256) * cdiv(cols, 256);
+        int64_t want = cdiv(kSplitTargetGroups, tiles);
+        if (want > 16) want = 16;
+        double best = 1e30;
+        for (int64_t c = 1; c <= 16; ++c) {
+          const double cost = (double)cdiv(tiles * c, kPersistentGroups) / (double)c;
+          const bool nearer = std::llabs(c - want) < std::llabs(sp - want);
+          if (cost < best * (1.0 - 1e-9) || (cost <= best * (1.0 + 1e-9) && nearer)) {
+            best = cost;
+            sp = c;
+          }
         }
       }
+      // each split's K range of both MN-major operands (the chunk's dlogits,
+      // ld = fldL, and the weight, ld = cols) must stay inside one 32-bit
+      // buffer resource
+      const int64_t ldmax = std::max<int64_t>(pl.fldL, cols) * pl.eb;
+      const int64_t kmax = kRsrcBytes / ldmax / 64 * 64;
+      if (kmax < 64) return fail(ORDA_EINVAL, "vocab rows of %lld bytes exceed a buffer resource", (long long)ldmax);
+      const int64_t need = cdiv(pl.V, kmax);
+      if (need > 64) return fail(ORDA_EINVAL, "grad hidden needs %lld splits of the vocabulary (at most 64)", (long long)need);
+      if (sp < need) sp = need;
       kps = round_up(cdiv(pl.V, sp), 64);
       splits = (int)cdiv(pl.V, kps);
+      return ORDA_OK;
     };
-    split_plan(pl.H, pl.splits_s, pl.kps_s);
-    split_plan(pl.Ht, pl.splits_t, pl.kps_t);
+    ORDA_TRY_PLAN(split_plan(pl.H, pl.splits_s, pl.kps_s));
+    ORDA_TRY_PLAN(split_plan(pl.Ht, pl.splits_t, pl.kps_t));
     size_t fo = 0;
     pl.off_L = carve(fo, (size_t)pl.V * pl.fldL * pl.eb);
     pl.off_fpart = carve(fo, (size_t)pl.f_nvr * kNStat * pl.fnP * 4);
@@ -355,14 +403,21 @@ struct Timed {
       std::lock_guard<std::mutex> lk(g_timing_mu);
       rec = TimedLaunch{pooled_event(), pooled_event(), kind, alg, exe};
     }
-    if (!rec.start || !rec.stop) { on = false; return; }
-    hipEventRecord(rec.start, s);
+    if (!rec.start || !rec.stop || hipEventRecord(rec.start, s) != hipSuccess) drop();
   }
   ~Timed() {
     if (!on) return;
-    hipEventRecord(rec.stop, s);
+    if (hipEventRecord(rec.stop, s) != hipSuccess) { drop(); return; }
     std::lock_guard<std::mutex> lk(g_timing_mu);
     g_launches.push_back(rec);
+  }
+  // a launch whose events could not be recorded is not timed (its events go
+  // back to the pool)
+  void drop() {
+    on = false;
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    if (rec.start) g_event_pool.push_back(rec.start);
+    if (rec.stop) g_event_pool.push_back(rec.stop);
   }
 };
 
@@ -902,6 +957,42 @@ size_t orda_backward_workspace_bytes(const orda_problem_t* p) {
   Plan pl;
   if (make_plan(p, pl) != ORDA_OK) return 0;
   return pl.bwd_bytes;
+}
+
+int orda_plan_info(const orda_problem_t* p, orda_plan_info_t* out) {
+  g_err.clear();
+  if (!out) return fail(ORDA_EINVAL, "out is NULL");
+  Plan pl;
+  ORDA_TRY(make_plan(p, pl));
+  *out = orda_plan_info_t{};
+  out->grads_in_forward = pl.fused ? 1 : 0;
+  out->table_entry = pl.fused ? pl.table_entry : -1;
+  out->teacher_class = pl.fused ? pl.tclass : -1;
+  out->vocab_chunk = pl.Vc;
+  out->forward_workspace_bytes = pl.fwd_bytes;
+  out->backward_workspace_bytes = pl.bwd_bytes;
+  if (pl.fused) {
+    // the ring scan runs 16-bit tied teachers (two tokens per lane) and
+    // teacher logits from memory of the non-power families (four tokens per
+    // lane); the rest the two-stage engine
+    const bool ring = pl.tclass == TC_TIED || pl.f_tl;
+    out->scan_engine = ring ? 1 : 0;
+    out->token_chunk = pl.fn;
+    out->n_token_chunks = pl.fnchunks;
+    out->chunk_scale = pl.chunk_scale;
+    out->scan_tokens_per_tile = pl.f_tl ? 256 : 128;
+    out->scan_workgroups = (int)(cdiv(pl.fn, pl.f_tl ? 256 : 128) * pl.f_nvr);
+    out->grad_hidden_splits = pl.splits_s;
+    out->grad_teacher_hidden_splits = pl.splits_t;
+    out->vocab_rows_per_split = pl.kps_s;
+  } else {
+    out->scan_engine = 0;
+    out->token_chunk = pl.N;
+    out->n_token_chunks = 1;
+    out->scan_tokens_per_tile = 128;
+    out->scan_workgroups = pl.n_ttiles * pl.n_vranges;
+  }
+  return ORDA_OK;
 }
 
 int orda_forward(const orda_problem_t* p, const orda_tensors_t* t, void* workspace, size_t workspace_bytes,

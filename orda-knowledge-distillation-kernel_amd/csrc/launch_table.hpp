@@ -1,0 +1,78 @@
+// launch_table.hpp -- the gfx950 launch table of the gradients-in-forward
+// schedule (host side, read by make_plan in abi.hip).
+//
+// The reference tunes a Triton (BLOCK_SIZE, num_warps) pair per mode and shape
+// (src/orda_ce_kernel/utils/_autotune.py:34-46 DEFAULT_CONFIGS, :255-340
+// select_config).  Here the tile is fixed per engine (256 x 256 workgroup
+// tiles; the ring engine for 16-bit operands, the two-stage engine for fp32)
+// and what is chosen per shape is the launch geometry around it:
+//
+//   chunk_scale  tokens per chunk = chunk_scale x the requested chunk (the
+//                reference's chunk_size); a chunk's logits live in HBM, so
+//                this trades grad-W K depth (fewer bf16 read-modify-write
+//                passes, fewer per-tile epilogues per token) against memory
+//   splits_h     split-K count of the grad-hidden GEMM (contraction over V):
+//                the 256 persistent workgroups run tiles x splits items, so
+//                it sets how full the last round is
+//   scan_groups  workgroups of one chunk's scan (one per CU)
+//
+// Entries are keyed by (teacher class, dtype, vocabulary, student hidden) and
+// were chosen by sweeping on an MI355X (the sweep and its timings are in the
+// repository's profiles, launch_table_sweep.md); every other shape takes the
+// rule in choose_launch().
+#pragma once
+
+#include <stdint.h>
+
+namespace orda {
+
+// How a chunk's teacher logits reach the scan.
+enum TeacherClass {
+  TC_TIED = 0,     // teacher GEMM inside the scan, sharing W's tiles
+  TC_STAGED = 1,   // written to the chunk buffer first (separate / frozen
+                   // hidden teachers, precomputed logits not read in place)
+  TC_INPLACE = 2,  // precomputed logits read in place (compute dtype, V % 8 == 0)
+  TC_OTHER = 3     // no teacher, fp32, power-family divergences with a
+                   // staged teacher (two-stage scan)
+};
+
+struct LaunchEntry {
+  int tclass;
+  int dtype;  // ORDA_BF16 / ORDA_F16 / ORDA_F32
+  int64_t vocab, hidden;
+  int chunk_scale;
+  int splits_h;
+  int scan_groups;
+  const char* evidence;  // the sweep row the entry comes from
+};
+
+// dtype 0 = bf16 (orda_dtype).
+constexpr LaunchEntry kLaunchTable[] = {
+    // config 2: tied, N = 8192, H = 4096, V = 128256.  1024-token chunks
+    // (2048 would pass the 2 GB memory ceiling); 4 splits: 41.5 ms/step vs
+    // 41.8-42.2 for 8-16 and 46.2-49.1 with 512-token chunks
+    {TC_TIED, 0, 128256, 4096, 2, 4, 256, "c2: chunk 512 x 2, split 4"},
+    // config 3: separate, Hs = 2048 (teacher 4096), V = 128256.  2048-token
+    // chunks: 22.6 ms/step vs 24.3 with 1024 (grad W K twice as deep); 4
+    // splits (8, 16 within noise, more scratch)
+    {TC_STAGED, 0, 128256, 2048, 4, 4, 256, "c3: chunk 512 x 4, split 4"},
+    // config 4: precomputed logits read in place, H = 4096, V = 128256.
+    // 2048-token chunks: 25.7 ms/step vs 27.8 with 1024; split 2 = 4 within noise,
+    // 67 MB less split-K scratch
+    {TC_INPLACE, 0, 128256, 4096, 4, 2, 256, "c4: chunk 512 x 4, split 2"},
+    // config 5: tied, N = 32768, H = 5120, V = 152064.  16 splits fill whole
+    // rounds (80 tiles x 16 = 5 x 256): 240.3 ms/step vs 241.9 (12), 245.5 (8)
+    {TC_TIED, 0, 152064, 5120, 2, 16, 256, "c5: chunk 512 x 2, split 16"},
+};
+constexpr int kLaunchTableSize = (int)(sizeof(kLaunchTable) / sizeof(kLaunchTable[0]));
+
+// Index of the entry for this shape, or -1.
+inline int find_launch_entry(int tclass, int dtype, int64_t vocab, int64_t hidden) {
+  for (int i = 0; i < kLaunchTableSize; ++i) {
+    const LaunchEntry& e = kLaunchTable[i];
+    if (e.tclass == tclass && e.dtype == dtype && e.vocab == vocab && e.hidden == hidden) return i;
+  }
+  return -1;
+}
+
+}  // namespace orda

@@ -15,12 +15,12 @@ from pathlib import Path
 import torch
 
 __all__ = [
-    "ABI_VERSION", "Problem", "Tensors", "library", "library_path", "forward", "forward_static", "backward",
+    "ABI_VERSION", "PlanInfo", "Problem", "Tensors", "library", "plan_info", "library_path", "forward", "forward_static", "backward",
     "saved_bytes", "forward_workspace_bytes", "backward_workspace_bytes", "gemm_abt", "gemm",
     "MODE", "DTYPE", "FLAG", "KERNEL_CLASSES", "timing_enable", "timing_collect",
 ]
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MODE = {"tied": 0, "separate": 1, "precomputed_logits": 2, "precomputed_hidden": 3}
 DTYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
@@ -58,8 +58,31 @@ class Problem(ctypes.Structure):
         ("kl_weight", ctypes.c_float),
         ("div_alpha", ctypes.c_float),
         ("div_beta", ctypes.c_float),
-        ("reserved", ctypes.c_int32),
+        ("grad_hidden_splits", ctypes.c_int32),
         ("token_chunk", ctypes.c_int64),
+    ]
+
+
+class PlanInfo(ctypes.Structure):
+    """orda_plan_info_t"""
+
+    _fields_ = [
+        ("grads_in_forward", ctypes.c_int32),
+        ("table_entry", ctypes.c_int32),
+        ("teacher_class", ctypes.c_int32),
+        ("scan_engine", ctypes.c_int32),
+        ("token_chunk", ctypes.c_int64),
+        ("n_token_chunks", ctypes.c_int64),
+        ("chunk_scale", ctypes.c_int32),
+        ("scan_tokens_per_tile", ctypes.c_int32),
+        ("scan_workgroups", ctypes.c_int32),
+        ("grad_hidden_splits", ctypes.c_int32),
+        ("grad_teacher_hidden_splits", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("vocab_rows_per_split", ctypes.c_int64),
+        ("vocab_chunk", ctypes.c_int64),
+        ("forward_workspace_bytes", ctypes.c_uint64),
+        ("backward_workspace_bytes", ctypes.c_uint64),
     ]
 
 
@@ -127,6 +150,8 @@ def library() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [P, T, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.orda_plan_info.restype = ctypes.c_int
+        lib.orda_plan_info.argtypes = [P, ctypes.POINTER(PlanInfo)]
         lib.orda_forward_static.restype = ctypes.c_int
         lib.orda_forward_static.argtypes = [P, T, ctypes.c_void_p]
         lib.orda_gemm_abt.restype = ctypes.c_int
@@ -176,6 +201,13 @@ def forward_workspace_bytes(problem: Problem) -> int:
 
 def backward_workspace_bytes(problem: Problem) -> int:
     return _size("orda_backward_workspace_bytes", problem)
+
+
+def plan_info(problem: Problem) -> dict:
+    """The launch plan orda_forward would use for ``problem`` (host only)."""
+    info = PlanInfo()
+    _check(library().orda_plan_info(ctypes.byref(problem), ctypes.byref(info)), "orda_plan_info")
+    return {name: getattr(info, name) for name, _ in PlanInfo._fields_ if name != "reserved"}
 
 
 def _stream(device: torch.device) -> int:

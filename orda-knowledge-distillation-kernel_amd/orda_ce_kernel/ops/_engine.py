@@ -62,15 +62,20 @@ def vocab_chunk_for(BT: int, V: int, chunk_size, max_chunks) -> int:
 
 
 def token_chunk_for(chunk_size) -> int:
-    """Tokens per chunk of the gradients-in-forward schedule: twice the
+    """Requested tokens per chunk of the gradients-in-forward schedule: the
     reference's chunk (``utils/resolver.py:28-62``, as the dispatcher passes
-    it).  A chunk keeps only its student and teacher logits (16-bit) in HBM;
-    twice the reference's token count keeps a 128K vocabulary near 0.5 GB,
-    and the dispatcher's OOM retry, which halves the chunk, still halves it.
-    0 lets the library choose."""
+    it).  The library's chunk is this times the gfx950 launch table's scale
+    (2, or 4 when precomputed logits are read in place): a chunk keeps only
+    its 16-bit logits in HBM, and the dispatcher's OOM retry, which halves
+    the chunk, still halves it.  0 lets the library choose."""
     if chunk_size is None or isinstance(chunk_size, str):
         return 0
-    return 2 * int(chunk_size)
+    return int(chunk_size)
+
+
+# Launch overrides for tuning sweeps (bench.py --splits): fields of
+# orda_problem_t set on every call when not None.  None = the launch table.
+LAUNCH_OVERRIDES: dict[str, int | None] = {"grad_hidden_splits": None}
 
 
 def grads_in_forward(mode: str, use_fp32_accum, divergence, any_grad: bool) -> bool:
@@ -171,6 +176,8 @@ def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None)
     p.div_alpha = float(div.alpha) if div.alpha is not None else 0.0
     p.div_beta = float(div.beta) if div.beta is not None else 0.0
     p.token_chunk = int(call.token_chunk)
+    splits = LAUNCH_OVERRIDES.get("grad_hidden_splits")
+    p.grad_hidden_splits = int(splits) if splits else 0
     return p
 
 

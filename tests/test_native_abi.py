@@ -26,7 +26,7 @@ def _declared_functions():
 
 def test_library_loads_with_matching_abi():
     lib = _native.library()
-    assert lib.orda_abi_version() == _native.ABI_VERSION == 2
+    assert lib.orda_abi_version() == _native.ABI_VERSION == 3
 
 
 def test_every_declared_function_is_exported():
@@ -52,8 +52,12 @@ int main(void) {
   printf("orda_problem_t %zu\n", sizeof(orda_problem_t));
   printf("orda_tensors_t %zu\n", sizeof(orda_tensors_t));
   printf("orda_timing_t %zu\n", sizeof(orda_timing_t));
+  printf("orda_plan_info_t %zu\n", sizeof(orda_plan_info_t));
   F(orda_problem_t, n_rows) F(orda_problem_t, vocab_chunk) F(orda_problem_t, flags) F(orda_problem_t, divergence)
-  F(orda_problem_t, temperature) F(orda_problem_t, div_beta) F(orda_problem_t, token_chunk)
+  F(orda_problem_t, temperature) F(orda_problem_t, div_beta) F(orda_problem_t, grad_hidden_splits)
+  F(orda_problem_t, token_chunk)
+  F(orda_plan_info_t, token_chunk) F(orda_plan_info_t, grad_hidden_splits) F(orda_plan_info_t, vocab_rows_per_split)
+  F(orda_plan_info_t, backward_workspace_bytes)
   F(orda_tensors_t, labels) F(orda_tensors_t, saved) F(orda_tensors_t, grad_output)
   F(orda_tensors_t, grad_teacher_weight)
   F(orda_timing_t, milliseconds) F(orda_timing_t, executed_flops)
@@ -74,7 +78,8 @@ def test_struct_layout_matches_the_header(tmp_path):
     subprocess.run([gcc, "-std=c11", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
     got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
                                                                check=True).stdout.splitlines())
-    P, T, Ti = _native.Problem, _native.Tensors, _native.Timing
+    P, T, Ti, Pi = _native.Problem, _native.Tensors, _native.Timing, _native.PlanInfo
+    assert int(got["orda_plan_info_t"]) == ctypes.sizeof(Pi)
     assert int(got["orda_problem_t"]) == ctypes.sizeof(P)
     assert int(got["orda_tensors_t"]) == ctypes.sizeof(T)
     assert int(got["orda_timing_t"]) == ctypes.sizeof(Ti)
@@ -82,7 +87,7 @@ def test_struct_layout_matches_the_header(tmp_path):
         if "." not in key:
             continue
         struct, field = key.split(".")
-        cls = {"orda_problem_t": P, "orda_tensors_t": T, "orda_timing_t": Ti}[struct]
+        cls = {"orda_problem_t": P, "orda_tensors_t": T, "orda_timing_t": Ti, "orda_plan_info_t": Pi}[struct]
         assert getattr(cls, field).offset == int(value), key
     assert int(got["ORDA_DIV_COUNT"]) == 15
     assert int(got["ORDA_K_COUNT"]) == len(_native.KERNEL_CLASSES)
@@ -172,7 +177,7 @@ def test_grads_in_forward_plan_for_the_headline_shape():
     # one token chunk of student + teacher logits (1024 tokens x V x 2 x bf16)
     # plus split-K partials and row state; far below an [N x V] tensor
     assert 1024 * 128256 * 2 * 2 < ws < 900 << 20
-    p.token_chunk = 512
+    p.token_chunk = 256  # requested chunk x 2 = 512 tokens
     assert _native.forward_workspace_bytes(p) < ws
     # the backward only scales the gradients: no workspace
     assert lib_backward_bytes(p) == 0
@@ -208,3 +213,72 @@ def test_timing_hook_without_launches_reports_zeros():
     _native.timing_enable(False)
     assert set(rows) == set(_native.KERNEL_CLASSES)
     assert all(r["launches"] == 0 for r in rows.values())
+
+
+# ------------------------------------------------------------ launch table
+def _cfg_problem(cfg):
+    """orda_problem_t of a benchmark configuration, as the Python layer builds
+    it for the default call (the dispatcher's auto chunk: 512 tokens)."""
+    if cfg == "c2":
+        return _problem(flags=0x33 | GIF, token_chunk=512)
+    if cfg == "c3":  # separate, student-only Function (teacher CE off), reverse KL
+        return _problem(mode=1, hidden=2048, teacher_hidden=4096, flags=0x23 | GIF, teacher_ce_weight=0.0,
+                        divergence=1, temperature=2.0, token_chunk=512)
+    if cfg == "c4":  # precomputed bf16 logits read in place
+        return _problem(mode=2, flags=0x23 | GIF, teacher_ce_weight=0.0, logits_dtype=0, token_chunk=512)
+    if cfg == "c5":
+        return _problem(n_rows=32768, hidden=5120, teacher_hidden=5120, vocab=152064, flags=0x33 | GIF,
+                        token_chunk=512)
+    raise ValueError(cfg)
+
+
+@pytest.mark.parametrize("cfg, entry, chunk, splits, tclass", [
+    ("c2", 0, 1024, 4, 0), ("c3", 1, 2048, 4, 1), ("c4", 2, 2048, 2, 2), ("c5", 3, 1024, 16, 0)])
+def test_launch_table_drives_the_benchmark_configurations(cfg, entry, chunk, splits, tclass):
+    """Each benchmark configuration finds its row of the gfx950 launch table
+    (csrc/launch_table.hpp) and takes its chunk scale and split count."""
+    info = _native.plan_info(_cfg_problem(cfg))
+    assert info["grads_in_forward"] == 1
+    assert info["table_entry"] == entry
+    assert info["teacher_class"] == tclass
+    assert info["token_chunk"] == chunk and info["chunk_scale"] == chunk // 512
+    assert info["grad_hidden_splits"] == splits
+    assert info["scan_engine"] == 1  # the ring engine
+    assert info["scan_workgroups"] <= 256
+    # the plan's workspace is the one orda_forward_workspace_bytes reports
+    assert info["forward_workspace_bytes"] == _native.forward_workspace_bytes(_cfg_problem(cfg))
+
+
+def test_launch_overrides_and_rule_for_unlisted_shapes():
+    p = _cfg_problem("c2")
+    p.grad_hidden_splits = 12
+    assert _native.plan_info(p)["grad_hidden_splits"] == 12
+    # a shape the table does not list takes the rule (round-filling split count)
+    q = _problem(hidden=3072, teacher_hidden=3072, flags=0x33 | GIF, token_chunk=512)
+    info = _native.plan_info(q)
+    assert info["table_entry"] == -1 and info["chunk_scale"] == 2
+    tiles = (1024 // 256) * (3072 // 256)
+    s = info["grad_hidden_splits"]
+    assert (tiles * s) % 256 == 0 or tiles * s < 256
+    # the two-phase schedule has no token chunks
+    r = _problem(flags=0x33)
+    assert _native.plan_info(r)["grads_in_forward"] == 0
+
+
+def test_grad_hidden_splits_keep_each_split_inside_a_buffer_resource():
+    """H = 8192, V = 262144, 4096-token chunks: the whole W (4 GiB of bf16)
+    exceeds one 32-bit buffer resource, so the grad-hidden GEMM is split at
+    least until each split's K range of W and of the chunk's logits fits,
+    whatever the requested split count."""
+    for requested in (0, 1):
+        p = _problem(hidden=8192, teacher_hidden=8192, vocab=262144, flags=0x33 | GIF, token_chunk=2048,
+                     grad_hidden_splits=requested)
+        info = _native.plan_info(p)
+        assert info["token_chunk"] == 4096
+        ld_bytes = max(8192, 2 * 4096) * 2
+        assert info["vocab_rows_per_split"] * ld_bytes < 2 ** 31
+        assert info["grad_hidden_splits"] >= 3
+    with pytest.raises(ValueError, match="shape too large"):
+        _native.plan_info(_problem(hidden=1 << 23, teacher_hidden=1 << 23))
+    with pytest.raises(ValueError, match="grad_hidden_splits"):
+        _native.plan_info(_problem(grad_hidden_splits=65))
