@@ -475,11 +475,11 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int64_t v = v0 + wm * 128 + acc_row(mb, g * 4, lane) + q;
-        float x[4], o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = acc_get(acc[mb][nb], g * 4 + e);
-        quad_transpose(x, o);
-        if (v < P.V && tok_ok) store4(L + v * P.ldL + col, o, true, 4);
+        uint32_t x[2], o[2];
+        x[0] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 0), acc_get(acc[mb][nb], g * 4 + 1));
+        x[1] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 2), acc_get(acc[mb][nb], g * 4 + 3));
+        quad_transpose16(x, o);
+        if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + col) = make_uint2(o[0], o[1]);
         __builtin_amdgcn_sched_barrier(0);
       }
   }
@@ -538,11 +538,17 @@ template <class T, int TL>
 __device__ __forceinline__ void finish_teacher4(const uint2 (&raw)[16], f32x16 (&tv)[4]) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    float x[4], o[4];
-    unpack_raw4<T>(raw[i], x);
-    if constexpr (TL == TL_FROM_L) quad_transpose(x, o);
+    uint2 r = raw[i];
+    if constexpr (TL == TL_FROM_L) {
+      const uint32_t x[2] = {r.x, r.y};
+      uint32_t o[2];
+      quad_transpose16(x, o);
+      r = make_uint2(o[0], o[1]);
+    }
+    float x[4];
+    unpack_raw4<T>(r, x);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) tv[i >> 2][(i & 3) * 4 + e] = TL == TL_FROM_L ? o[e] : x[e];
+    for (int e = 0; e < 4; ++e) tv[i >> 2][(i & 3) * 4 + e] = x[e];
   }
 }
 // Token block nb's teacher logits (registers, accumulator layout) to Lout's
@@ -559,11 +565,12 @@ __device__ __forceinline__ void store_teacher4(const f32x16 (&tv)[4], const Fuse
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane) + q;
-    float x[4], o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = tv[i >> 2][(i & 3) * 4 + e];
-    quad_transpose(x, o);
-    if (v < P.V && tok_ok) store4(L + v * P.ldL + P.tcolL + tb, o, true, 4);
+    const f32x16& t = tv[i >> 2];
+    const int e0 = (i & 3) * 4;
+    const uint32_t x[2] = {pack2<T>(t[e0], t[e0 + 1]), pack2<T>(t[e0 + 2], t[e0 + 3])};
+    uint32_t o[2];
+    quad_transpose16(x, o);
+    if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + P.tcolL + tb) = make_uint2(o[0], o[1]);
   }
 }
 struct AccPairTL {  // student from accumulator block nb, teacher from registers
@@ -1156,9 +1163,82 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
       return;
     }
     T* C = static_cast<T*>(P.C) + (int64_t)x.m0 * ldc + x.n0;
+    // 16-byte accesses need 16-byte aligned rows (uniform test: the library's
+    // own outputs always pass; the general entry may not)
+    const bool wide = sizeof(T) == 2 && ldc % 8 == 0 && reinterpret_cast<uintptr_t>(P.C) % 16 == 0;
+    if (mlim == 256 && nlim == 256 && wide) {
+      // Interior tile, 16-byte accesses.  Lanes l and l + 32 hold the two
+      // 4-column halves of each 8-column group of the same row;
+      // v_permlane32_swap trades lane l's half of group g + 1 for lane
+      // l + 32's half of group g (no LDS round trip), so lane l then holds
+      // group g whole and lane l + 32 group g + 1: one 16-byte store each.
+      // GEMM_ACC_T trades the fp32 sums, adds the 8 old values of the lane's
+      // group (one 16-byte load) and rounds once.  The loads of C for two
+      // row blocks go out before the first add, so one memory latency covers
+      // 16 groups.
+      const bool hi = lane >= 32;
+      const int cq = wn * 64;  // tile column of the lanes' 8-column group 0, block 0
+      auto gcol = [&](int nb, int g) { return cq + col(nb, g + (hi ? 1 : 0)); };
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        uint4 cv[2][4][2];
+        if constexpr (MODE == GEMM_ACC_T) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const T* rp = C + (int64_t)(wm * 128 + (2 * hh + j) * 32 + (lane & 31)) * ldc;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+              for (int q = 0; q < 2; ++q) cv[j][nb][q] = *reinterpret_cast<const uint4*>(rp + gcol(nb, 2 * q));
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int mb = 2 * hh + j;
+          T* rp = C + (int64_t)(wm * 128 + mb * 32 + (lane & 31)) * ldc;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const int g = 2 * q;
+              uint4 out;
+              if constexpr (MODE == GEMM_ACC_T) {
+                float lo[4], up[4];  // the lane's group after the trade: columns 0-3, 4-7
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const float a = acc_get(c[mb][nb], g * 4 + e), b = acc_get(c[mb][nb], (g + 1) * 4 + e);
+                  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                                  false);
+                  lo[e] = __uint_as_float(r[0]);
+                  up[e] = __uint_as_float(r[1]);
+                }
+                const uint4 old = cv[j][nb][q];
+                out.x = pack2<T>(lo[0] + lo16<T>(old.x), lo[1] + hi16<T>(old.x));
+                out.y = pack2<T>(lo[2] + lo16<T>(old.y), lo[3] + hi16<T>(old.y));
+                out.z = pack2<T>(up[0] + lo16<T>(old.z), up[1] + hi16<T>(old.z));
+                out.w = pack2<T>(up[2] + lo16<T>(old.w), up[3] + hi16<T>(old.w));
+              } else {
+                float a[4], b[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  a[e] = acc_get(c[mb][nb], g * 4 + e);
+                  b[e] = acc_get(c[mb][nb], (g + 1) * 4 + e);
+                }
+                const auto r0 = __builtin_amdgcn_permlane32_swap(pack2<T>(a[0], a[1]), pack2<T>(b[0], b[1]), false,
+                                                                 false);
+                const auto r1 = __builtin_amdgcn_permlane32_swap(pack2<T>(a[2], a[3]), pack2<T>(b[2], b[3]), false,
+                                                                 false);
+                out = make_uint4(r0[0], r1[0], r0[1], r1[1]);
+              }
+              *reinterpret_cast<uint4*>(rp + gcol(nb, g)) = out;
+              __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+      }
+      return;
+    }
     if (mlim == 256 && nlim == 256) {
-      // interior tile; for GEMM_ACC_T the reads of C for two row blocks go
-      // out before the first add, so one memory latency covers 32 groups
+      // interior tile, 8-byte accesses (rows not 16-byte aligned)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         uint2 cv[2][4][4];
@@ -1176,59 +1256,22 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
         for (int j = 0; j < 2; ++j) {
           const int mb = 2 * hh + j;
           T* rp = C + (int64_t)(wm * 128 + mb * 32 + (lane & 31)) * ldc + cl;
-          auto group = [&](int nb, int g, float (&o)[4]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
-            if constexpr (MODE == GEMM_ACC_T) {
-              union { T e[4]; uint2 u; } v;
-              v.u = cv[j][nb][g];
+          for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
+            for (int g = 0; g < 4; ++g) {
+              float o[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
+              if constexpr (MODE == GEMM_ACC_T) {
+                union { T e[4]; uint2 u; } v;
+                v.u = cv[j][nb][g];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
+              }
+              store4(rp + col(nb, g), o, true, 4);
+              __builtin_amdgcn_sched_barrier(0);
             }
-          };
-          // 16-byte stores need 16-byte aligned rows (uniform test: the
-          // library's own outputs always pass; the general entry may not)
-          const bool wide = sizeof(T) == 2 && ldc % 8 == 0 && reinterpret_cast<uintptr_t>(P.C) % 16 == 0;
-          if (wide) {
-            // lanes l and l + 32 hold the two 4-column halves of each 8-column
-            // group of the same row: exchanging one group of each pair (g,
-            // g + 1) gives lane l group g whole and lane l + 32 group g + 1
-            // whole, one 16-byte store each instead of two 8-byte stores
-            const bool hi = lane >= 32;
-            T* rq = rp - (hi ? 4 : 0);  // the row's 8-column group base
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-              for (int g = 0; g < 4; g += 2) {
-                float oa[4], ob[4];
-                group(nb, g, oa);
-                group(nb, g + 1, ob);
-                union { T e[4]; uint2 u; } pa, pb;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  pa.e[e] = from_f32<T>(oa[e]);
-                  pb.e[e] = from_f32<T>(ob[e]);
-                }
-                const uint2 send = hi ? pa.u : pb.u;
-                uint2 recv;
-                recv.x = __shfl_xor(send.x, 32);
-                recv.y = __shfl_xor(send.y, 32);
-                const uint4 out = hi ? make_uint4(recv.x, recv.y, pb.u.x, pb.u.y)
-                                     : make_uint4(pa.u.x, pa.u.y, recv.x, recv.y);
-                *reinterpret_cast<uint4*>(rq + col(nb, hi ? g + 1 : g)) = out;
-                __builtin_amdgcn_sched_barrier(0);
-              }
-          } else {
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-              for (int g = 0; g < 4; ++g) {
-                float o[4];
-                group(nb, g, o);
-                store4(rp + col(nb, g), o, true, 4);
-                __builtin_amdgcn_sched_barrier(0);
-              }
-          }
         }
       }
       return;

@@ -81,6 +81,25 @@ template <> struct Traits<float> {
 template <class T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
 template <class T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
 
+// Two floats rounded to a 16-bit type, packed low-first in one dword (one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950).
+template <class T>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef T t2v __attribute__((ext_vector_type(2)));
+  const f2v v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, t2v));
+}
+// The low / high 16-bit element of a packed dword, as float.
+template <class T>
+__device__ __forceinline__ float lo16(uint32_t u) {
+  return to_f32(__builtin_bit_cast(T, (unsigned short)(u & 0xffffu)));
+}
+template <class T>
+__device__ __forceinline__ float hi16(uint32_t u) {
+  return to_f32(__builtin_bit_cast(T, (unsigned short)(u >> 16)));
+}
+
 // Wave coordinates inside the workgroup tile (wave-uniform: scalar registers).
 __device__ __forceinline__ int wave_m() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 2; }  // 0..1
 __device__ __forceinline__ int wave_n() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3; }   // 0..3
@@ -120,6 +139,34 @@ template <int J>
 __device__ __forceinline__ float quad_rot(float v) {
   constexpr int ctrl = J == 1 ? 0x93 : J == 2 ? 0x4E : 0x39;  // perm[q] = (q - J) & 3
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+// Value of the 32-bit v held by lane (quad_perm ctrl) of this lane's quad.
+template <int CTRL>
+__device__ __forceinline__ uint32_t quad_dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+
+// 4 x 4 transpose of 16-bit values inside a lane quad, in two exchange
+// stages (lanes q ^ 2, then q ^ 1) of one packed dword each: lane q holds row
+// q of M as p[0] = (M[q][0], M[q][1]), p[1] = (M[q][2], M[q][3]) (low half
+// first); on return out[0] = (M[0][q], M[1][q]), out[1] = (M[2][q], M[3][q]).
+// Eight VALU instructions (v_perm_b32 byte selects, DPP moves) in place of
+// the ~32 of quad_transpose on unpacked floats.
+__device__ __forceinline__ void quad_transpose16(const uint32_t (&p)[2], uint32_t (&out)[2]) {
+  const int q = threadIdx.x & 3;
+  const bool top = q < 2, odd = (q & 1) != 0;
+  // stage 1: top lanes keep columns 0-1 and take rows q + 2's; bottom lanes
+  // keep columns 2-3 and take rows q - 2's.  Then A = row (q & 1), B = row
+  // (q & 1) + 2, both over columns c0, c0 + 1 with c0 = top ? 0 : 2.
+  const uint32_t r1 = quad_dpp<0x4E>(top ? p[1] : p[0]);
+  const uint32_t a = top ? p[0] : r1, b = top ? r1 : p[1];
+  // stage 2: even lanes collect column c0, odd lanes column c0 + 1; each
+  // sends the partner the halves it needs (even: A.hi, B.hi; odd: A.lo, B.lo)
+  const uint32_t send = __builtin_amdgcn_perm(b, a, odd ? 0x05040100u : 0x07060302u);
+  const uint32_t r = quad_dpp<0xB1>(send);
+  out[0] = __builtin_amdgcn_perm(r, a, odd ? 0x03020504u : 0x05040100u);  // even (A.lo, R.lo), odd (R.lo, A.hi)
+  out[1] = __builtin_amdgcn_perm(r, b, odd ? 0x03020706u : 0x07060100u);  // even (B.lo, R.hi), odd (R.hi, B.hi)
 }
 
 // 4 x 4 transpose inside a lane quad: lane q holds x[e] = M[q][e]; on return

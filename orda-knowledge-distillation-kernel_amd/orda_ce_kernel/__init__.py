@@ -19,6 +19,9 @@ from .api import (
 )
 
 
+from . import compiled  # noqa: E402,F401  (torch.compile-friendly entry; not in __all__)
+
+
 def is_available() -> bool:
     """True when the HIP kernels can be selected (library loaded and a HIP
     device present)."""

@@ -34,7 +34,8 @@ from .. import _native
 from .._runtime import HAS_NATIVE, native_error
 from ..divergences import Divergence, resolve_divergence
 
-__all__ = ["FusedCall", "cast_to", "fused_forward", "fused_backward", "vocab_chunk_for", "require_native",
+__all__ = ["FusedCall", "cast_to", "fused_forward", "fused_backward", "run_fused_call", "vocab_chunk_for",
+           "require_native",
            "grads_in_forward", "token_chunk_for"]
 
 
@@ -188,6 +189,26 @@ def fused_forward(ctx, call: FusedCall):
     Functions do that, as the reference does at ``ops/tied_teacher.py:334-344``).
     Returns ``(loss, student_ce, teacher_ce, kl)`` as fp32 0-dim tensors.
     """
+    outs, grads, state = run_fused_call(call)
+    problem, (H, Ht), inputs, saved = state
+    ctx.orda_problem = problem
+    ctx.orda_shapes = (H, Ht)
+    ctx.orda_mode = call.mode
+    ctx.save_for_backward(*inputs, saved)
+    # Gradients computed in forward: the first backward scales them in place
+    # and hands them to autograd, dropping this reference (so autograd can
+    # keep the buffers as .grad without a copy); a later backward through a
+    # retained graph recomputes them, so no returned tensor is ever scaled
+    # twice.
+    ctx.orda_grads = grads if call.grads_in_forward else None
+    return tuple(outs)
+
+
+def run_fused_call(call: FusedCall):
+    """orda_forward for ``call`` without autograd state.  Returns ``(outs,
+    grads, state)``: the four fp32 0-dim losses, the four gradients (None
+    where not computed; padded columns included) and ``(problem, (H, Ht),
+    padded inputs, saved)`` for a later backward."""
     require_native("the fused HIP path")
     dev = call.student_hidden.device
     if dev.type != "cuda":
@@ -219,19 +240,9 @@ def fused_forward(ctx, call: FusedCall):
     saved = torch.empty(_native.saved_bytes(problem), dtype=torch.uint8, device=dev)
     outs = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(4)]
     grads = _alloc_grads(problem.flags, hs, w, ht, wt) if call.grads_in_forward else (None,) * 4
-    _run_forward(problem, (hs, w, ht, wt, lt, labels), saved, outs, grads)
-
-    ctx.orda_problem = problem
-    ctx.orda_shapes = (H, Ht)
-    ctx.orda_mode = call.mode
-    ctx.save_for_backward(hs, w, ht, wt, lt, labels, saved)
-    # Gradients computed in forward: the first backward scales them in place
-    # and hands them to autograd, dropping this reference (so autograd can
-    # keep the buffers as .grad without a copy); a later backward through a
-    # retained graph recomputes them, so no returned tensor is ever scaled
-    # twice.
-    ctx.orda_grads = grads if call.grads_in_forward else None
-    return tuple(outs)
+    inputs = (hs, w, ht, wt, lt, labels)
+    _run_forward(problem, inputs, saved, outs, grads)
+    return outs, grads, (problem, (H, Ht), inputs, saved)
 
 
 def _run_forward(problem, inputs, saved, outs, grads) -> None:
