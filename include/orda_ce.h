@@ -30,14 +30,19 @@
 extern "C" {
 #endif
 
-#define ORDA_ABI_VERSION 3
+#define ORDA_ABI_VERSION 4
 
 /* Teacher modes (reference api.py:21-52, ops/separate_teacher.py:1102). */
 enum orda_mode {
   ORDA_MODE_TIED = 0,               /* student and teacher share W          */
   ORDA_MODE_SEPARATE = 1,           /* teacher (hidden_t, W_t)              */
   ORDA_MODE_PRECOMPUTED_LOGITS = 2, /* teacher logits [N x V] given         */
-  ORDA_MODE_PRECOMPUTED_HIDDEN = 3  /* frozen (hidden_t, W_t), no grads     */
+  ORDA_MODE_PRECOMPUTED_HIDDEN = 3, /* frozen (hidden_t, W_t), no grads     */
+  ORDA_MODE_TOPK = 4                /* teacher as k (id, log-prob) pairs per
+                                       row, renormalised over its ids; no
+                                       counterpart in the reference (its
+                                       precomputed teacher is [N x V] logits,
+                                       ops/precomputed_teacher.py:336-356)   */
 };
 
 /* Element types. */
@@ -125,6 +130,11 @@ typedef struct orda_problem {
                              chunk_scale (2; 4 when precomputed logits are
                              read in place), at most 2^21 tokens.
                              0 = library choice (chunk logits <= 512 MiB)     */
+  int64_t topk;           /* ORDA_MODE_TOPK: ids per row (1 <= topk <= V);
+                             the mode needs ORDA_GRADS_IN_FORWARD (with or
+                             without gradients), teacher CE off and the
+                             divergence ORDA_DIV_FORWARD_KL or
+                             ORDA_DIV_SOFT_TARGET_CE                          */
 } orda_problem_t;
 
 /* Tensors of one loss evaluation.  Unused pointers may be NULL. */
@@ -152,6 +162,10 @@ typedef struct orda_tensors {
   void* grad_weight;             /* [V x H]  dtype                          */
   void* grad_teacher_hidden;     /* [N x Ht] dtype                          */
   void* grad_teacher_weight;     /* [V x Ht] dtype                          */
+  /* ORDA_MODE_TOPK: per row, topk distinct vocabulary ids in [0, V) and the
+   * teacher's log-probabilities there (temperature 1)                        */
+  const int64_t* teacher_topk_indices; /* [N x topk]                          */
+  const float* teacher_topk_logprobs;  /* [N x topk] fp32                     */
 } orda_tensors_t;
 
 /* ABI version of the loaded library (ORDA_ABI_VERSION). */

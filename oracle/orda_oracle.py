@@ -48,7 +48,21 @@ from __future__ import annotations
 
 import numpy as np
 
-__all__ = ["DIVERGENCE_DEFS", "divergence_value_and_grad", "distillation_loss_oracle", "log_softmax", "round_to"]
+__all__ = ["DIVERGENCE_DEFS", "divergence_value_and_grad", "distillation_loss_oracle", "log_softmax", "round_to",
+           "topk_dense_logits"]
+
+
+def topk_dense_logits(indices: np.ndarray, logprobs: np.ndarray, V: int) -> np.ndarray:
+    """A top-k teacher as dense teacher logits: its log-probabilities at its k
+    vocabulary ids, -inf elsewhere.  Softmax of these (over V, at any
+    temperature) is the teacher renormalised over its k ids, zero elsewhere --
+    the distribution a top-k teacher stands for; the precomputed-logits path
+    of the oracle then gives its loss and gradients."""
+    idx = np.asarray(indices, dtype=np.int64)
+    lp = np.asarray(logprobs, dtype=np.float64)
+    out = np.full((idx.shape[0], int(V)), -np.inf)
+    np.put_along_axis(out, idx, lp, axis=1)
+    return out
 
 
 def round_to(x: np.ndarray, dtype: str | None) -> np.ndarray:
@@ -75,7 +89,8 @@ def log_softmax(x: np.ndarray) -> np.ndarray:
 
 def _xlogy_ratio(p: np.ndarray, lp: np.ndarray, lq: np.ndarray) -> np.ndarray:
     """p * (log p - log q) with the 0 * (...) = 0 convention."""
-    return np.where(p > 0, p * (lp - lq), 0.0)
+    with np.errstate(invalid="ignore"):
+        return np.where(p > 0, p * (lp - lq), 0.0)
 
 
 def _logaddexp(a, b):

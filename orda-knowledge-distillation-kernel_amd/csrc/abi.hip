@@ -61,7 +61,7 @@ constexpr int64_t kRsrcBytes = 0x7fffffffll;
 // Largest hidden size (K-major rows of 128 x hidden x 4 bytes stay below 2^31)
 // and largest tokens per chunk (the chunk buffer's rows, 2 x chunk columns).
 constexpr int64_t kMaxHidden = 1ll << 22;
-constexpr int64_t kMaxChunkTokens = 1ll << 21;
+constexpr int64_t kMaxChunkTokens = 1ll << 20;
 
 struct Plan {
   int mode, dtype, eb, kelems;
@@ -80,12 +80,12 @@ struct Plan {
   int64_t NP, ldT, ldh, Vc, nchunks;
   size_t off_hT, off_htT, off_dLT, off_dLNs, off_dLNt, off_WT, off_WtT, off_g32s, off_g32t, bwd_bytes;
   // gradients inside forward (materialised token chunks)
-  bool fused, store_t, f_tl, f_tmem;
+  bool fused, store_t, f_tl, f_tmem, f_sring, topk;
   int tclass, table_entry, chunk_scale, scan_groups;
   int64_t fn, fnP, fldL, fnchunks;
   int f_nvr, f_tpr, splits_s, splits_t;
   int64_t kps_s, kps_t;
-  size_t off_L, off_fpart, off_flabelx, off_frowp, off_frowv, off_split, off_fhT, off_fhtT;
+  size_t off_L, off_fpart, off_flabelx, off_frowp, off_frowv, off_split, off_fhT, off_fhtT, off_corr, off_lse;
   int64_t fldh;
 };
 
@@ -103,7 +103,7 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
   if (p->abi_version != ORDA_ABI_VERSION)
     return fail(ORDA_EINVAL, "abi_version %d does not match library version %d", p->abi_version,
                 ORDA_ABI_VERSION);
-  if (p->mode < ORDA_MODE_TIED || p->mode > ORDA_MODE_PRECOMPUTED_HIDDEN)
+  if (p->mode < ORDA_MODE_TIED || p->mode > ORDA_MODE_TOPK)
     return fail(ORDA_EINVAL, "unknown mode %d", p->mode);
   if (p->dtype < ORDA_BF16 || p->dtype > ORDA_F32) return fail(ORDA_EINVAL, "unknown dtype %d", p->dtype);
   if (p->n_rows <= 0 || p->vocab <= 0 || p->hidden <= 0)
@@ -133,7 +133,19 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
   pl.teacher_ce = (p->flags & ORDA_COMPUTE_TEACHER_CE) != 0;
   pl.t1 = p->temperature == 1.0f;
   const bool need_teacher = pl.div_on || pl.teacher_ce;
-  if (!need_teacher) pl.tsrc = TSRC_NONE;
+  pl.topk = p->mode == ORDA_MODE_TOPK;
+  if (pl.topk) {
+    // the scan sees the student alone; k_topk_rows forms the divergence
+    if (p->topk < 1 || p->topk > p->vocab)
+      return fail(ORDA_EINVAL, "topk must be in [1, vocab], got %lld", (long long)p->topk);
+    if (pl.teacher_ce) return fail(ORDA_EINVAL, "a top-k teacher has no teacher CE (teacher_ce_weight must be 0)");
+    if (pl.div_on && p->divergence != ORDA_DIV_FORWARD_KL && p->divergence != ORDA_DIV_SOFT_TARGET_CE)
+      return fail(ORDA_EUNSUPPORTED, "a top-k teacher supports forward KL and soft-target CE, got divergence %d",
+                  p->divergence);
+    if (!(p->flags & ORDA_GRADS_IN_FORWARD))
+      return fail(ORDA_EINVAL, "a top-k teacher runs the gradients-in-forward schedule (ORDA_GRADS_IN_FORWARD)");
+  }
+  if (!need_teacher || pl.topk) pl.tsrc = TSRC_NONE;
   else if (p->mode == ORDA_MODE_TIED) pl.tsrc = TSRC_SHARED;
   else if (p->mode == ORDA_MODE_PRECOMPUTED_LOGITS) pl.tsrc = TSRC_MEM;
   else pl.tsrc = TSRC_SEP;
@@ -265,6 +277,9 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // then runs half as many read-modify-write passes with twice the K).
     pl.f_tmem = pl.eb == 2 && pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype && pl.V % 8 == 0;
     pl.store_t = pl.tsrc != TSRC_NONE && !pl.f_tmem;
+    // no teacher on the scan (student CE only, or a top-k teacher): the ring
+    // engine's student-only tiles, 256 tokens per workgroup (16-bit, K > 64)
+    pl.f_sring = pl.eb == 2 && pl.H > 64 && pl.tsrc == TSRC_NONE;
     const int64_t ncol = pl.store_t ? 2 : 1;
     const int64_t Nr = round_up(pl.N, 8);
     // launch geometry: the gfx950 table for measured shapes, else the rule
@@ -289,7 +304,7 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.fnP = round_up(n, 8);
     pl.fldL = ncol * pl.fnP;
     pl.fnchunks = cdiv(pl.N, n);
-    const int64_t ntt = cdiv(n, pl.f_tl ? 256 : 128);
+    const int64_t ntt = cdiv(n, (pl.f_tl || pl.f_sring) ? 256 : 128);
     int64_t nvr = cdiv(pl.scan_groups, ntt);
     if (nvr < 1) nvr = 1;
     if (nvr > pl.n_vtiles) nvr = pl.n_vtiles;
@@ -355,6 +370,8 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.fldh = (tied && pl.w_dlt_t) ? 2 * pl.fnP : pl.fnP;
     pl.off_fhT = pl.need_gw ? carve(fo, (size_t)pl.H * pl.fldh * pl.eb) : 0;
     pl.off_fhtT = (sep && pl.need_gwt && pl.w_dlt_t) ? carve(fo, (size_t)pl.Ht * pl.fnP * pl.eb) : 0;
+    pl.off_corr = pl.topk ? carve(fo, (size_t)pl.fnP * p->topk * 4) : 0;
+    pl.off_lse = pl.topk ? carve(fo, (size_t)pl.fnP * 4) : 0;
     pl.fwd_bytes = fo + kAlign;
     pl.bwd_bytes = 0;
   }
@@ -694,7 +711,8 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     F.labels = t->labels + r0;
     F.N = nc; F.V = V; F.H = H; F.Ht = Ht; F.ignore_index = p->ignore_index;
     F.tsrc = pl.tsrc; F.lt_dtype = p->logits_dtype;
-    F.div = pl.div; F.fam = pl.fam; F.t_is_one = pl.t1; F.tgrad = 0;
+    // (a top-k teacher's scan and merge see the student alone: no family)
+    F.div = pl.div; F.fam = pl.topk ? FAM_NONE : pl.fam; F.t_is_one = pl.t1; F.tgrad = 0;
     F.temperature = p->temperature; F.invT = 1.0f / p->temperature;
     F.alpha = p->div_alpha; F.beta = p->div_beta;
     F.log_alpha = std::log(p->div_alpha); F.log_1m_alpha = std::log1p(-p->div_alpha);
@@ -705,6 +723,8 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     F.tiles_per_range = pl.f_tpr; F.n_vtiles = pl.n_vtiles;
     F.partial = part; F.rowp = rowp;
     F.Lout = L; F.ldL = ldL; F.tcolL = nP; F.store_t = pl.store_t;
+    F.student_ring = pl.f_sring ? 1 : 0;
+    if (pl.f_sring) F.n_ttiles = (int)cdiv(nc, 256);
     // teacher logits from memory are no GEMM
     bool tgemm = pl.tsrc == TSRC_SHARED || pl.tsrc == TSRC_SEP;
     if (pl.f_tl) {
@@ -731,8 +751,9 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
 
     MergeParams M{};
     M.partial = part; M.n_vranges = pl.f_nvr; M.N = nc; M.V = V; M.ignore_index = p->ignore_index;
-    M.labels = t->labels + r0; M.label_x = labelx; M.phase = 0; M.fam = pl.fam; M.div = pl.div;
-    M.t_is_one = pl.t1; M.has_t = pl.tsrc != TSRC_NONE; M.teacher_ce = pl.teacher_ce; M.div_on = pl.div_on;
+    M.labels = t->labels + r0; M.label_x = labelx; M.phase = 0; M.fam = F.fam; M.div = pl.div;
+    M.t_is_one = pl.t1; M.has_t = pl.tsrc != TSRC_NONE; M.teacher_ce = pl.teacher_ce;
+    M.div_on = pl.div_on && !pl.topk;  // a top-k teacher's divergence rows come from k_topk_rows
     M.invT = F.invT; M.temperature = p->temperature; M.alpha = p->div_alpha; M.beta = p->div_beta;
     for (int i = 0; i < 3; ++i) { M.pa[i] = pl.pa[i]; M.pb[i] = pl.pb[i]; }
     M.npow = pl.npow; M.rowp = rowp; M.rowv = rowv + r0; M.ldv = N;
@@ -741,7 +762,20 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     const int round_code = std::is_same<T, bf16>::value ? 1 : std::is_same<T, f16>::value ? 2 : 0;
     M.round_s = round_code;
     M.round_t = tgemm ? round_code : 0;
+    M.lse_sT_out = pl.topk ? reinterpret_cast<float*>(ws + pl.off_lse) : nullptr;
     { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
+    M.lse_sT_out = nullptr;
+    TopKParams K{};
+    if (pl.topk && pl.div_on) {
+      // the teacher's k ids: divergence rows and the ids' dlogits share
+      K.hs = hs + r0 * H; K.W = W; K.idx = t->teacher_topk_indices + r0 * p->topk;
+      K.lp = t->teacher_topk_logprobs + r0 * p->topk; K.labels = t->labels + r0; K.mean_scale = scal;
+      K.lse_sT = reinterpret_cast<const float*>(ws + pl.off_lse); K.rowp = rowp; K.rowv = rowv + r0; K.ldv = N; K.corr = reinterpret_cast<float*>(ws + pl.off_corr);
+      K.L = L; K.ldL = ldL; K.N = nc; K.V = V; K.H = H; K.k = p->topk; K.ignore_index = p->ignore_index;
+      K.div = pl.div_on ? pl.div : DIV_FKL; K.invT = F.invT; K.temperature = p->temperature;
+      K.w_kl = pl.div_on ? p->kl_weight : 0.f;
+      { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_topk_rows<T>(K, s)); }
+    }
     if (pl.two_pass) {
       // the two-pass divergences' row sums over the stored logits, then the
       // merge of their partial states into D and the dlogits row constants
@@ -769,7 +803,9 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     D.ldtm = V;
     D.invT = F.invT; D.temperature = p->temperature; D.alpha = p->div_alpha; D.beta = p->div_beta;
     D.w_s = p->student_ce_weight; D.w_t = p->teacher_ce_weight; D.w_kl = pl.div_on ? p->kl_weight : 0.f;
+    D.no_t = pl.topk ? 1 : 0;
     { Timed tm_(ORDA_K_DLOGITS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_dlm<T>(D, s)); }
+    if (pl.topk && pl.div_on) { Timed tm_(ORDA_K_DLOGITS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_topk_scatter<T>(K, s)); }
 
     // token columns [nc, nP) of L are read by the grad-W GEMM (K = tokens):
     // keep them zero (the matching hidden rows read as zero too)
@@ -872,6 +908,8 @@ int check_operands(const Plan& pl, const orda_tensors_t* t) {
     return fail(ORDA_EINVAL, "teacher_hidden must be 16-byte aligned");
   if (pl.tsrc == TSRC_SEP && !aligned16(t->teacher_weight)) return fail(ORDA_EINVAL, "teacher_weight must be 16-byte aligned");
   if (pl.tsrc == TSRC_MEM && !t->teacher_logits) return fail(ORDA_EINVAL, "teacher_logits are required");
+  if (pl.topk && (!t->teacher_topk_indices || !t->teacher_topk_logprobs))
+    return fail(ORDA_EINVAL, "teacher_topk_indices and teacher_topk_logprobs are required");
   if (!t->saved) return fail(ORDA_EINVAL, "saved buffer is required");
   return ORDA_OK;
 }
@@ -972,16 +1010,16 @@ int orda_plan_info(const orda_problem_t* p, orda_plan_info_t* out) {
   out->forward_workspace_bytes = pl.fwd_bytes;
   out->backward_workspace_bytes = pl.bwd_bytes;
   if (pl.fused) {
-    // the ring scan runs 16-bit tied teachers (two tokens per lane) and
-    // teacher logits from memory of the non-power families (four tokens per
-    // lane); the rest the two-stage engine
-    const bool ring = pl.tclass == TC_TIED || pl.f_tl;
+    // the ring scan runs 16-bit tied teachers (two tokens per lane), teacher
+    // logits from memory of the non-power families and 16-bit scans with no
+    // teacher (four tokens per lane); the rest the two-stage engine
+    const bool ring = pl.tclass == TC_TIED || pl.f_tl || pl.f_sring;
     out->scan_engine = ring ? 1 : 0;
     out->token_chunk = pl.fn;
     out->n_token_chunks = pl.fnchunks;
     out->chunk_scale = pl.chunk_scale;
-    out->scan_tokens_per_tile = pl.f_tl ? 256 : 128;
-    out->scan_workgroups = (int)(cdiv(pl.fn, pl.f_tl ? 256 : 128) * pl.f_nvr);
+    out->scan_tokens_per_tile = (pl.f_tl || pl.f_sring) ? 256 : 128;
+    out->scan_workgroups = (int)(cdiv(pl.fn, out->scan_tokens_per_tile) * pl.f_nvr);
     out->grad_hidden_splits = pl.splits_s;
     out->grad_teacher_hidden_splits = pl.splits_t;
     out->vocab_rows_per_split = pl.kps_s;

@@ -314,8 +314,11 @@ enum ScanVariant {
   SV_JSD = 6,       // phase 1 (second pass) of the two-pass divergences
   SV_SKEW_F = 7,
   SV_SKEW_R = 8,
-  SV_TVD = 9
+  SV_TVD = 9,
+  SV_STUDENT_T = 10  // no teacher term, the student also at T != 1 (top-k teachers)
 };
+// Second-pass variants (row sums given the first pass's normalisers).
+constexpr bool sv_phase1(int sv) { return sv >= SV_JSD && sv <= SV_TVD; }
 
 template <int SV, class AP>
 __device__ __forceinline__ void scan_variant(RowState& S, const AP& acc, int vlane0, int64_t vlimit,
@@ -323,6 +326,9 @@ __device__ __forceinline__ void scan_variant(RowState& S, const AP& acc, int vla
   if constexpr (SV == SV_STUDENT) {
     if (full) scan_tile<false, FAM_NONE, true, false>(S, acc, vlane0, vlimit, P);
     else scan_tile<false, FAM_NONE, true, true>(S, acc, vlane0, vlimit, P);
+  } else if constexpr (SV == SV_STUDENT_T) {
+    if (full) scan_tile<false, FAM_NONE, false, false>(S, acc, vlane0, vlimit, P);
+    else scan_tile<false, FAM_NONE, false, true>(S, acc, vlane0, vlimit, P);
   } else if constexpr (SV == SV_TCE_T1) {
     if (full) scan_tile<true, FAM_NONE, true, false>(S, acc, vlane0, vlimit, P);
     else scan_tile<true, FAM_NONE, true, true>(S, acc, vlane0, vlimit, P);
@@ -388,7 +394,7 @@ template <class T, int SV, bool STORE = false>
 __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   f32x16 acc[4][2];
-  constexpr bool kPhase1 = SV >= SV_JSD;
+  constexpr bool kPhase1 = sv_phase1(SV);
   const int lane = threadIdx.x & 63;
   const int wm = wave_m(), wn = wave_n();
   int tt, vr;
@@ -464,6 +470,49 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
   const int wm = w4_m(), wn = w4_n();
   const int q = lane & 3;
   T* L = static_cast<T*>(P.Lout);
+  constexpr int kTok = TL ? 256 : 128;
+  // the quad's packed transposed row (4 tokens) of block (mb, nb), group g
+  auto quad_row = [&](int mb, int nb, int g) __attribute__((always_inline)) {
+    uint32_t x[2], o[2];
+    x[0] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 0), acc_get(acc[mb][nb], g * 4 + 1));
+    x[1] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 2), acc_get(acc[mb][nb], g * 4 + 3));
+    quad_transpose16(x, o);
+    return make_uint2(o[0], o[1]);
+  };
+  if (t0 + kTok <= P.N) {
+    // Every token of the block is valid: stores through a buffer resource
+    // over the tile's rows of L, whose range check drops the rows past V,
+    // with 32-bit offsets -- no per-store address arithmetic or guard.
+    typedef unsigned int u2v __attribute__((ext_vector_type(2)));
+    const int64_t ldb = P.ldL * (int64_t)sizeof(T);
+    const int64_t rows = min<int64_t>(P.V - v0, 256);
+    // (v0, t0 are wave-uniform, which the compiler cannot always see: read
+    // the base and size through readfirstlane so the resource is scalar)
+    const uint64_t base = reinterpret_cast<uint64_t>(L + v0 * P.ldL + t0);
+    const uint64_t ubase = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(base >> 32)) << 32) |
+                           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+    const int nbytes = __builtin_amdgcn_readfirstlane((int)(rows * ldb));
+    const __amdgpu_buffer_rsrc_t rs = rsrc_bytes(reinterpret_cast<const void*>(ubase), nbytes);
+    const uint32_t lane_off = (uint32_t)(wm * 128 + (lane >> 5) * 4 + q) * (uint32_t)ldb +
+                              (uint32_t)(wn * 64 + (lane & 31) - q) * (uint32_t)sizeof(T);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      if (!TL && nb >= 2 && !P.store_t) break;
+      const int64_t tok = TL ? (nb >> 1) * 128 + (nb & 1) * 32 : (nb & 1) * 32 + (nb >= 2 ? P.tcolL : 0);
+      const uint32_t nb_off = lane_off + (uint32_t)(tok * (int64_t)sizeof(T));
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint2 o = quad_row(mb, nb, g);
+          const u2v d = {o.x, o.y};
+          __builtin_amdgcn_raw_buffer_store_b64(d, rs, (int)(nb_off + (uint32_t)(mb * 32 + g * 8) * (uint32_t)ldb), 0,
+                                                0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) {
     if (!TL && nb >= 2 && !P.store_t) break;
@@ -475,11 +524,8 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int64_t v = v0 + wm * 128 + acc_row(mb, g * 4, lane) + q;
-        uint32_t x[2], o[2];
-        x[0] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 0), acc_get(acc[mb][nb], g * 4 + 1));
-        x[1] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 2), acc_get(acc[mb][nb], g * 4 + 3));
-        quad_transpose16(x, o);
-        if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + col) = make_uint2(o[0], o[1]);
+        const uint2 o = quad_row(mb, nb, g);
+        if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + col) = o;
         __builtin_amdgcn_sched_barrier(0);
       }
   }
@@ -497,7 +543,7 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 //    then writes them to Lout's teacher columns for the dlogits pass.
 // Rows past V and tokens past N read as 0 (the scan masks rows past V;
 // tokens past N are never merged).
-enum { TL_NONE = 0, TL_FROM_L = 1, TL_FROM_MEM = 2 };
+enum { TL_NONE = 0, TL_FROM_L = 1, TL_FROM_MEM = 2, TL_STUDENT = 3 };
 
 template <class T>
 __device__ __forceinline__ void unpack_raw4(uint2 r, float (&x)[4]) {
@@ -573,6 +619,12 @@ __device__ __forceinline__ void store_teacher4(const f32x16 (&tv)[4], const Fuse
     if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + P.tcolL + tb) = make_uint2(o[0], o[1]);
   }
 }
+struct AccPairS {  // student only: accumulator block nb (the teacher accessor is never used)
+  const Acc4& a;
+  int nb;
+  __device__ __forceinline__ float s(int mb, int r) const { return acc_get(a[mb][nb], r); }
+  __device__ __forceinline__ float t(int, int) const { return 0.f; }
+};
 struct AccPairTL {  // student from accumulator block nb, teacher from registers
   const Acc4& a;
   int nb;
@@ -593,13 +645,14 @@ struct AccPairTL {  // student from accumulator block nb, teacher from registers
 //    each lane holds four tokens (blocks 0..3).
 template <class T, int SV, bool STORE, int TL>
 __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
-  static_assert(TL == TL_NONE || (SV < SV_JSD && STORE), "teacher logits from memory: one-pass, stored");
+  static_assert(TL == TL_NONE || (!sv_phase1(SV) && STORE), "teacher logits from memory: one-pass, stored");
+  static_assert(TL != TL_STUDENT || SV == SV_STUDENT || SV == SV_STUDENT_T, "student-only tiles: no teacher");
   constexpr int NJ = TL ? 4 : 2;        // tokens per lane
   constexpr int kTok = TL ? 256 : 128;  // tokens per workgroup
   __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
   Acc4 acc;
   zero_acc4(acc);
-  constexpr bool kPhase1 = SV >= SV_JSD;
+  constexpr bool kPhase1 = sv_phase1(SV);
   const int lane = threadIdx.x & 63;
   const int wm = w4_m(), wn = w4_n();
   int tt, vr;
@@ -640,7 +693,13 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   auto epilogue = [&](int, const TI& x, Acc4& c) __attribute__((always_inline)) {
     const int vlane0 = wm * 128 + (opaque_lane() >> 5) * 4;
     const int64_t vlimit = P.V - x.v0;
-    if constexpr (TL != TL_NONE) {
+    if constexpr (TL == TL_STUDENT) {
+      store_logits4<T, true>(c, P, x.v0, t0);
+      static_for<0, NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        scan_variant<SV>(st[j], AccPairS{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+      });
+    } else if constexpr (TL != TL_NONE) {
       uint2 raw[2][16];
       issue_teacher4<T, TL>(raw[0], P, x.v0, t0, 0);
       store_logits4<T, true>(c, P, x.v0, t0);
@@ -1565,7 +1624,7 @@ struct DlmQuad {
 // student columns [0, N), teacher columns [tcol, tcol + N)): the dlogits of
 // DlmQuad.  Thread: 4 consecutive tokens x rows_per_block vocabulary rows;
 // block: 256 threads = 1024 tokens.
-template <class T, int DIV, bool T1>
+template <class T, int DIV, bool T1, bool NO_T = false>
 __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
   const int64_t t0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (t0 >= P.N) return;
@@ -1576,7 +1635,9 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
   q.init(P, t0, nt);
   T* Ls = static_cast<T*>(P.L) + t0;
   T* Lt = Ls + P.tcol;
-  const bool need_t = DIV >= 0 || P.tgrad;
+  // (a compile-time no-teacher variant: a run-time flag here splits the
+  // interior loop's batched loads)
+  const bool need_t = !NO_T && (DIV >= 0 || P.tgrad);
   int64_t v = v0;
   if (nt == 4) {
     // interior: R rows per iteration, every load issued before any use
@@ -1761,7 +1822,7 @@ inline int scan_variant_of(const FusedParams& P) {
       default: return SV_TVD;
     }
   }
-  if (P.tsrc == TSRC_NONE) return SV_STUDENT;
+  if (P.tsrc == TSRC_NONE) return P.t_is_one ? SV_STUDENT : SV_STUDENT_T;
   if (P.fam == FAM_LIN) return P.t_is_one ? SV_LIN_T1 : SV_LIN;
   if (P.fam == FAM_POW) return SV_POW;
   return P.t_is_one ? SV_TCE_T1 : SV_TCE;
@@ -1795,6 +1856,7 @@ inline bool scan_on_ring(const FusedParams& P) {
   template <> hipError_t launch_scan<T>(const FusedParams& P, int grid, hipStream_t s) { \
     switch (scan_variant_of(P)) {                                                    \
       ORDA_SCAN_CASE(T, SV_STUDENT)                                                  \
+      ORDA_SCAN_CASE(T, SV_STUDENT_T)                                                \
       ORDA_SCAN_CASE(T, SV_TCE_T1)                                                   \
       ORDA_SCAN_CASE(T, SV_TCE)                                                      \
       ORDA_SCAN_CASE(T, SV_LIN_T1)                                                   \
@@ -1862,12 +1924,103 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------- top-k teachers
+// Sum over the 64 lanes of a wave, in every lane.
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// Per token of the chunk (one wave each): the student's logit at each of the
+// teacher's k ids as an fp32 dot product (the wave cooperating on each), the
+// teacher renormalised over its ids at temperature T (online max / sum of
+// lp / T), the divergence row D (forward KL: sum p_t (log p_t - log p_s^T);
+// soft-target CE: -sum p_t log p_s^T) times T^2, and the ids' share of the
+// student's dlogits, -mean_scale w_kl T p_t (scattered after the dense pass).
+// Ids outside [0, V) are clamped to stay in bounds (the caller's contract is
+// distinct ids in range); ids of log-probability -inf add nothing.  Sets the row's teacher log-normaliser to +inf so
+// the dense pass sees a zero teacher.
+template <class T>
+__global__ __launch_bounds__(256) void k_topk_rows(TopKParams P) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= P.N) return;  // whole waves
+  const int64_t y = P.labels[t];
+  const bool ignored = y == P.ignore_index;
+  const float invT = P.invT;
+  const float lse_sT = P.lse_sT[t];
+  const T* hs = static_cast<const T*>(P.hs) + t * P.H;
+  const T* W = static_cast<const T*>(P.W);
+  const int64_t* idx = P.idx + t * P.k;
+  const float* lp = P.lp + t * P.k;
+  float m = -kInf, sum = 0.f, a = 0.f;
+  for (int64_t c0 = 0; c0 < P.k; c0 += 64) {
+    const int cnt = (int)min<int64_t>(64, P.k - c0);
+    float mine = 0.f;
+    for (int j = 0; j < cnt; ++j) {
+      int64_t v = idx[c0 + j];
+      v = (v >= 0 && v < P.V) ? v : 0;
+      const float d = wave_sum(row_dot<T>(hs, W + v * P.H, P.H, lane));
+      mine = lane == j ? d : mine;
+    }
+    const float z = lane < cnt ? lp[c0 + lane] * invT : -kInf;
+    if (z > -kInf) {  // (an id of probability 0 adds nothing)
+      const float nm = fmaxf(m, z);
+      const float sc = m == -kInf ? 0.f : fexp(m - nm);
+      const float e = fexp(z - nm);
+      sum = sum * sc + e;
+      a = a * sc + e * (P.div == DIV_FKL ? z - mine * invT : mine * invT);
+      m = nm;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float m2 = __shfl_xor(m, off), s2 = __shfl_xor(sum, off), a2 = __shfl_xor(a, off);
+    const float nm = fmaxf(m, m2);
+    const float c1 = m == -kInf ? 0.f : fexp(m - nm), c2 = m2 == -kInf ? 0.f : fexp(m2 - nm);
+    sum = sum * c1 + s2 * c2;
+    a = a * c1 + a2 * c2;
+    m = nm;
+  }
+  const float lse_p = m + flog(sum);
+  const float D = P.div == DIV_FKL ? a / sum - lse_p + lse_sT : lse_sT - a / sum;
+  if (lane == 0) {
+    P.rowv[2 * P.ldv + t] = ignored ? 0.f : P.temperature * P.temperature * D;
+    P.rowp[3 * P.N + t] = kInf;
+  }
+  const float sc = ignored ? 0.f : -P.mean_scale[0] * P.w_kl * P.temperature;
+  float* corr = P.corr + t * P.k;
+  for (int64_t i = lane; i < P.k; i += 64) corr[i] = sc * fexp(lp[i] * invT - lse_p);
+}
+
+// L[id][t] += corr[t][i] for every token t of the chunk and each of its k ids
+// (the chunk's dlogits, in T; distinct ids per token, so no two threads
+// touch one element).
+template <class T>
+__global__ __launch_bounds__(256) void k_topk_scatter(TopKParams P) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= P.N * P.k) return;
+  const int64_t t = g / P.k;
+  int64_t v = P.idx[g];
+  v = (v >= 0 && v < P.V) ? v : 0;
+  T* e = static_cast<T*>(P.L) + v * P.ldL + t;
+  *e = from_f32<T>(to_f32(*e) + P.corr[g]);
+}
+
 // Materialised path: scan variants with the logits store (phase 0 only).
 #define ORDA_SCANST_CASE(T, SV)                                                                  \
   case SV:                                                                                       \
     if constexpr (sizeof(T) == 2) {                                                              \
+      if (P.tsrc == TSRC_NONE && P.student_ring) {                                               \
+        if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T)                                    \
+          hipLaunchKernelGGL((k_scan4<T, SV, true, TL_STUDENT>), dim3(grid), dim3(kThreads4), 0, s, P); \
+        else                                                                                     \
+          return hipErrorInvalidValue;                                                           \
+        break;                                                                                   \
+      }                                                                                          \
       if (P.tsrc == TSRC_L || P.tsrc == TSRC_MEM_RING) {                                         \
-        if constexpr (SV == SV_STUDENT || SV == SV_POW)                                          \
+        if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T || SV == SV_POW)                    \
           return hipErrorInvalidValue;                                                           \
         else if (P.tsrc == TSRC_L)                                                               \
           hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_L>), dim3(grid), dim3(kThreads4), 0, s, P); \
@@ -1890,6 +2043,7 @@ hipError_t launch_label(const LabelParams& P, hipStream_t s) {
     if (P.tsrc == TSRC_MEM_RING && P.V % 4 != 0) return hipErrorInvalidValue;              \
     switch (scan_variant_of(P)) {                                                          \
       ORDA_SCANST_CASE(T, SV_STUDENT)                                                      \
+      ORDA_SCANST_CASE(T, SV_STUDENT_T)                                                    \
       ORDA_SCANST_CASE(T, SV_TCE_T1)                                                       \
       ORDA_SCANST_CASE(T, SV_TCE)                                                          \
       ORDA_SCANST_CASE(T, SV_LIN_T1)                                                       \
@@ -1959,7 +2113,7 @@ inline void gemm2_go(const GemmParams& P, hipStream_t s) {
   }
 
 // In-place dlogits variants (the divergences of families LIN and POW).
-template <class T, int DIV, bool T1>
+template <class T, int DIV, bool T1, bool NO_T = false>
 inline void dlm_go(const DlmParams& P, hipStream_t s) {
   if (P.Ltm) {
     const int64_t rows = kDlmTmRows * kDlmTmTiles;
@@ -1968,17 +2122,46 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
     return;
   }
   const dim3 grid((unsigned)((P.N + 1023) / 1024), (unsigned)((P.V + P.rows_per_block - 1) / P.rows_per_block));
-  hipLaunchKernelGGL((k_dlm<T, DIV, T1>), grid, dim3(256), 0, s, P);
+  hipLaunchKernelGGL((k_dlm<T, DIV, T1, NO_T>), grid, dim3(256), 0, s, P);
 }
 #define ORDA_DLM_CASE(T, D) \
   case D: dlm_go<T, D, false>(P, s); break;
+// forward KL / soft-target CE: T = 1 specialised, and the no-teacher variant
+// of a top-k teacher (P.no_t; its logits are never read in place)
+#define ORDA_DLM_T1_CASE(T, D)                                   \
+  if (P.no_t && P.Ltm) return hipErrorInvalidValue;              \
+  if (P.no_t) {                                                  \
+    if (t1) dlm_go<T, D, true, true>(P, s);                      \
+    else dlm_go<T, D, false, true>(P, s);                        \
+  } else if (t1) {                                               \
+    dlm_go<T, D, true>(P, s);                                    \
+  } else {                                                       \
+    dlm_go<T, D, false>(P, s);                                   \
+  }
 #define ORDA_INSTANTIATE_FB(T)                                                             \
+  template <> hipError_t launch_topk_rows<T>(const TopKParams& P, hipStream_t s) {         \
+    if (!P.hs || !P.W || !P.idx || !P.lp || !P.labels || !P.mean_scale || !P.lse_sT ||     \
+        !P.rowp || !P.rowv || !P.corr || P.k < 1)                                          \
+      return hipErrorInvalidValue;                                                         \
+    if (P.N <= 0) return hipSuccess;                                                       \
+    hipLaunchKernelGGL(k_topk_rows<T>, dim3((unsigned)((P.N + 3) / 4)), dim3(256), 0, s, P); \
+    return hipGetLastError();                                                              \
+  }                                                                                        \
+  template <> hipError_t launch_topk_scatter<T>(const TopKParams& P, hipStream_t s) {      \
+    const int64_t n = P.N * P.k;                                                           \
+    if (!P.idx || !P.corr || !P.L) return hipErrorInvalidValue;                            \
+    if (n <= 0) return hipSuccess;                                                         \
+    hipLaunchKernelGGL(k_topk_scatter<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, P); \
+    return hipGetLastError();                                                              \
+  }                                                                                        \
   template <> hipError_t launch_dlm<T>(const DlmParams& P, hipStream_t s) {                \
     const bool t1 = P.t_is_one != 0;                                                       \
+    if (P.no_t && (P.tgrad || (P.div != -1 && P.div != DIV_FKL && P.div != DIV_SOFT)))     \
+      return hipErrorInvalidValue; /* no teacher logits to read */                         \
     switch (P.div) {                                                                       \
       case -1: dlm_go<T, -1, true>(P, s); break;                                           \
-      case DIV_FKL: if (t1) dlm_go<T, DIV_FKL, true>(P, s); else dlm_go<T, DIV_FKL, false>(P, s); break; \
-      case DIV_SOFT: if (t1) dlm_go<T, DIV_SOFT, true>(P, s); else dlm_go<T, DIV_SOFT, false>(P, s); break; \
+      case DIV_FKL: ORDA_DLM_T1_CASE(T, DIV_FKL) break;                                    \
+      case DIV_SOFT: ORDA_DLM_T1_CASE(T, DIV_SOFT) break;                                  \
       ORDA_DLM_CASE(T, DIV_RKL)                                                            \
       ORDA_DLM_CASE(T, DIV_SYM)                                                            \
       ORDA_DLM_CASE(T, DIV_HELL)                                                           \

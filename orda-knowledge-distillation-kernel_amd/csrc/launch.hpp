@@ -65,6 +65,8 @@ struct FusedParams {
   void* Lout;
   int64_t ldL, tcolL;
   int store_t;
+  // no teacher (TSRC_NONE) on the ring scan: 256 student tokens per workgroup
+  int student_ring;
 };
 
 struct GemmParams {
@@ -97,6 +99,30 @@ struct DlmParams {
   // they are not staged in L's teacher columns; else null
   const void* Ltm;
   int64_t ldtm;
+  // no teacher logits at all (a top-k teacher): the dense teacher term reads
+  // as zero, and its ids' share is scattered in afterwards (k_topk_scatter)
+  int no_t;
+};
+
+// Per-token pass of a top-k teacher (k_topk_rows) and the scatter of its
+// dlogits share (k_topk_scatter).
+struct TopKParams {
+  const void* hs;  // [N x H] student hidden rows of the chunk
+  const void* W;   // [V x H]
+  const int64_t* idx;   // [N x k] vocabulary ids
+  const float* lp;      // [N x k] teacher log-probabilities (T = 1)
+  const int64_t* labels;
+  const float* mean_scale;
+  const float* lse_sT;  // [N] student lse at T (MergeParams.lse_sT_out)
+  float* rowp;          // [kNRowP][N]: row 3 (teacher lse at T) set to +inf
+  float* rowv;          // [3][ldv]: row 2 (the divergence row, x T^2) written
+  int64_t ldv;
+  float* corr;          // [N x k]: the dlogits share at the ids
+  void* L;              // [V][ldL] chunk dlogits (scatter)
+  int64_t ldL;
+  int64_t N, V, H, k, ignore_index;
+  int div;              // DIV_FKL or DIV_SOFT
+  float invT, temperature, w_kl;
 };
 
 // Phase-1 row sums of the two-pass divergences over stored logits (k_two_rows).
@@ -134,6 +160,8 @@ template <class T> hipError_t launch_label(const LabelParams& P, hipStream_t s);
 template <class T> hipError_t launch_scan_store(const FusedParams& P, int grid, hipStream_t s);
 template <class T> hipError_t launch_gemm2(const GemmParams& P, hipStream_t s);
 template <class T> hipError_t launch_dlm(const DlmParams& P, hipStream_t s);
+template <class T> hipError_t launch_topk_rows(const TopKParams& P, hipStream_t s);
+template <class T> hipError_t launch_topk_scatter(const TopKParams& P, hipStream_t s);
 template <class T> hipError_t launch_two(const TwoParams& P, hipStream_t s);
 template <class T>
 hipError_t launch_splitk_reduce(const float* part, int splits, int64_t stride, void* out, int64_t ldo, int64_t M,
@@ -162,6 +190,9 @@ struct MergeParams {
   // 0 none (fp32, recomputed, or teacher logits read back from memory),
   // 1 bf16, 2 fp16
   int round_s, round_t;
+  // when set: the student's log-sum-exp at T per row as the losses use it
+  // (fp32 statistics, no rounding adjustment) -- a top-k teacher's rows
+  float* lse_sT_out;
 };
 hipError_t launch_merge(const MergeParams& P, hipStream_t s);
 

@@ -152,6 +152,7 @@ __global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams 
     g_t += d * exp((double)S.mt - lse_t);
     g_tT = t1 ? g_t : g_tT + d * invT * exp((double)S.mt * invT - lse_tT);
   }
+  if (P.lse_sT_out) P.lse_sT_out[t] = (float)lse_sT;
   P.rowp[0 * N + t] = (float)g_s;
   P.rowp[1 * N + t] = (float)g_sT;
   P.rowp[2 * N + t] = (float)g_t;

@@ -15,11 +15,15 @@ from .api import (
     PrecomputedTeacher,
     SeparateTeacher,
     TiedTeacher,
+    TopKTeacher,
     distillation_loss,
 )
 
 
 from . import compiled  # noqa: E402,F401  (torch.compile-friendly entry; not in __all__)
+
+# TopKTeacher (a top-k precomputed teacher) is importable from here but kept
+# out of __all__, which stays the reference's public surface.
 
 
 def is_available() -> bool:

@@ -20,9 +20,9 @@ __all__ = [
     "MODE", "DTYPE", "FLAG", "KERNEL_CLASSES", "timing_enable", "timing_collect",
 ]
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
-MODE = {"tied": 0, "separate": 1, "precomputed_logits": 2, "precomputed_hidden": 3}
+MODE = {"tied": 0, "separate": 1, "precomputed_logits": 2, "precomputed_hidden": 3, "topk": 4}
 DTYPE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 FLAG = {
     "need_grad_student_hidden": 1 << 0,
@@ -60,6 +60,7 @@ class Problem(ctypes.Structure):
         ("div_beta", ctypes.c_float),
         ("grad_hidden_splits", ctypes.c_int32),
         ("token_chunk", ctypes.c_int64),
+        ("topk", ctypes.c_int64),
     ]
 
 
@@ -109,6 +110,7 @@ class Tensors(ctypes.Structure):
             "student_hidden", "weight", "teacher_hidden", "teacher_weight", "teacher_logits", "labels",
             "out_loss", "out_student_ce", "out_teacher_ce", "out_kl", "saved", "grad_output",
             "grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight",
+            "teacher_topk_indices", "teacher_topk_logprobs",
         )
     ]
 

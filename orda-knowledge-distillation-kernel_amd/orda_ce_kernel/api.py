@@ -15,6 +15,10 @@ the unfused formulation explicitly.
 
 ``divergence=`` (new, default ``"forward_kl"``) selects the distillation
 term; see :mod:`orda_ce_kernel.divergences`.
+
+``TopKTeacher`` (new, no counterpart in the reference) is a precomputed
+teacher kept as its k most likely ids and their log-probabilities per token;
+see :mod:`orda_ce_kernel.ops.topk_teacher`.
 """
 from __future__ import annotations
 
@@ -36,7 +40,7 @@ Backend = Literal["auto", "triton", "hip", "torch"]
 
 __all__ = [
     "DistillationLoss", "DistillationLossOutput", "KernelConfig", "PrecomputedTeacher", "SeparateTeacher",
-    "TiedTeacher", "distillation_loss",
+    "TiedTeacher", "TopKTeacher", "distillation_loss",
 ]
 
 
@@ -73,6 +77,21 @@ class PrecomputedTeacher:
             raise ValueError("PrecomputedTeacher: must provide logits or (teacher_hidden, teacher_weight)")
         if with_pair and (self.teacher_hidden is None or self.teacher_weight is None):
             raise ValueError("PrecomputedTeacher: teacher_hidden and teacher_weight must both be provided")
+
+
+@dataclass(frozen=True)
+class TopKTeacher:
+    """A precomputed teacher as its top-k (id, log-probability) pairs per
+    token: ``indices`` ``[BT, k]`` integer ids, distinct per row, in
+    ``[0, V)``; ``logprobs`` ``[BT, k]`` the teacher's log-probabilities at
+    those ids (temperature 1).  The distribution it stands for is the teacher
+    renormalised over its ids: ``softmax(logprobs / T)`` there, zero
+    elsewhere.  Divergences: ``forward_kl`` and ``soft_target_ce``; no
+    teacher CE.  Not in the reference, whose precomputed teacher is full
+    ``[BT, V]`` logits (``PrecomputedTeacher``)."""
+
+    indices: torch.Tensor
+    logprobs: torch.Tensor
 
 
 # ── Config and output types (reference api.py:56-76) ────────────────────────
@@ -273,6 +292,73 @@ def _torch_reference(*, student_hidden, weight, labels, teacher, student_ce_weig
     return DistillationLossOutput(loss, student_ce.detach(), teacher_ce.detach(), kl.detach())
 
 
+def _torch_topk_reference(*, student_hidden, weight, labels, teacher: TopKTeacher, student_ce_weight, kl_weight,
+                          kl_temperature, ignore_index, reduction, divergence: Divergence):
+    """The top-k teacher's loss, unfused (CPU tensors, ``backend="torch"``):
+    student CE plus ``T^2 D(p_t || p_s)`` with ``p_t = softmax(logprobs / T)``
+    on the ids and zero elsewhere -- forward KL ``sum p_t (log p_t - log
+    p_s^T)`` or soft-target CE ``-sum p_t log p_s^T`` over the ids."""
+    logits_s = student_hidden @ weight.t()
+    ce_s_rows = F.cross_entropy(logits_s, labels, ignore_index=ignore_index, reduction="none")
+    keep = labels != ignore_index
+    denom = keep.sum().clamp(min=1)
+    T = float(kl_temperature)
+    log_p_s = F.log_softmax(logits_s / T, dim=-1)
+    lps_k = log_p_s.gather(1, teacher.indices.long())
+    p_t = F.softmax(teacher.logprobs.detach().to(lps_k.dtype) / T, dim=-1)
+    cross = -(p_t * lps_k).sum(-1)
+    d = cross + torch.xlogy(p_t, p_t).sum(-1) if divergence.name == "forward_kl" else cross
+    d_rows = (d * (T * T)).masked_fill(~keep, 0.0)
+    if reduction == "mean":
+        student_ce, kl = ce_s_rows.sum() / denom, d_rows.sum() / denom
+    else:
+        student_ce, kl = ce_s_rows.sum(), d_rows.sum()
+    loss = student_ce_weight * student_ce + kl_weight * kl
+    return DistillationLossOutput(loss, student_ce.detach(), student_ce.new_zeros(()), kl.detach())
+
+
+def _topk_loss(*, student_hidden, weight, labels, teacher: TopKTeacher, teacher_ce_weight, student_ce_weight,
+               kl_weight, kl_temperature, ignore_index, reduction, profile, backend, resolved: KernelConfig,
+               divergence: Divergence) -> DistillationLossOutput:
+    from .ops.topk_teacher import check_topk_teacher, topk_distillation_loss
+
+    if teacher_ce_weight not in (None, 0.0):
+        raise ValueError("a TopKTeacher has no teacher CE: teacher_ce_weight must be None or 0.0")
+    BT, V = student_hidden.shape[0], weight.shape[0]
+    check_topk_teacher(teacher.indices, teacher.logprobs, BT, V, divergence)
+    if teacher.indices.device != student_hidden.device or teacher.logprobs.device != student_hidden.device:
+        raise ValueError("TopKTeacher tensors must be on the student's device")
+    if profile == "debug":
+        idx = teacher.indices.long()
+        if bool(((idx < 0) | (idx >= V)).any()):
+            raise ValueError(f"TopKTeacher.indices must lie in [0, {V})")
+        srt = idx.sort(dim=1).values
+        if bool((srt[:, 1:] == srt[:, :-1]).any()):
+            raise ValueError("TopKTeacher.indices must be distinct within each row")
+    if backend == "torch" or (backend == "auto" and student_hidden.device.type != "cuda"):
+        return _torch_topk_reference(
+            student_hidden=student_hidden, weight=weight, labels=labels, teacher=teacher,
+            student_ce_weight=student_ce_weight, kl_weight=kl_weight, kl_temperature=kl_temperature,
+            ignore_index=ignore_index, reduction=reduction, divergence=divergence,
+        )
+    if not _supports_native(student_hidden):
+        raise RuntimeError(
+            f"backend={backend!r} on {student_hidden.device} tensors requires the HIP extension liborda_ce.so "
+            f"({native_error() or 'loaded'}); pass backend='torch' to run the unfused PyTorch formulation"
+        )
+    from .utils.resolver import resolve_chunk_size
+
+    cs, _ = resolve_chunk_size(BT, resolved.chunk_size, V=V, max_chunks=resolved.max_chunks,
+                               num_chunks=resolved.num_chunks)
+    out = topk_distillation_loss(
+        student_hidden, weight, teacher.indices, teacher.logprobs, labels, student_ce_weight=student_ce_weight,
+        ignore_index=ignore_index, reduction=reduction, chunk_size=cs, kl_weight=kl_weight,
+        kl_temperature=kl_temperature, max_chunks=resolved.max_chunks, max_fused_size=resolved.max_fused_size,
+        validate_labels=profile == "debug", divergence=divergence,
+    )
+    return DistillationLossOutput(*out)
+
+
 def _supports_native(student_hidden: torch.Tensor) -> bool:
     return bool(HAS_NATIVE and student_hidden.device.type == "cuda")
 
@@ -283,7 +369,7 @@ def distillation_loss(
     student_hidden: torch.Tensor,
     weight: torch.Tensor,
     labels: torch.Tensor,
-    teacher: TiedTeacher | SeparateTeacher | PrecomputedTeacher,
+    teacher: TiedTeacher | SeparateTeacher | PrecomputedTeacher | TopKTeacher,
     *,
     student_ce_weight: float = 1.0,
     teacher_ce_weight: float | None = None,
@@ -311,6 +397,13 @@ def distillation_loss(
         backend=backend, config=resolved,
     )
     div = resolve_divergence(divergence)
+    if isinstance(teacher, TopKTeacher):
+        return _topk_loss(
+            student_hidden=student_hidden, weight=weight, labels=labels, teacher=teacher,
+            teacher_ce_weight=teacher_ce_weight, student_ce_weight=student_ce_weight, kl_weight=kl_w,
+            kl_temperature=kl_t, ignore_index=ignore_index, reduction=reduction, profile=profile, backend=backend,
+            resolved=resolved, divergence=div,
+        )
     mode, t_hidden, t_weight, t_logits = _teacher_mode_and_tensors(teacher)
     _validate_teacher(
         mode=mode, teacher_hidden=t_hidden, teacher_weight=t_weight, teacher_logits=t_logits,

@@ -114,7 +114,7 @@ def _ptr(x: torch.Tensor | None):
 class FusedCall:
     """Everything one fused loss evaluation needs (built by the Functions)."""
 
-    mode: str                         # tied / separate / precomputed_logits / precomputed_hidden
+    mode: str                         # tied / separate / precomputed_logits / precomputed_hidden / topk
     student_hidden: torch.Tensor
     weight: torch.Tensor
     labels: torch.Tensor
@@ -136,6 +136,8 @@ class FusedCall:
     need_grad_teacher_weight: bool = False
     grads_in_forward: bool = False
     token_chunk: int = 0
+    topk_indices: torch.Tensor | None = None   # mode "topk": [N x k] int64
+    topk_logprobs: torch.Tensor | None = None  # mode "topk": [N x k] fp32
 
 
 def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None) -> _native.Problem:
@@ -179,6 +181,7 @@ def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None)
     p.token_chunk = int(call.token_chunk)
     splits = LAUNCH_OVERRIDES.get("grad_hidden_splits")
     p.grad_hidden_splits = int(splits) if splits else 0
+    p.topk = int(call.topk_indices.shape[1]) if call.topk_indices is not None else 0
     return p
 
 
@@ -233,6 +236,17 @@ def run_fused_call(call: FusedCall):
         if lt.data_ptr() % 16 != 0:  # the kernels read 16-byte rows in place
             lt = lt.clone()
     labels = call.labels.contiguous()
+    tk_i = tk_lp = None
+    if call.mode == "topk":
+        # the kernels read N x k int64 ids and fp32 log-probs on this device
+        tk_i = call.topk_indices.contiguous()
+        tk_lp = call.topk_logprobs.contiguous()
+        n = call.student_hidden.shape[0]
+        if (tk_i.dtype != torch.int64 or tk_lp.dtype != torch.float32 or tk_i.ndim != 2 or tk_i.shape[0] != n
+                or tk_lp.shape != tk_i.shape or tk_i.device != dev or tk_lp.device != dev):
+            raise ValueError("top-k teacher: indices must be int64 and logprobs float32, both [N, k] on "
+                             f"{dev}; got {tk_i.dtype} {tuple(tk_i.shape)} on {tk_i.device}, "
+                             f"{tk_lp.dtype} {tuple(tk_lp.shape)} on {tk_lp.device}")
     Hp = hs.shape[1]
     Htp = ht.shape[1] if (ht is not None and call.mode != "tied") else Hp
     problem = _problem(call, Hp, Htp, lt.dtype if lt is not None else None)
@@ -240,18 +254,19 @@ def run_fused_call(call: FusedCall):
     saved = torch.empty(_native.saved_bytes(problem), dtype=torch.uint8, device=dev)
     outs = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(4)]
     grads = _alloc_grads(problem.flags, hs, w, ht, wt) if call.grads_in_forward else (None,) * 4
-    inputs = (hs, w, ht, wt, lt, labels)
+    inputs = (hs, w, ht, wt, lt, labels, tk_i, tk_lp)
     _run_forward(problem, inputs, saved, outs, grads)
     return outs, grads, (problem, (H, Ht), inputs, saved)
 
 
 def _run_forward(problem, inputs, saved, outs, grads) -> None:
     """One orda_forward call with a fresh workspace (freed on return)."""
-    hs, w, ht, wt, lt, labels = inputs
+    hs, w, ht, wt, lt, labels, tk_i, tk_lp = inputs
     ws = torch.empty(_native.forward_workspace_bytes(problem), dtype=torch.uint8, device=hs.device)
     t = _native.Tensors()
     t.student_hidden, t.weight, t.labels = _ptr(hs), _ptr(w), _ptr(labels)
     t.teacher_hidden, t.teacher_weight, t.teacher_logits = _ptr(ht), _ptr(wt), _ptr(lt)
+    t.teacher_topk_indices, t.teacher_topk_logprobs = _ptr(tk_i), _ptr(tk_lp)
     t.out_loss, t.out_student_ce, t.out_teacher_ce, t.out_kl = (o.data_ptr() for o in outs)
     t.saved = saved.data_ptr()
     t.grad_student_hidden, t.grad_weight, t.grad_teacher_hidden, t.grad_teacher_weight = (_ptr(g) for g in grads)
@@ -271,7 +286,7 @@ def _alloc_grads(flags: int, hs, w, ht, wt):
 def fused_backward(ctx, grad_output: torch.Tensor):
     """Gradients ``(d_student_hidden, d_weight, d_teacher_hidden,
     d_teacher_weight)`` in the compute dtype, unpadded; None where not needed."""
-    hs, w, ht, wt, lt, labels, saved = ctx.saved_tensors
+    hs, w, ht, wt, lt, labels, tk_i, tk_lp, saved = ctx.saved_tensors
     problem = ctx.orda_problem
     H, Ht = ctx.orda_shapes
     flags = problem.flags
@@ -281,7 +296,7 @@ def fused_backward(ctx, grad_output: torch.Tensor):
         if grads is None:  # a second backward through a retained graph
             grads = _alloc_grads(flags, hs, w, ht, wt)
             outs = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(4)]
-            _run_forward(problem, (hs, w, ht, wt, lt, labels), torch.empty_like(saved), outs, grads)
+            _run_forward(problem, (hs, w, ht, wt, lt, labels, tk_i, tk_lp), torch.empty_like(saved), outs, grads)
         g_hs, g_w, g_ht, g_wt = grads
     else:
         g_hs, g_w, g_ht, g_wt = _alloc_grads(flags, hs, w, ht, wt)
@@ -291,6 +306,7 @@ def fused_backward(ctx, grad_output: torch.Tensor):
     t = _native.Tensors()
     t.student_hidden, t.weight, t.labels = _ptr(hs), _ptr(w), _ptr(labels)
     t.teacher_hidden, t.teacher_weight, t.teacher_logits = _ptr(ht), _ptr(wt), _ptr(lt)
+    t.teacher_topk_indices, t.teacher_topk_logprobs = _ptr(tk_i), _ptr(tk_lp)
     t.saved = saved.data_ptr()
     t.grad_output = go.data_ptr()
     t.grad_student_hidden, t.grad_weight = _ptr(g_hs), _ptr(g_w)

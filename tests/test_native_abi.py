@@ -26,7 +26,7 @@ def _declared_functions():
 
 def test_library_loads_with_matching_abi():
     lib = _native.library()
-    assert lib.orda_abi_version() == _native.ABI_VERSION == 3
+    assert lib.orda_abi_version() == _native.ABI_VERSION == 4
 
 
 def test_every_declared_function_is_exported():
@@ -55,11 +55,12 @@ int main(void) {
   printf("orda_plan_info_t %zu\n", sizeof(orda_plan_info_t));
   F(orda_problem_t, n_rows) F(orda_problem_t, vocab_chunk) F(orda_problem_t, flags) F(orda_problem_t, divergence)
   F(orda_problem_t, temperature) F(orda_problem_t, div_beta) F(orda_problem_t, grad_hidden_splits)
-  F(orda_problem_t, token_chunk)
+  F(orda_problem_t, token_chunk) F(orda_problem_t, topk)
   F(orda_plan_info_t, token_chunk) F(orda_plan_info_t, grad_hidden_splits) F(orda_plan_info_t, vocab_rows_per_split)
   F(orda_plan_info_t, backward_workspace_bytes)
   F(orda_tensors_t, labels) F(orda_tensors_t, saved) F(orda_tensors_t, grad_output)
-  F(orda_tensors_t, grad_teacher_weight)
+  F(orda_tensors_t, grad_teacher_weight) F(orda_tensors_t, teacher_topk_indices)
+  F(orda_tensors_t, teacher_topk_logprobs)
   F(orda_timing_t, milliseconds) F(orda_timing_t, executed_flops)
   printf("ORDA_DIV_COUNT %d\n", (int)ORDA_DIV_COUNT);
   printf("ORDA_K_COUNT %d\n", (int)ORDA_K_COUNT);
@@ -138,6 +139,41 @@ def test_invalid_problems_are_rejected(field, value, message):
     p = _problem(**{field: value})
     with pytest.raises(ValueError, match=message):
         _native.forward_workspace_bytes(p)
+
+
+_TOPK_FLAGS = 0x3 | 0x20 | 0x80  # both student gradients, divergence, gradients in forward
+
+
+@pytest.mark.parametrize(
+    "kw, message",
+    [
+        (dict(topk=0), "topk must be in"),
+        (dict(topk=128257), "topk must be in"),
+        (dict(flags=_TOPK_FLAGS | 0x10), "no teacher CE"),
+        (dict(flags=_TOPK_FLAGS & ~0x80), "ORDA_GRADS_IN_FORWARD"),
+        (dict(divergence=1), "forward KL and soft-target CE"),
+    ],
+)
+def test_invalid_topk_problems_are_rejected(kw, message):
+    p = _problem(mode=_native.MODE["topk"], flags=_TOPK_FLAGS, topk=64, teacher_ce_weight=0.0)
+    for k, v in kw.items():
+        setattr(p, k, v)
+    with pytest.raises(ValueError, match=message):
+        _native.forward_workspace_bytes(p)
+
+
+def test_topk_plan_runs_the_student_ring_scan():
+    """A top-k teacher's scan sees the student alone: the ring engine with
+    256-token tiles; the workspace holds the ids' dlogits share ([chunk x k]
+    fp32) and a row of log-sum-exps."""
+    p = _problem(mode=_native.MODE["topk"], flags=_TOPK_FLAGS, topk=64, teacher_ce_weight=0.0, token_chunk=512)
+    info = _native.plan_info(p)
+    assert info["grads_in_forward"] == 1 and info["scan_engine"] == 1
+    assert info["scan_tokens_per_tile"] == 256
+    p.topk = 1
+    small = _native.forward_workspace_bytes(p)
+    p.topk = 65
+    assert _native.forward_workspace_bytes(p) - small >= 64 * 4 * info["token_chunk"]
 
 
 def test_divergence_parameters_are_validated_by_the_library():
