@@ -47,7 +47,10 @@ CONFIGS = {
     "c3jsd": ("separate", 8192, 2048, 4096, 128256, "bfloat16", "jsd", 2.0, 1.0, None, 1.0, 0.05),
     "c4": ("precomputed", 8192, 4096, 4096, 128256, "bfloat16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
     "c5": ("tied", 32768, 5120, 5120, 152064, "bfloat16", "forward_kl", 1.0, 0.7, None, 0.3, 0.20),
+    # config 4's teacher as its top-64 (id, log-prob) pairs per token (TopKTeacher)
+    "c4topk": ("topk", 8192, 4096, 4096, 128256, "bfloat16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
 }
+TOPK = 64
 # config 5: teacher rows scaled by c / tau_n, tau_n ~ U[0.5, 4]; c puts the teacher logit spread at
 # ~6.4 standard deviations for tau = 0.5 (entropy of a few nats) and ~0.8 for tau = 4 (near uniform)
 ROW_TEMPERATURE = {"c5": (0.5, 4.0, 6.4 * 0.5 / (0.02 * 5120 ** 0.5))}
@@ -79,12 +82,16 @@ def make_inputs(cfg, device, seed, row_tau=None):
     n_ign = int(round(ignore_frac * N))
     y[torch.randperm(N, generator=g, device=device)[:n_ign]] = -100
     lt = None
-    if mode == "precomputed":
+    if mode in ("precomputed", "topk"):
         # teacher log-probs of N(0, 3) logits, stored bf16 (config 4)
         lt = torch.empty(N, V, dtype=dtype, device=device)
         for s in range(0, N, 1024):
             e = min(N, s + 1024)
             lt[s:e] = torch.log_softmax(3.0 * torch.randn(e - s, V, generator=g, device=device), -1).to(dtype)
+    if mode == "topk":
+        vals, idx = lt.float().topk(TOPK, dim=1)
+        del lt
+        lt = (idx, vals)
     return hs, ht, W, Wt, lt, y
 
 
@@ -103,7 +110,7 @@ def algorithmic_flops(cfg) -> float:
     return 3 * G(H)
 
 
-def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=None):
+def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=None, student_norm=False):
     import torch
 
     import orda_ce_kernel as orda
@@ -123,16 +130,26 @@ def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=N
         teacher = orda.TiedTeacher(ht)
     elif mode == "separate":
         teacher = orda.SeparateTeacher(ht, Wt)
+    elif mode == "topk":
+        teacher = orda.TopKTeacher(*lt)
     else:
         teacher = orda.PrecomputedTeacher(logits=lt)
+    norm = None
+    if student_norm:
+        # the student's final RMSNorm fused in front of the loss (hs is its input)
+        nw = (1.0 + 0.1 * torch.randn(H, generator=torch.Generator(device=device).manual_seed(seed + 7),
+                                      device=device)).to(hs.dtype).requires_grad_(True)
+        norm = orda.StudentRMSNorm(nw)
 
     def step():
         out = orda.distillation_loss(hs, W, y, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t,
                                      kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div,
-                                     config=config)
+                                     config=config, student_norm=norm)
         out.loss.backward()
         hs.grad = None
         W.grad = None
+        if norm is not None:
+            norm.weight.grad = None
         return out
 
     _log(f"[bench] warmup {warmup} step(s)")
@@ -175,7 +192,8 @@ def launch_plan_of(cfg, chunk, splits):
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, _ = cfg
     p = _native.Problem()
     p.abi_version = _native.ABI_VERSION
-    p.mode = {"tied": 0, "separate": 1, "precomputed": 2}[mode]
+    p.mode = {"tied": 0, "separate": 1, "precomputed": 2, "topk": 4}[mode]
+    p.topk = TOPK if mode == "topk" else 0
     p.dtype = p.logits_dtype = {"bfloat16": 0, "float16": 1, "float32": 2}[dtype_name]
     p.n_rows, p.vocab, p.hidden, p.teacher_hidden = N, V, H, Ht
     p.ignore_index = -100
@@ -386,6 +404,8 @@ def main() -> int:
     ap.add_argument("--table-sweep", action="store_true",
                     help="instead of the one-line benchmark, time the launch-table candidates (requested chunk x "
                          "grad-hidden splits) of configs 2-5, one json line each")
+    ap.add_argument("--student-norm", action="store_true",
+                    help="fuse the student's final RMSNorm in front of the loss (StudentRMSNorm)")
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true")
@@ -414,7 +434,8 @@ def main() -> int:
         return table_sweep(args)
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, ignore_frac = cfg
     ms_step, peak_extra, loss_val, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, not args.no_timing,
-                                                 row_tau, chunk=args.chunk, splits=args.splits)
+                                                 row_tau, chunk=args.chunk, splits=args.splits,
+                                                 student_norm=args.student_norm)
     peak = PEAK_FP32_TFLOPS if dtype_name == "float32" else PEAK_BF16_TFLOPS
     alg = algorithmic_flops(cfg)
     step_tflops = alg / (ms_step / 1e3) / 1e12
@@ -435,7 +456,9 @@ def main() -> int:
         "config": {
             "workload": f"{args.config}: {mode} teacher, N={N} tokens, hidden={H}"
                         + (f", teacher hidden={Ht}" if mode != "tied" else "")
-                        + f", vocab={V}, {div}, T={T}, fwd+bwd (grad hidden + grad W)",
+                        + f", vocab={V}, {div}, T={T}, fwd+bwd (grad hidden + grad W)"
+                        + (f", top-{TOPK} teacher" if mode == "topk" else "")
+                        + (", student RMSNorm fused (grad x + grad norm weight)" if args.student_norm else ""),
             "tokens": N, "hidden": H, "vocab": V, "teacher": mode, "divergence": div, "temperature": T,
             "student_ce_weight": w_s, "teacher_ce_weight": w_t, "kl_weight": kl_w, "ignore_frac": ignore_frac,
         },
@@ -471,7 +494,8 @@ def main() -> int:
             es = 4 if dtype_name == "float32" else 2
             w_t_eff = (1.0 if mode == "tied" else 0.0) if w_t is None else w_t
             tgrad = w_t_eff != 0.0
-            passes = 2 + (1 if (kl_w != 0.0 or tgrad) else 0) + (1 if tgrad else 0)
+            # (a top-k teacher has no dense teacher logits to read)
+            passes = 2 + (1 if ((kl_w != 0.0 and mode != "topk") or tgrad) else 0) + (1 if tgrad else 0)
             if kl_w != 0.0 and div in TWO_PASS:
                 passes += 2  # the second pass of the two-pass divergences reads both halves again
             d = kern["dlogits"]

@@ -90,6 +90,17 @@ enum orda_divergence {
  * (the two-pass ones, JSD, skew KLs and TVD, take their second pass over the
  * chunk's stored logits). */
 #define ORDA_GRADS_IN_FORWARD (1u << 7)
+/* The student's final RMSNorm fused in front of the loss (no counterpart in
+ * the reference's loss API; its producer applies the norm before calling the
+ * loss, test/benchmark/src/core.py:7-14,135): student_hidden is the norm's
+ * input x, and the loss is taken on
+ *   y = x * rsqrt(mean_j x_j^2 + norm_eps) * student_norm_weight
+ * (mean over the first norm_dim columns; y rounded to the compute dtype).
+ * grad_student_hidden is then dloss/dx, and with
+ * ORDA_NEED_GRAD_STUDENT_NORM_WEIGHT grad_student_norm_weight is
+ * dloss/dnorm_weight.  Needs ORDA_GRADS_IN_FORWARD. */
+#define ORDA_STUDENT_RMSNORM (1u << 8)
+#define ORDA_NEED_GRAD_STUDENT_NORM_WEIGHT (1u << 9)
 
 /* Error codes. */
 #define ORDA_OK 0
@@ -135,6 +146,11 @@ typedef struct orda_problem {
                              without gradients), teacher CE off and the
                              divergence ORDA_DIV_FORWARD_KL or
                              ORDA_DIV_SOFT_TARGET_CE                          */
+  int64_t norm_dim;       /* ORDA_STUDENT_RMSNORM: columns the mean of x^2
+                             runs over (the unpadded hidden size,
+                             1 <= norm_dim <= hidden; 0 = hidden); columns
+                             past it must be zero in x                        */
+  float norm_eps;         /* ORDA_STUDENT_RMSNORM: >= 0                       */
 } orda_problem_t;
 
 /* Tensors of one loss evaluation.  Unused pointers may be NULL. */
@@ -166,6 +182,9 @@ typedef struct orda_tensors {
    * teacher's log-probabilities there (temperature 1)                        */
   const int64_t* teacher_topk_indices; /* [N x topk]                          */
   const float* teacher_topk_logprobs;  /* [N x topk] fp32                     */
+  /* ORDA_STUDENT_RMSNORM                                                     */
+  const void* student_norm_weight;     /* [H] dtype                           */
+  void* grad_student_norm_weight;      /* [H] dtype                           */
 } orda_tensors_t;
 
 /* ABI version of the loaded library (ORDA_ABI_VERSION). */

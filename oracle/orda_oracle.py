@@ -35,6 +35,16 @@ relative to ``src/orda_ce_kernel/``):
   definition; then the GEMMs of ``ops/tied_teacher.py:468-495`` and the
   ``grad_output * mean_scale`` scaling of ``:538-545``.
 
+Two teachers and a prologue that the reference's loss API does not have
+(its benchmark producer and cache have them; see the tests named here):
+
+* a top-k teacher read as precomputed logits ``lp`` on its ids and ``-inf``
+  elsewhere (``topk_dense_logits``; ``tests/test_topk_teacher.py``);
+* the student's final RMSNorm in front of the loss, ``y = x rsqrt(mean(x^2)
+  + eps) w`` (the reference producer, ``test/benchmark/src/core.py:13-14``),
+  with ``dx``, ``dw`` by the chain rule (``student_norm_weight=``;
+  ``tests/test_rmsnorm_prologue.py``).
+
 How it is pinned (``tests/test_oracle.py``): against torch float64 autograd
 of ``F.cross_entropy`` / ``F.log_softmax`` / ``F.kl_div`` (the reference's own
 test oracle, ``test/utils/reference.py:60-93``) on the reference's CPU test
@@ -235,6 +245,9 @@ def distillation_loss_oracle(
     grad_output: float = 1.0,
     teacher_grads: bool = True,
     grad_logits_dtype: str | None = None,
+    student_norm_weight: np.ndarray | None = None,
+    norm_eps: float = 1e-6,
+    normed_dtype: str | None = None,
 ) -> dict:
     """Loss components and gradients, float64.
 
@@ -246,6 +259,14 @@ def distillation_loss_oracle(
     """
     hs = np.asarray(student_hidden, dtype=np.float64)
     W = np.asarray(weight, dtype=np.float64)
+    x_in = r_norm = g_norm = None
+    if student_norm_weight is not None:
+        # the student's RMSNorm (reference test/benchmark/src/core.py:13-14);
+        # y optionally rounded to the dtype the kernels store it in
+        x_in = hs
+        g_norm = np.asarray(student_norm_weight, dtype=np.float64)
+        r_norm = 1.0 / np.sqrt((x_in * x_in).mean(axis=1) + float(norm_eps))
+        hs = round_to(x_in * r_norm[:, None] * g_norm[None, :], normed_dtype)
     y = np.asarray(labels, dtype=np.int64)
     N, V = hs.shape[0], W.shape[0]
     w_t = (1.0 if mode == "tied" else 0.0) if teacher_ce_weight is None else float(teacher_ce_weight)
@@ -310,4 +331,12 @@ def distillation_loss_oracle(
         if mode == "separate" and teacher_grads:
             out["grad_teacher_hidden"] = dl_t @ Wt
             out["grad_teacher_weight"] = dl_t.T @ ht
+    if x_in is not None:
+        # through the RMSNorm: dy -> dw = sum_t dy x r, dx = r (w dy) - x r^3 <w dy, x> / H
+        dy = out["grad_student_hidden"]
+        out["grad_student_norm_weight"] = (dy * x_in * r_norm[:, None]).sum(axis=0)
+        gdy = dy * g_norm[None, :]
+        c = (gdy * x_in).sum(axis=1)
+        out["grad_student_hidden"] = (r_norm[:, None] * gdy
+                                      - x_in * (r_norm ** 3 * c / x_in.shape[1])[:, None])
     return out

@@ -87,6 +87,11 @@ struct Plan {
   int64_t kps_s, kps_t;
   size_t off_L, off_fpart, off_flabelx, off_frowp, off_frowv, off_split, off_fhT, off_fhtT, off_corr, off_lse;
   int64_t fldh;
+  // the student's final RMSNorm in front of the loss
+  bool norm, need_gnw, need_dy;
+  int64_t norm_dim;
+  int norm_groups;
+  size_t off_hn, off_rstd, off_dy, off_gpart, off_gacc;
 };
 
 constexpr int kScalFloats = 64;  // scalars at the head of the saved buffer
@@ -144,6 +149,19 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
                   p->divergence);
     if (!(p->flags & ORDA_GRADS_IN_FORWARD))
       return fail(ORDA_EINVAL, "a top-k teacher runs the gradients-in-forward schedule (ORDA_GRADS_IN_FORWARD)");
+  }
+  pl.norm = (p->flags & ORDA_STUDENT_RMSNORM) != 0;
+  pl.need_gnw = pl.norm && (p->flags & ORDA_NEED_GRAD_STUDENT_NORM_WEIGHT) != 0;
+  if (!pl.norm && (p->flags & ORDA_NEED_GRAD_STUDENT_NORM_WEIGHT))
+    return fail(ORDA_EINVAL, "ORDA_NEED_GRAD_STUDENT_NORM_WEIGHT needs ORDA_STUDENT_RMSNORM");
+  if (pl.norm) {
+    if (!(p->flags & ORDA_GRADS_IN_FORWARD))
+      return fail(ORDA_EINVAL, "ORDA_STUDENT_RMSNORM runs the gradients-in-forward schedule (ORDA_GRADS_IN_FORWARD)");
+    pl.norm_dim = p->norm_dim > 0 ? p->norm_dim : p->hidden;
+    if (p->norm_dim < 0 || pl.norm_dim > p->hidden)
+      return fail(ORDA_EINVAL, "norm_dim must be in [1, hidden] (0 = hidden), got %lld", (long long)p->norm_dim);
+    if (!(p->norm_eps >= 0.f) || !std::isfinite(p->norm_eps))
+      return fail(ORDA_EINVAL, "norm_eps must be finite and >= 0, got %g", (double)p->norm_eps);
   }
   if (!need_teacher || pl.topk) pl.tsrc = TSRC_NONE;
   else if (p->mode == ORDA_MODE_TIED) pl.tsrc = TSRC_SHARED;
@@ -360,7 +378,7 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.off_frowp = carve(fo, (size_t)kNRowP * pl.fnP * 4);
     pl.off_frowv = carve(fo, (size_t)3 * pl.N * 4);
     int64_t split_cols = 0;
-    if (pl.need_gs && pl.splits_s > 1) split_cols = pl.splits_s * pl.H;
+    if ((pl.need_gs || pl.need_gnw) && pl.splits_s > 1) split_cols = pl.splits_s * pl.H;
     if (pl.w_dln_t && pl.splits_t > 1 && pl.splits_t * pl.Ht > split_cols) split_cols = pl.splits_t * pl.Ht;
     pl.off_split = split_cols ? carve(fo, (size_t)split_cols * pl.fnP * 4) : 0;
     // the chunk's hidden states transposed (token-contiguous) for the grad-W
@@ -372,6 +390,15 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.off_fhtT = (sep && pl.need_gwt && pl.w_dlt_t) ? carve(fo, (size_t)pl.Ht * pl.fnP * pl.eb) : 0;
     pl.off_corr = pl.topk ? carve(fo, (size_t)pl.fnP * p->topk * 4) : 0;
     pl.off_lse = pl.topk ? carve(fo, (size_t)pl.fnP * 4) : 0;
+    // RMSNorm prologue: the chunk's normalised rows, their rsqrt, dloss/dy when
+    // dloss/dx is not asked for, and the norm weight's gradient sums
+    pl.need_dy = pl.need_gs || pl.need_gnw;
+    pl.norm_groups = (int)std::min<int64_t>(64, cdiv(pl.fn, 8));
+    pl.off_hn = pl.norm ? carve(fo, (size_t)pl.fnP * pl.H * pl.eb) : 0;
+    pl.off_rstd = pl.norm ? carve(fo, (size_t)pl.fnP * 4) : 0;
+    pl.off_dy = (pl.need_gnw && !pl.need_gs) ? carve(fo, (size_t)pl.fnP * pl.H * pl.eb) : 0;
+    pl.off_gpart = pl.need_gnw ? carve(fo, (size_t)pl.norm_groups * pl.H * 4) : 0;
+    pl.off_gacc = pl.need_gnw ? carve(fo, (size_t)pl.H * 4) : 0;
     pl.fwd_bytes = fo + kAlign;
     pl.bwd_bytes = 0;
   }
@@ -680,7 +707,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
   float* scal = static_cast<float*>(t->saved);
   const bool reduction_sum = (p->flags & ORDA_REDUCTION_SUM) != 0;
   const bool tgrad = pl.w_dlt_t || pl.w_dln_t;
-  const bool any_grad = pl.need_gs || pl.need_gw || tgrad;
+  const bool any_grad = pl.need_gs || pl.need_gw || pl.need_gnw || tgrad;
   const T* hs = static_cast<const T*>(t->student_hidden);
   const T* ht = static_cast<const T*>(t->teacher_hidden);
   const T* W = static_cast<const T*>(t->weight);
@@ -695,19 +722,32 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     const int64_t r0 = c * pl.fn;
     const int64_t nc = (N - r0 < pl.fn) ? N - r0 : pl.fn;
 
+    // the chunk's student rows as the GEMMs see them: the caller's, or their
+    // RMSNorm (then x is the caller's rows and hsc the normalised copy)
+    const T* hsc = hs + r0 * H;
+    NormParams Nm{};
+    if (pl.norm) {
+      Nm.x = hs + r0 * H; Nm.gamma = t->student_norm_weight; Nm.y = ws + pl.off_hn;
+      Nm.rstd = reinterpret_cast<float*>(ws + pl.off_rstd);
+      Nm.N = nc; Nm.H = H; Nm.D = pl.norm_dim; Nm.eps = p->norm_eps;
+      Nm.groups = pl.norm_groups; Nm.first = c == 0 ? 1 : 0;
+      { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_rmsnorm_fwd<T>(Nm, s)); }
+      hsc = reinterpret_cast<const T*>(ws + pl.off_hn);
+    }
+
     LabelParams Lb{};
     // the chunk's rows of precomputed teacher logits [N x V] (logits dtype)
     const void* Ltc = t->teacher_logits
                           ? static_cast<const char*>(t->teacher_logits) + r0 * V * dtype_bytes(p->logits_dtype)
                           : nullptr;
-    Lb.hs = hs + r0 * H; Lb.W = W; Lb.ht = ht ? ht + r0 * Ht : nullptr; Lb.Wt = Wt; Lb.Lt = Ltc;
+    Lb.hs = hsc; Lb.W = W; Lb.ht = ht ? ht + r0 * Ht : nullptr; Lb.Wt = Wt; Lb.Lt = Ltc;
     Lb.labels = t->labels + r0;
     Lb.N = nc; Lb.V = V; Lb.H = H; Lb.Ht = Ht; Lb.ignore_index = p->ignore_index;
     Lb.tsrc = pl.tsrc; Lb.lt_dtype = p->logits_dtype; Lb.out = labelx;
     { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_label<T>(Lb, s)); }
 
     FusedParams F{};
-    F.W = W; F.hs = hs + r0 * H; F.ht = ht ? ht + r0 * Ht : nullptr; F.Wt = Wt; F.Lt = Ltc;
+    F.W = W; F.hs = hsc; F.ht = ht ? ht + r0 * Ht : nullptr; F.Wt = Wt; F.Lt = Ltc;
     F.labels = t->labels + r0;
     F.N = nc; F.V = V; F.H = H; F.Ht = Ht; F.ignore_index = p->ignore_index;
     F.tsrc = pl.tsrc; F.lt_dtype = p->logits_dtype;
@@ -768,7 +808,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     TopKParams K{};
     if (pl.topk && pl.div_on) {
       // the teacher's k ids: divergence rows and the ids' dlogits share
-      K.hs = hs + r0 * H; K.W = W; K.idx = t->teacher_topk_indices + r0 * p->topk;
+      K.hs = hsc; K.W = W; K.idx = t->teacher_topk_indices + r0 * p->topk;
       K.lp = t->teacher_topk_logprobs + r0 * p->topk; K.labels = t->labels + r0; K.mean_scale = scal;
       K.lse_sT = reinterpret_cast<const float*>(ws + pl.off_lse); K.rowp = rowp; K.rowv = rowv + r0; K.ldv = N; K.corr = reinterpret_cast<float*>(ws + pl.off_corr);
       K.L = L; K.ldL = ldL; K.N = nc; K.V = V; K.H = H; K.k = p->topk; K.ignore_index = p->ignore_index;
@@ -825,7 +865,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     if (pl.need_gw) {
       const bool both = tied && pl.w_dlt_t;
       char* hT = ws + pl.off_fhT;
-      ORDA_TRY(transpose_chunk(hs + r0 * H, H, hT, pl.fldh, 0));
+      ORDA_TRY(transpose_chunk(hsc, H, hT, pl.fldh, 0));
       if (both) ORDA_TRY(transpose_chunk(ht + r0 * H, H, hT, pl.fldh, nP));
       const int64_t K = both ? 2 * nP : nP;
       ORDA_TRY(gemm2<T>(KMAJ, KMAJ, L, ldL, hT, pl.fldh, nullptr, 0, K, K, 0, t->grad_weight, nullptr, H, V, H, K,
@@ -838,9 +878,9 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
                         t->grad_teacher_weight, nullptr, Ht, V, Ht, nP, wmode, 1, 0, s, ORDA_K_GEMM_W,
                         2.0 * (double)V * (double)Ht * (double)nc));
     }
-    auto grad_hidden = [&](const char* Lcol, const T* Wx, int64_t Hx, void* out, int splits, int64_t kps) -> int {
+    // (dst: the chunk's first output row)
+    auto grad_hidden = [&](const char* Lcol, const T* Wx, int64_t Hx, T* dst, int splits, int64_t kps) -> int {
       const double fl = 2.0 * (double)nc * (double)Hx * (double)V;
-      T* dst = static_cast<T*>(out) + r0 * Hx;
       if (splits <= 1)
         return gemm2<T>(MNMAJ, MNMAJ, Lcol, ldL, Wx, Hx, nullptr, 0, V, V, 0, dst, nullptr, Hx, nc, Hx, V,
                         GEMM_STORE, 1, 0, s, ORDA_K_GEMM_H, fl);
@@ -850,9 +890,26 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       ORDA_CHECK_LAUNCH(launch_splitk_reduce<T>(split, splits, nc * Hx, dst, Hx, nc, Hx, s));
       return ORDA_OK;
     };
-    if (pl.need_gs) ORDA_TRY(grad_hidden(L, W, H, t->grad_student_hidden, pl.splits_s, pl.kps_s));
+    if (pl.need_dy) {
+      // dloss/dy of the chunk's rows; with the norm, then dloss/dgamma and
+      // dloss/dx (in place)
+      T* dy = pl.need_gs ? static_cast<T*>(t->grad_student_hidden) + r0 * H : reinterpret_cast<T*>(ws + pl.off_dy);
+      ORDA_TRY(grad_hidden(L, W, H, dy, pl.splits_s, pl.kps_s));
+      if (pl.norm) {
+        Nm.dxy = dy;
+        if (pl.need_gnw) {
+          Nm.gpart = reinterpret_cast<float*>(ws + pl.off_gpart);
+          Nm.gacc = reinterpret_cast<float*>(ws + pl.off_gacc);
+          Nm.gout = c + 1 == pl.fnchunks ? t->grad_student_norm_weight : nullptr;
+          Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+          ORDA_CHECK_LAUNCH(launch_rmsnorm_dgamma<T>(Nm, s));
+        }
+        if (pl.need_gs) { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_rmsnorm_bwd<T>(Nm, s)); }
+      }
+    }
     if (pl.w_dln_t)
-      ORDA_TRY(grad_hidden(L + nP * eb, tied ? W : Wt, Ht, t->grad_teacher_hidden, pl.splits_t, pl.kps_t));
+      ORDA_TRY(grad_hidden(L + nP * eb, tied ? W : Wt, Ht, static_cast<T*>(t->grad_teacher_hidden) + r0 * Ht,
+                           pl.splits_t, pl.kps_t));
   }
 
   FinalizeParams Z{};
@@ -884,6 +941,7 @@ int run_scale(const Plan& pl, const orda_tensors_t* t, hipStream_t s) {
   if (pl.need_gw) ORDA_TRY(sc(t->grad_weight, pl.V * pl.H));
   if (pl.need_gt) ORDA_TRY(sc(t->grad_teacher_hidden, pl.N * pl.Ht));
   if (pl.need_gwt) ORDA_TRY(sc(t->grad_teacher_weight, pl.V * pl.Ht));
+  if (pl.need_gnw) ORDA_TRY(sc(t->grad_student_norm_weight, pl.H));
   return ORDA_OK;
 }
 
@@ -892,7 +950,9 @@ int check_grads(const Plan& pl, const orda_tensors_t* t) {
   if (pl.need_gw && !t->grad_weight) return fail(ORDA_EINVAL, "grad_weight is required");
   if (pl.need_gt && !t->grad_teacher_hidden) return fail(ORDA_EINVAL, "grad_teacher_hidden is required");
   if (pl.need_gwt && !t->grad_teacher_weight) return fail(ORDA_EINVAL, "grad_teacher_weight is required");
-  for (const void* g : {t->grad_student_hidden, t->grad_weight, t->grad_teacher_hidden, t->grad_teacher_weight})
+  if (pl.need_gnw && !t->grad_student_norm_weight) return fail(ORDA_EINVAL, "grad_student_norm_weight is required");
+  for (const void* g : {t->grad_student_hidden, t->grad_weight, t->grad_teacher_hidden, t->grad_teacher_weight,
+                        t->grad_student_norm_weight})
     if (g && !aligned16(g)) return fail(ORDA_EINVAL, "gradient buffers must be 16-byte aligned");
   return ORDA_OK;
 }
@@ -908,6 +968,8 @@ int check_operands(const Plan& pl, const orda_tensors_t* t) {
     return fail(ORDA_EINVAL, "teacher_hidden must be 16-byte aligned");
   if (pl.tsrc == TSRC_SEP && !aligned16(t->teacher_weight)) return fail(ORDA_EINVAL, "teacher_weight must be 16-byte aligned");
   if (pl.tsrc == TSRC_MEM && !t->teacher_logits) return fail(ORDA_EINVAL, "teacher_logits are required");
+  if (pl.norm && (!t->student_norm_weight || !aligned16(t->student_norm_weight)))
+    return fail(ORDA_EINVAL, "student_norm_weight is required (16-byte aligned) with ORDA_STUDENT_RMSNORM");
   if (pl.topk && (!t->teacher_topk_indices || !t->teacher_topk_logprobs))
     return fail(ORDA_EINVAL, "teacher_topk_indices and teacher_topk_logprobs are required");
   if (!t->saved) return fail(ORDA_EINVAL, "saved buffer is required");

@@ -1391,11 +1391,12 @@ __global__ __launch_bounds__(256) void k_scale(T* __restrict__ x, int64_t n, con
   const float s = g[0];
   if (s == 1.0f) return;
   for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
+    const int cnt = (int)min<int64_t>(4, n - i);  // (a ragged tail element by element)
     float v[4];
-    load4(x + i, v, true, 4);
+    load4(x + i, v, cnt == 4, cnt);
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] *= s;
-    store4(x + i, v, true, 4);
+    store4(x + i, v, cnt == 4, cnt);
   }
 }
 
@@ -2008,6 +2009,101 @@ __global__ __launch_bounds__(256) void k_topk_scatter(TopKParams P) {
   *e = from_f32<T>(to_f32(*e) + P.corr[g]);
 }
 
+// ------------------------------------------------ student RMSNorm prologue
+// One wave per row: y = x * r * gamma with r = rsqrt(sum(x^2) / D + eps),
+// in fp32 from the row's 4-element groups, rounded once to T (the reference
+// producer's RMSNorm, test/benchmark/src/core.py:13-14, computes the same
+// product in the activation dtype).
+template <class T>
+__global__ __launch_bounds__(256) void k_rmsnorm_fwd(NormParams P) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= P.N) return;  // whole waves
+  const T* x = static_cast<const T*>(P.x) + t * P.H;
+  const T* g = static_cast<const T*>(P.gamma);
+  T* y = static_cast<T*>(P.y) + t * P.H;
+  const int64_t ng = P.H / 4;
+  float ss = 0.f;
+  for (int64_t c = lane; c < ng; c += 64) {
+    float v[4];
+    load4(x + c * 4, v, true, 4);
+    ss += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)P.D + P.eps);
+  if (lane == 0) P.rstd[t] = r;
+  for (int64_t c = lane; c < ng; c += 64) {
+    float v[4], w[4];
+    load4(x + c * 4, v, true, 4);
+    load4(g + c * 4, w, true, 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = v[e] * r * w[e];
+    store4(y + c * 4, v, true, 4);
+  }
+}
+
+// dloss/dgamma_h = sum_t dy[t][h] x[t][h] r_t: one thread per column h and
+// token group (blockIdx.y), a sequential sum over the group's tokens into
+// gpart[group][h]; then (k_rmsnorm_gacc) the groups summed in order into gacc,
+// and on the last chunk the result in T.
+template <class T>
+__global__ __launch_bounds__(256) void k_rmsnorm_dgamma(NormParams P) {
+  const int64_t h = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (h >= P.H) return;
+  const int64_t per = (P.N + P.groups - 1) / P.groups;
+  const int64_t t0 = (int64_t)blockIdx.y * per;
+  const int64_t t1 = min<int64_t>(P.N, t0 + per);
+  const T* dy = static_cast<const T*>(P.dxy);
+  const T* x = static_cast<const T*>(P.x);
+  float acc = 0.f;
+  for (int64_t t = t0; t < t1; ++t) acc += to_f32(dy[t * P.H + h]) * to_f32(x[t * P.H + h]) * P.rstd[t];
+  P.gpart[(int64_t)blockIdx.y * P.H + h] = acc;
+}
+template <class T>
+__global__ __launch_bounds__(256) void k_rmsnorm_gacc(NormParams P) {
+  const int64_t h = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (h >= P.H) return;
+  float s = 0.f;
+  for (int gi = 0; gi < P.groups; ++gi) s += P.gpart[(int64_t)gi * P.H + h];
+  const float a = P.first ? s : P.gacc[h] + s;
+  P.gacc[h] = a;
+  if (P.gout) static_cast<T*>(P.gout)[h] = from_f32<T>(a);
+}
+
+// dloss/dx = r (gamma . dy) - x r^3 <gamma . dy, x> / D, in place over dy
+// (one wave per row; two passes over the row).
+template <class T>
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= P.N) return;
+  const T* x = static_cast<const T*>(P.x) + t * P.H;
+  const T* g = static_cast<const T*>(P.gamma);
+  T* d = static_cast<T*>(P.dxy) + t * P.H;
+  const int64_t ng = P.H / 4;
+  float c = 0.f;
+  for (int64_t i = lane; i < ng; i += 64) {
+    float v[4], w[4], dy[4];
+    load4(x + i * 4, v, true, 4);
+    load4(g + i * 4, w, true, 4);
+    load4(d + i * 4, dy, true, 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c += w[e] * dy[e] * v[e];
+  }
+  c = wave_sum(c);
+  const float r = P.rstd[t];
+  const float k = r * r * r * c / (float)P.D;
+  for (int64_t i = lane; i < ng; i += 64) {
+    float v[4], w[4], dy[4];
+    load4(x + i * 4, v, true, 4);
+    load4(g + i * 4, w, true, 4);
+    load4(d + i * 4, dy, true, 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dy[e] = r * w[e] * dy[e] - v[e] * k;
+    store4(d + i * 4, dy, true, 4);
+  }
+}
+
 // Materialised path: scan variants with the logits store (phase 0 only).
 #define ORDA_SCANST_CASE(T, SV)                                                                  \
   case SV:                                                                                       \
@@ -2139,6 +2235,28 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
     dlm_go<T, D, false>(P, s);                                   \
   }
 #define ORDA_INSTANTIATE_FB(T)                                                             \
+  template <> hipError_t launch_rmsnorm_fwd<T>(const NormParams& P, hipStream_t s) {       \
+    if (!P.x || !P.gamma || !P.y || !P.rstd || P.H % 4 != 0 || P.D < 1 || P.D > P.H)       \
+      return hipErrorInvalidValue;                                                         \
+    if (P.N <= 0) return hipSuccess;                                                       \
+    hipLaunchKernelGGL(k_rmsnorm_fwd<T>, dim3((unsigned)((P.N + 3) / 4)), dim3(256), 0, s, P); \
+    return hipGetLastError();                                                              \
+  }                                                                                        \
+  template <> hipError_t launch_rmsnorm_dgamma<T>(const NormParams& P, hipStream_t s) {    \
+    if (!P.x || !P.dxy || !P.rstd || !P.gpart || !P.gacc || P.groups < 1 || P.groups > 65535) \
+      return hipErrorInvalidValue;                                                         \
+    const unsigned bx = (unsigned)((P.H + 255) / 256);                                     \
+    hipLaunchKernelGGL(k_rmsnorm_dgamma<T>, dim3(bx, (unsigned)P.groups), dim3(256), 0, s, P); \
+    hipLaunchKernelGGL(k_rmsnorm_gacc<T>, dim3(bx), dim3(256), 0, s, P);                   \
+    return hipGetLastError();                                                              \
+  }                                                                                        \
+  template <> hipError_t launch_rmsnorm_bwd<T>(const NormParams& P, hipStream_t s) {       \
+    if (!P.x || !P.gamma || !P.dxy || !P.rstd || P.H % 4 != 0 || P.D < 1)                  \
+      return hipErrorInvalidValue;                                                         \
+    if (P.N <= 0) return hipSuccess;                                                       \
+    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3((unsigned)((P.N + 3) / 4)), dim3(256), 0, s, P); \
+    return hipGetLastError();                                                              \
+  }                                                                                        \
   template <> hipError_t launch_topk_rows<T>(const TopKParams& P, hipStream_t s) {         \
     if (!P.hs || !P.W || !P.idx || !P.lp || !P.labels || !P.mean_scale || !P.lse_sT ||     \
         !P.rowp || !P.rowv || !P.corr || P.k < 1)                                          \

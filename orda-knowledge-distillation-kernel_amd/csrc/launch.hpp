@@ -125,6 +125,24 @@ struct TopKParams {
   float invT, temperature, w_kl;
 };
 
+// The student's final RMSNorm in front of the loss, per token chunk:
+// y = x * rsqrt(mean(x^2) + eps) * gamma (k_rmsnorm_fwd), dloss/dgamma
+// accumulated over chunks (k_rmsnorm_dgamma, then the fixed-order sum of its
+// token-group partials), dloss/dx in place of dloss/dy (k_rmsnorm_bwd).
+struct NormParams {
+  const void* x;      // [N x H] the norm's input rows of the chunk
+  const void* gamma;  // [H]
+  void* y;            // [N x H] the normalised rows (compute dtype)
+  float* rstd;        // [N] rsqrt(mean(x^2) + eps) per row
+  void* dxy;          // [N x H] dloss/dy in; dloss/dx out (k_rmsnorm_bwd)
+  float* gpart;       // [groups x H] fp32 token-group partial sums of dloss/dgamma
+  float* gacc;        // [H] fp32 dloss/dgamma over the chunks so far
+  void* gout;         // [H] dloss/dgamma in the compute dtype (last chunk), or null
+  int64_t N, H, D;    // rows, columns (padded), columns of the mean
+  int groups, first;  // token groups; first chunk (gacc stored, not added)
+  float eps;
+};
+
 // Phase-1 row sums of the two-pass divergences over stored logits (k_two_rows).
 struct TwoParams {
   const void* L;  // [V][ldL]; student columns [0, N), teacher columns [tcol, tcol + N)
@@ -162,6 +180,9 @@ template <class T> hipError_t launch_gemm2(const GemmParams& P, hipStream_t s);
 template <class T> hipError_t launch_dlm(const DlmParams& P, hipStream_t s);
 template <class T> hipError_t launch_topk_rows(const TopKParams& P, hipStream_t s);
 template <class T> hipError_t launch_topk_scatter(const TopKParams& P, hipStream_t s);
+template <class T> hipError_t launch_rmsnorm_fwd(const NormParams& P, hipStream_t s);
+template <class T> hipError_t launch_rmsnorm_dgamma(const NormParams& P, hipStream_t s);
+template <class T> hipError_t launch_rmsnorm_bwd(const NormParams& P, hipStream_t s);
 template <class T> hipError_t launch_two(const TwoParams& P, hipStream_t s);
 template <class T>
 hipError_t launch_splitk_reduce(const float* part, int splits, int64_t stride, void* out, int64_t ldo, int64_t M,

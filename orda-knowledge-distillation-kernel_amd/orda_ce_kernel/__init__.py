@@ -14,6 +14,7 @@ from .api import (
     KernelConfig,
     PrecomputedTeacher,
     SeparateTeacher,
+    StudentRMSNorm,
     TiedTeacher,
     TopKTeacher,
     distillation_loss,
@@ -22,7 +23,8 @@ from .api import (
 
 from . import compiled  # noqa: E402,F401  (torch.compile-friendly entry; not in __all__)
 
-# TopKTeacher (a top-k precomputed teacher) is importable from here but kept
+# TopKTeacher (a top-k precomputed teacher) and StudentRMSNorm (the student's
+# final RMSNorm fused in front of the loss) are importable from here but kept
 # out of __all__, which stays the reference's public surface.
 
 

@@ -33,6 +33,8 @@ FLAG = {
     "compute_divergence": 1 << 5,
     "reduction_sum": 1 << 6,
     "grads_in_forward": 1 << 7,
+    "student_rmsnorm": 1 << 8,
+    "need_grad_student_norm_weight": 1 << 9,
 }
 
 
@@ -61,6 +63,8 @@ class Problem(ctypes.Structure):
         ("grad_hidden_splits", ctypes.c_int32),
         ("token_chunk", ctypes.c_int64),
         ("topk", ctypes.c_int64),
+        ("norm_dim", ctypes.c_int64),
+        ("norm_eps", ctypes.c_float),
     ]
 
 
@@ -111,6 +115,7 @@ class Tensors(ctypes.Structure):
             "out_loss", "out_student_ce", "out_teacher_ce", "out_kl", "saved", "grad_output",
             "grad_student_hidden", "grad_weight", "grad_teacher_hidden", "grad_teacher_weight",
             "teacher_topk_indices", "teacher_topk_logprobs",
+            "student_norm_weight", "grad_student_norm_weight",
         )
     ]
 

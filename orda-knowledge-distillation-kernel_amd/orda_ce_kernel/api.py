@@ -18,7 +18,10 @@ term; see :mod:`orda_ce_kernel.divergences`.
 
 ``TopKTeacher`` (new, no counterpart in the reference) is a precomputed
 teacher kept as its k most likely ids and their log-probabilities per token;
-see :mod:`orda_ce_kernel.ops.topk_teacher`.
+see :mod:`orda_ce_kernel.ops.topk_teacher`.  ``student_norm=StudentRMSNorm(w,
+eps)`` (new) fuses the student's final RMSNorm in front of the loss:
+``student_hidden`` is then the norm's input; see
+:mod:`orda_ce_kernel.ops.rmsnorm_prologue`.
 """
 from __future__ import annotations
 
@@ -40,7 +43,7 @@ Backend = Literal["auto", "triton", "hip", "torch"]
 
 __all__ = [
     "DistillationLoss", "DistillationLossOutput", "KernelConfig", "PrecomputedTeacher", "SeparateTeacher",
-    "TiedTeacher", "TopKTeacher", "distillation_loss",
+    "StudentRMSNorm", "TiedTeacher", "TopKTeacher", "distillation_loss",
 ]
 
 
@@ -92,6 +95,23 @@ class TopKTeacher:
 
     indices: torch.Tensor
     logprobs: torch.Tensor
+
+
+@dataclass(frozen=True)
+class StudentRMSNorm:
+    """The student's final RMSNorm, fused in front of the loss:
+    ``y = x * rsqrt(mean(x^2, -1) + eps) * weight`` (reference producer,
+    ``test/benchmark/src/core.py:7-14``), with ``x`` the ``student_hidden``
+    passed to the loss and ``weight`` of shape ``[H]``.  Gradients flow to
+    ``x`` and ``weight``.  Not in the reference's loss API."""
+
+    weight: torch.Tensor
+    eps: float = 1e-6
+
+
+def _rmsnorm_torch(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """The reference producer's RMSNorm (``test/benchmark/src/core.py:13-14``)."""
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * weight
 
 
 # ── Config and output types (reference api.py:56-76) ────────────────────────
@@ -359,6 +379,67 @@ def _topk_loss(*, student_hidden, weight, labels, teacher: TopKTeacher, teacher_
     return DistillationLossOutput(*out)
 
 
+def _normed_loss(*, x, weight, labels, teacher, norm: StudentRMSNorm, kw: dict, profile, backend,
+                 resolved: KernelConfig, divergence: Divergence) -> DistillationLossOutput:
+    """``student_norm=`` given: the unfused torch formulation on CPU tensors
+    (or ``backend="torch"``), else the fused HIP prologue."""
+    if not isinstance(norm, StudentRMSNorm):
+        raise TypeError(f"student_norm must be a StudentRMSNorm, got {type(norm).__name__}")
+    nw = norm.weight
+    H = x.shape[1]
+    if not isinstance(nw, torch.Tensor) or nw.ndim != 1 or nw.shape[0] != H or not nw.is_floating_point():
+        raise ValueError(f"StudentRMSNorm.weight must be a floating tensor of shape ({H},), got "
+                         f"{getattr(nw, 'shape', None)}")
+    if nw.device != x.device:
+        raise ValueError("StudentRMSNorm.weight must be on the student's device")
+    eps = float(norm.eps)
+    if not (eps >= 0.0) or eps == float("inf"):
+        raise ValueError(f"StudentRMSNorm.eps must be finite and >= 0, got {norm.eps}")
+    if backend == "torch" or (backend == "auto" and x.device.type != "cuda"):
+        y = _rmsnorm_torch(x, nw, eps)
+        return distillation_loss(y, weight, labels, teacher, profile=profile, backend="torch", config=resolved,
+                                 divergence=divergence, **kw)
+    if not _supports_native(x):
+        raise RuntimeError(
+            f"backend={backend!r} on {x.device} tensors requires the HIP extension liborda_ce.so "
+            f"({native_error() or 'loaded'}); pass backend='torch' to run the unfused PyTorch formulation"
+        )
+    from .ops.rmsnorm_prologue import NormedCall, RMSNormPrologueFunction
+    from .utils.resolver import resolve_chunk_size
+
+    w_t_arg = kw["teacher_ce_weight"]
+    t_logits = tk_i = tk_lp = t_hidden = t_weight = None
+    if isinstance(teacher, TopKTeacher):
+        from .ops.topk_teacher import check_topk_teacher
+
+        if w_t_arg not in (None, 0.0):
+            raise ValueError("a TopKTeacher has no teacher CE: teacher_ce_weight must be None or 0.0")
+        check_topk_teacher(teacher.indices, teacher.logprobs, x.shape[0], weight.shape[0], divergence)
+        mode, w_t, tk_i, tk_lp = "topk", 0.0, teacher.indices, teacher.logprobs
+    else:
+        mode, t_hidden, t_weight, t_logits = _teacher_mode_and_tensors(teacher)
+        _validate_teacher(mode=mode, teacher_hidden=t_hidden, teacher_weight=t_weight, teacher_logits=t_logits,
+                          student_hidden=x, weight=weight)
+        w_t = _resolve_teacher_ce_weight(mode, w_t_arg)
+        if mode == "precomputed":
+            mode = "precomputed_logits" if t_logits is not None else "precomputed_hidden"
+    if profile == "debug":
+        from .ops._checks import check_labels_in_range
+
+        check_labels_in_range(labels, weight.shape[0], kw["ignore_index"])
+    cs, _ = resolve_chunk_size(x.shape[0], resolved.chunk_size, V=weight.shape[0], max_chunks=resolved.max_chunks,
+                               num_chunks=resolved.num_chunks)
+    spec = NormedCall(
+        mode=mode, teacher_logits=t_logits, topk_indices=tk_i, topk_logprobs=tk_lp,
+        student_ce_weight=float(kw["student_ce_weight"]), teacher_ce_weight=float(w_t),
+        kl_weight=float(kw["kl_weight"]), kl_temperature=float(kw["kl_temperature"]),
+        ignore_index=int(kw["ignore_index"]), reduction=kw["reduction"], divergence=divergence,
+        token_chunk=int(cs), eps=eps,
+    )
+    out = RMSNormPrologueFunction.apply(x, nw, weight, t_hidden, t_weight, labels, spec)
+    return DistillationLossOutput(*out)
+
+
 def _supports_native(student_hidden: torch.Tensor) -> bool:
     return bool(HAS_NATIVE and student_hidden.device.type == "cuda")
 
@@ -381,6 +462,7 @@ def distillation_loss(
     backend: Backend = "auto",
     config: KernelConfig | None = None,
     divergence: str | Divergence = "forward_kl",
+    student_norm: StudentRMSNorm | None = None,
 ) -> DistillationLossOutput:
     """Fused LM-head CE + distillation loss.
 
@@ -397,6 +479,11 @@ def distillation_loss(
         backend=backend, config=resolved,
     )
     div = resolve_divergence(divergence)
+    if student_norm is not None:
+        kw = dict(student_ce_weight=student_ce_weight, teacher_ce_weight=teacher_ce_weight, kl_weight=kl_w,
+                  kl_temperature=kl_t, ignore_index=ignore_index, reduction=reduction)
+        return _normed_loss(x=student_hidden, weight=weight, labels=labels, teacher=teacher, norm=student_norm,
+                            kw=kw, profile=profile, backend=backend, resolved=resolved, divergence=div)
     if isinstance(teacher, TopKTeacher):
         return _topk_loss(
             student_hidden=student_hidden, weight=weight, labels=labels, teacher=teacher,
@@ -483,11 +570,11 @@ class DistillationLoss(nn.Module):
         self.config = config
         self.divergence = divergence
 
-    def forward(self, student_hidden, weight, labels, teacher) -> DistillationLossOutput:
+    def forward(self, student_hidden, weight, labels, teacher, student_norm=None) -> DistillationLossOutput:
         return distillation_loss(
             student_hidden, weight, labels, teacher,
             student_ce_weight=self.student_ce_weight, teacher_ce_weight=self.teacher_ce_weight,
             kl_weight=self.kl_weight, kl_temperature=self.kl_temperature, ignore_index=self.ignore_index,
             reduction=self.reduction, profile=self.profile, backend=self.backend, config=self.config,
-            divergence=self.divergence,
+            divergence=self.divergence, student_norm=student_norm,
         )

@@ -138,6 +138,11 @@ class FusedCall:
     token_chunk: int = 0
     topk_indices: torch.Tensor | None = None   # mode "topk": [N x k] int64
     topk_logprobs: torch.Tensor | None = None  # mode "topk": [N x k] fp32
+    # the student's final RMSNorm fused in front of the loss: student_hidden
+    # is then its input x and this its weight [H] (compute dtype)
+    student_norm_weight: torch.Tensor | None = None
+    norm_eps: float = 1e-6
+    need_grad_student_norm_weight: bool = False
 
 
 def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None) -> _native.Problem:
@@ -158,6 +163,10 @@ def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None)
         flags |= _native.FLAG["reduction_sum"]
     if call.grads_in_forward:
         flags |= _native.FLAG["grads_in_forward"]
+    if call.student_norm_weight is not None:
+        flags |= _native.FLAG["student_rmsnorm"]
+        if call.need_grad_student_norm_weight:
+            flags |= _native.FLAG["need_grad_student_norm_weight"]
     div = call.divergence
     p = _native.Problem()
     p.abi_version = _native.ABI_VERSION
@@ -182,6 +191,9 @@ def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None)
     splits = LAUNCH_OVERRIDES.get("grad_hidden_splits")
     p.grad_hidden_splits = int(splits) if splits else 0
     p.topk = int(call.topk_indices.shape[1]) if call.topk_indices is not None else 0
+    if call.student_norm_weight is not None:
+        p.norm_dim = int(call.student_hidden.shape[1])  # the unpadded hidden size
+        p.norm_eps = float(call.norm_eps)
     return p
 
 
@@ -247,59 +259,71 @@ def run_fused_call(call: FusedCall):
             raise ValueError("top-k teacher: indices must be int64 and logprobs float32, both [N, k] on "
                              f"{dev}; got {tk_i.dtype} {tuple(tk_i.shape)} on {tk_i.device}, "
                              f"{tk_lp.dtype} {tuple(tk_lp.shape)} on {tk_lp.device}")
+    nw = None
+    if call.student_norm_weight is not None:
+        # padded like the hidden rows: zero weight on zero columns
+        nw = _pad_cols(call.student_norm_weight.reshape(1, -1), mult).reshape(-1)
+        if nw.dtype != hs.dtype or nw.device != dev:
+            raise ValueError(f"student_norm_weight must be {hs.dtype} on {dev}, got {nw.dtype} on {nw.device}")
     Hp = hs.shape[1]
     Htp = ht.shape[1] if (ht is not None and call.mode != "tied") else Hp
     problem = _problem(call, Hp, Htp, lt.dtype if lt is not None else None)
 
     saved = torch.empty(_native.saved_bytes(problem), dtype=torch.uint8, device=dev)
     outs = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(4)]
-    grads = _alloc_grads(problem.flags, hs, w, ht, wt) if call.grads_in_forward else (None,) * 4
-    inputs = (hs, w, ht, wt, lt, labels, tk_i, tk_lp)
+    grads = _alloc_grads(problem.flags, hs, w, ht, wt, nw) if call.grads_in_forward else (None,) * 5
+    inputs = (hs, w, ht, wt, lt, labels, tk_i, tk_lp, nw)
     _run_forward(problem, inputs, saved, outs, grads)
     return outs, grads, (problem, (H, Ht), inputs, saved)
 
 
 def _run_forward(problem, inputs, saved, outs, grads) -> None:
     """One orda_forward call with a fresh workspace (freed on return)."""
-    hs, w, ht, wt, lt, labels, tk_i, tk_lp = inputs
+    hs, w, ht, wt, lt, labels, tk_i, tk_lp, nw = inputs
     ws = torch.empty(_native.forward_workspace_bytes(problem), dtype=torch.uint8, device=hs.device)
     t = _native.Tensors()
     t.student_hidden, t.weight, t.labels = _ptr(hs), _ptr(w), _ptr(labels)
     t.teacher_hidden, t.teacher_weight, t.teacher_logits = _ptr(ht), _ptr(wt), _ptr(lt)
     t.teacher_topk_indices, t.teacher_topk_logprobs = _ptr(tk_i), _ptr(tk_lp)
+    t.student_norm_weight = _ptr(nw)
     t.out_loss, t.out_student_ce, t.out_teacher_ce, t.out_kl = (o.data_ptr() for o in outs)
     t.saved = saved.data_ptr()
-    t.grad_student_hidden, t.grad_weight, t.grad_teacher_hidden, t.grad_teacher_weight = (_ptr(g) for g in grads)
+    t.grad_student_hidden, t.grad_weight, t.grad_teacher_hidden, t.grad_teacher_weight = (_ptr(g) for g in grads[:4])
+    t.grad_student_norm_weight = _ptr(grads[4])
     _native.forward(problem, t, ws)
     del ws
 
 
-def _alloc_grads(flags: int, hs, w, ht, wt):
+def _alloc_grads(flags: int, hs, w, ht, wt, nw=None):
     need = lambda name: bool(flags & _native.FLAG[name])  # noqa: E731
     g_hs = torch.empty_like(hs) if need("need_grad_student_hidden") else None
     g_w = torch.empty_like(w) if need("need_grad_weight") else None
     g_ht = torch.empty_like(ht) if (need("need_grad_teacher_hidden") and ht is not None) else None
     g_wt = torch.empty_like(wt) if (need("need_grad_teacher_weight") and wt is not None) else None
-    return g_hs, g_w, g_ht, g_wt
+    g_nw = torch.empty_like(nw) if (need("need_grad_student_norm_weight") and nw is not None) else None
+    return g_hs, g_w, g_ht, g_wt, g_nw
 
 
-def fused_backward(ctx, grad_output: torch.Tensor):
+def fused_backward(ctx, grad_output: torch.Tensor, with_norm: bool = False):
     """Gradients ``(d_student_hidden, d_weight, d_teacher_hidden,
-    d_teacher_weight)`` in the compute dtype, unpadded; None where not needed."""
-    hs, w, ht, wt, lt, labels, tk_i, tk_lp, saved = ctx.saved_tensors
+    d_teacher_weight)`` in the compute dtype, unpadded; None where not needed.
+    ``with_norm``: also ``d_student_norm_weight`` (the fused RMSNorm's
+    weight), as a fifth entry."""
+    hs, w, ht, wt, lt, labels, tk_i, tk_lp, nw, saved = ctx.saved_tensors
     problem = ctx.orda_problem
     H, Ht = ctx.orda_shapes
     flags = problem.flags
     dev = hs.device
+    inputs = (hs, w, ht, wt, lt, labels, tk_i, tk_lp, nw)
     if flags & _native.FLAG["grads_in_forward"]:
         grads, ctx.orda_grads = ctx.orda_grads, None
         if grads is None:  # a second backward through a retained graph
-            grads = _alloc_grads(flags, hs, w, ht, wt)
+            grads = _alloc_grads(flags, hs, w, ht, wt, nw)
             outs = [torch.empty((), dtype=torch.float32, device=dev) for _ in range(4)]
-            _run_forward(problem, (hs, w, ht, wt, lt, labels, tk_i, tk_lp), torch.empty_like(saved), outs, grads)
-        g_hs, g_w, g_ht, g_wt = grads
+            _run_forward(problem, inputs, torch.empty_like(saved), outs, grads)
+        g_hs, g_w, g_ht, g_wt, g_nw = grads
     else:
-        g_hs, g_w, g_ht, g_wt = _alloc_grads(flags, hs, w, ht, wt)
+        g_hs, g_w, g_ht, g_wt, g_nw = _alloc_grads(flags, hs, w, ht, wt, nw)
     go = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()
     ws_bytes = 0 if flags & _native.FLAG["grads_in_forward"] else _native.backward_workspace_bytes(problem)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
@@ -307,10 +331,12 @@ def fused_backward(ctx, grad_output: torch.Tensor):
     t.student_hidden, t.weight, t.labels = _ptr(hs), _ptr(w), _ptr(labels)
     t.teacher_hidden, t.teacher_weight, t.teacher_logits = _ptr(ht), _ptr(wt), _ptr(lt)
     t.teacher_topk_indices, t.teacher_topk_logprobs = _ptr(tk_i), _ptr(tk_lp)
+    t.student_norm_weight = _ptr(nw)
     t.saved = saved.data_ptr()
     t.grad_output = go.data_ptr()
     t.grad_student_hidden, t.grad_weight = _ptr(g_hs), _ptr(g_w)
     t.grad_teacher_hidden, t.grad_teacher_weight = _ptr(g_ht), _ptr(g_wt)
+    t.grad_student_norm_weight = _ptr(g_nw)
     _native.backward(problem, t, ws, dev)
     del ws
     if g_hs is not None and g_hs.shape[1] != H:
@@ -322,6 +348,10 @@ def fused_backward(ctx, grad_output: torch.Tensor):
         g_ht = g_ht[:, :ht_cols]
     if g_wt is not None and g_wt.shape[1] != Ht:
         g_wt = g_wt[:, :Ht]
+    if g_nw is not None and g_nw.shape[0] != H:
+        g_nw = g_nw[:H]
+    if with_norm:
+        return g_hs, g_w, g_ht, g_wt, g_nw
     return g_hs, g_w, g_ht, g_wt
 
 

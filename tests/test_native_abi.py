@@ -55,12 +55,13 @@ int main(void) {
   printf("orda_plan_info_t %zu\n", sizeof(orda_plan_info_t));
   F(orda_problem_t, n_rows) F(orda_problem_t, vocab_chunk) F(orda_problem_t, flags) F(orda_problem_t, divergence)
   F(orda_problem_t, temperature) F(orda_problem_t, div_beta) F(orda_problem_t, grad_hidden_splits)
-  F(orda_problem_t, token_chunk) F(orda_problem_t, topk)
+  F(orda_problem_t, token_chunk) F(orda_problem_t, topk) F(orda_problem_t, norm_dim) F(orda_problem_t, norm_eps)
   F(orda_plan_info_t, token_chunk) F(orda_plan_info_t, grad_hidden_splits) F(orda_plan_info_t, vocab_rows_per_split)
   F(orda_plan_info_t, backward_workspace_bytes)
   F(orda_tensors_t, labels) F(orda_tensors_t, saved) F(orda_tensors_t, grad_output)
   F(orda_tensors_t, grad_teacher_weight) F(orda_tensors_t, teacher_topk_indices)
-  F(orda_tensors_t, teacher_topk_logprobs)
+  F(orda_tensors_t, teacher_topk_logprobs) F(orda_tensors_t, student_norm_weight)
+  F(orda_tensors_t, grad_student_norm_weight)
   F(orda_timing_t, milliseconds) F(orda_timing_t, executed_flops)
   printf("ORDA_DIV_COUNT %d\n", (int)ORDA_DIV_COUNT);
   printf("ORDA_K_COUNT %d\n", (int)ORDA_K_COUNT);

@@ -45,7 +45,7 @@ def _call(mode, N, H, V, *, seed, grads, div="forward_kl", T=1.0, token_chunk=0,
     for static in (False, True):
         saved = torch.empty(_native.saved_bytes(problem), dtype=torch.uint8, device="cuda")
         outs = [torch.full((), float("nan"), device="cuda") for _ in range(4)]
-        gr = _alloc_grads(problem.flags, hs, W, ht, wt) if grads else (None,) * 4
+        gr = _alloc_grads(problem.flags, hs, W, ht, wt)[:4] if grads else (None,) * 4
         for x in gr:
             if x is not None:
                 x.fill_(float("nan"))
