@@ -307,7 +307,10 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
                                                                     : TC_OTHER;
     pl.table_entry = find_launch_entry(pl.tclass, pl.dtype, pl.V, pl.H);
     const LaunchEntry* te = pl.table_entry >= 0 ? &kLaunchTable[pl.table_entry] : nullptr;
-    pl.chunk_scale = te ? te->chunk_scale : (pl.f_tmem ? 4 : 2);
+    // (the rule: 4 when the chunk buffer holds only the student's 16-bit
+    // logits -- teacher logits read in place, or no teacher logits at all --
+    // else 2)
+    pl.chunk_scale = te ? te->chunk_scale : (pl.f_tmem || (pl.tsrc == TSRC_NONE && pl.eb == 2) ? 4 : 2);
     pl.scan_groups = te ? te->scan_groups : (int)kPersistentGroups;
     int64_t n = p->token_chunk;
     if (n > 0) {

@@ -1933,15 +1933,64 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// Per token of the chunk (one wave each): the student's logit at each of the
-// teacher's k ids as an fp32 dot product (the wave cooperating on each), the
-// teacher renormalised over its ids at temperature T (online max / sum of
-// lp / T), the divergence row D (forward KL: sum p_t (log p_t - log p_s^T);
-// soft-target CE: -sum p_t log p_s^T) times T^2, and the ids' share of the
-// student's dlogits, -mean_scale w_kl T p_t (scattered after the dense pass).
-// Ids outside [0, V) are clamped to stay in bounds (the caller's contract is
-// distinct ids in range); ids of log-probability -inf add nothing.  Sets the row's teacher log-normaliser to +inf so
-// the dense pass sees a zero teacher.
+// The student's logits at the teacher's ids, x_s[t][i] = <hs_t, W[id_ti]> in
+// fp32, into P.corr[t][i] (k_topk_rows reads them there and overwrites them
+// with the dlogits share).  One wave per (token, group of kTopkIds ids): the
+// hidden row's 16-byte pieces and those of kTopkIds weight rows are loaded
+// together (the rows are independent gathers, so many loads are in flight),
+// then one wave sum per id.  Ids outside [0, V) are clamped into range (the
+// caller's contract is distinct ids in range: no fault either way).
+constexpr int kTopkIds = 4;
+template <class T>
+__global__ __launch_bounds__(256) void k_topk_logits(TopKParams P) {
+  constexpr int E = 16 / sizeof(T);
+  const int lane = threadIdx.x & 63;
+  const int64_t groups = (P.k + kTopkIds - 1) / kTopkIds;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= P.N * groups) return;  // whole waves
+  const int64_t t = item / groups;
+  const int64_t i0 = (item - t * groups) * kTopkIds;
+  const T* hs = static_cast<const T*>(P.hs) + t * P.H;
+  const T* W = static_cast<const T*>(P.W);
+  const T* rows[kTopkIds];
+#pragma unroll
+  for (int j = 0; j < kTopkIds; ++j) {
+    int64_t v = i0 + j < P.k ? P.idx[t * P.k + i0 + j] : 0;
+    v = (v >= 0 && v < P.V) ? v : 0;
+    rows[j] = W + v * P.H;
+  }
+  float acc[kTopkIds];
+#pragma unroll
+  for (int j = 0; j < kTopkIds; ++j) acc[j] = 0.f;
+  const int64_t nc = P.H / E;  // H is a multiple of E (16-byte rows)
+#pragma unroll 2
+  for (int64_t c = lane; c < nc; c += 64) {
+    union U { uint4 u; T e[E]; };
+    U h, w[kTopkIds];
+    h.u = *reinterpret_cast<const uint4*>(hs + c * E);
+#pragma unroll
+    for (int j = 0; j < kTopkIds; ++j) w[j].u = *reinterpret_cast<const uint4*>(rows[j] + c * E);
+#pragma unroll
+    for (int j = 0; j < kTopkIds; ++j)
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[j] += to_f32(h.e[e]) * to_f32(w[j].e[e]);
+  }
+#pragma unroll
+  for (int j = 0; j < kTopkIds; ++j) {
+    const float d = wave_sum(acc[j]);
+    if (lane == 0 && i0 + j < P.k) P.corr[t * P.k + i0 + j] = d;
+  }
+}
+
+// Per token of the chunk (one wave each), from the student logits at its ids
+// (k_topk_logits, in P.corr): the teacher renormalised over its ids at
+// temperature T (online max / sum of lp / T), the divergence row D (forward
+// KL: sum p_t (log p_t - log p_s^T); soft-target CE: -sum p_t log p_s^T)
+// times T^2, and the ids' share of the student's dlogits,
+// -mean_scale w_kl T p_t, over P.corr (each lane reads its ids' logits before
+// it writes their share; scattered after the dense pass).  Ids of
+// log-probability -inf add nothing.  Sets the row's teacher log-normaliser to
+// +inf so the dense pass sees a zero teacher.
 template <class T>
 __global__ __launch_bounds__(256) void k_topk_rows(TopKParams P) {
   const int lane = threadIdx.x & 63;
@@ -1951,20 +2000,12 @@ __global__ __launch_bounds__(256) void k_topk_rows(TopKParams P) {
   const bool ignored = y == P.ignore_index;
   const float invT = P.invT;
   const float lse_sT = P.lse_sT[t];
-  const T* hs = static_cast<const T*>(P.hs) + t * P.H;
-  const T* W = static_cast<const T*>(P.W);
-  const int64_t* idx = P.idx + t * P.k;
+  const float* xk = P.corr + t * P.k;
   const float* lp = P.lp + t * P.k;
   float m = -kInf, sum = 0.f, a = 0.f;
   for (int64_t c0 = 0; c0 < P.k; c0 += 64) {
     const int cnt = (int)min<int64_t>(64, P.k - c0);
-    float mine = 0.f;
-    for (int j = 0; j < cnt; ++j) {
-      int64_t v = idx[c0 + j];
-      v = (v >= 0 && v < P.V) ? v : 0;
-      const float d = wave_sum(row_dot<T>(hs, W + v * P.H, P.H, lane));
-      mine = lane == j ? d : mine;
-    }
+    const float mine = lane < cnt ? xk[c0 + lane] : 0.f;
     const float z = lane < cnt ? lp[c0 + lane] * invT : -kInf;
     if (z > -kInf) {  // (an id of probability 0 adds nothing)
       const float nm = fmaxf(m, z);
@@ -2262,6 +2303,9 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
         !P.rowp || !P.rowv || !P.corr || P.k < 1)                                          \
       return hipErrorInvalidValue;                                                         \
     if (P.N <= 0) return hipSuccess;                                                       \
+    if (P.H % (16 / (int64_t)sizeof(T)) != 0) return hipErrorInvalidValue;                \
+    const int64_t items = P.N * ((P.k + kTopkIds - 1) / kTopkIds);                         \
+    hipLaunchKernelGGL(k_topk_logits<T>, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, P); \
     hipLaunchKernelGGL(k_topk_rows<T>, dim3((unsigned)((P.N + 3) / 4)), dim3(256), 0, s, P); \
     return hipGetLastError();                                                              \
   }                                                                                        \
