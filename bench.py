@@ -110,7 +110,8 @@ def algorithmic_flops(cfg) -> float:
     return 3 * G(H)
 
 
-def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=None, student_norm=False):
+def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=None, student_norm=False,
+            logits_gemm="default"):
     import torch
 
     import orda_ce_kernel as orda
@@ -144,7 +145,7 @@ def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=N
     def step():
         out = orda.distillation_loss(hs, W, y, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t,
                                      kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div,
-                                     config=config, student_norm=norm)
+                                     config=config, student_norm=norm, logits_gemm=logits_gemm)
         out.loss.backward()
         hs.grad = None
         W.grad = None
@@ -406,6 +407,8 @@ def main() -> int:
                          "grad-hidden splits) of configs 2-5, one json line each")
     ap.add_argument("--student-norm", action="store_true",
                     help="fuse the student's final RMSNorm in front of the loss (StudentRMSNorm)")
+    ap.add_argument("--logits-gemm", default="default", choices=("default", "fp8"),
+                    help="fp8: the logits GEMM on e4m3 operands (its own tolerance; not the headline number)")
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true")
@@ -435,7 +438,7 @@ def main() -> int:
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, ignore_frac = cfg
     ms_step, peak_extra, loss_val, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, not args.no_timing,
                                                  row_tau, chunk=args.chunk, splits=args.splits,
-                                                 student_norm=args.student_norm)
+                                                 student_norm=args.student_norm, logits_gemm=args.logits_gemm)
     peak = PEAK_FP32_TFLOPS if dtype_name == "float32" else PEAK_BF16_TFLOPS
     alg = algorithmic_flops(cfg)
     step_tflops = alg / (ms_step / 1e3) / 1e12
@@ -451,14 +454,16 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"bfloat16": "bf16", "float32": "f32", "float16": "f16"}[dtype_name],
+        "dtype": {"bfloat16": "bf16", "float32": "f32", "float16": "f16"}[dtype_name]
+                 + (" (fp8 e4m3 logits GEMM)" if args.logits_gemm == "fp8" else ""),
         "data": "synthetic (seeded randn hidden/weights, uniform labels with ignore_index; no checkpoint)",
         "config": {
             "workload": f"{args.config}: {mode} teacher, N={N} tokens, hidden={H}"
                         + (f", teacher hidden={Ht}" if mode != "tied" else "")
                         + f", vocab={V}, {div}, T={T}, fwd+bwd (grad hidden + grad W)"
                         + (f", top-{TOPK} teacher" if mode == "topk" else "")
-                        + (", student RMSNorm fused (grad x + grad norm weight)" if args.student_norm else ""),
+                        + (", student RMSNorm fused (grad x + grad norm weight)" if args.student_norm else "")
+                        + (", fp8 (e4m3) logits GEMM" if args.logits_gemm == "fp8" else ""),
             "tokens": N, "hidden": H, "vocab": V, "teacher": mode, "divergence": div, "temperature": T,
             "student_ce_weight": w_s, "teacher_ce_weight": w_t, "kl_weight": kl_w, "ignore_frac": ignore_frac,
         },

@@ -101,6 +101,18 @@ enum orda_divergence {
  * dloss/dnorm_weight.  Needs ORDA_GRADS_IN_FORWARD. */
 #define ORDA_STUDENT_RMSNORM (1u << 8)
 #define ORDA_NEED_GRAD_STUDENT_NORM_WEIGHT (1u << 9)
+/* The scan's logits GEMM on gfx950's fp8 MFMA (no counterpart in the
+ * reference; its logits GEMM is a bf16 torch.mm, ops/tied_teacher.py:444-445):
+ * W and the chunk's hidden rows are rounded to OCP e4m3 with one
+ * power-of-two scale per row (v_mfma_scale_f32_32x32x64_f8f6f4 applies the
+ * scales), and the logits (values, softmax statistics, dlogits) come from
+ * those products; the gradient GEMMs stay in the compute dtype.  Needs
+ * ORDA_GRADS_IN_FORWARD, a 16-bit compute dtype, hidden a multiple of 16 and
+ * > 128, and a tied teacher, precomputed logits read in place (ORDA_DIV
+ * families other than the power family) or no teacher term.  Accuracy: see
+ * the library's documentation of the flag (losses within ~1e-2 relative of
+ * the exact values at the headline shape). */
+#define ORDA_FP8_LOGITS (1u << 10)
 
 /* Error codes. */
 #define ORDA_OK 0

@@ -43,7 +43,10 @@ Two teachers and a prologue that the reference's loss API does not have
 * the student's final RMSNorm in front of the loss, ``y = x rsqrt(mean(x^2)
   + eps) w`` (the reference producer, ``test/benchmark/src/core.py:13-14``),
   with ``dx``, ``dw`` by the chain rule (``student_norm_weight=``;
-  ``tests/test_rmsnorm_prologue.py``).
+  ``tests/test_rmsnorm_prologue.py``);
+* the fp8 logits GEMM's operands: rows scaled by a power of two and rounded
+  to OCP E4M3 (``quantize_rows_e4m3``, ``fp8_operands=``; pinned against
+  torch's ``float8_e4m3fn`` in ``tests/test_fp8_logits.py``).
 
 How it is pinned (``tests/test_oracle.py``): against torch float64 autograd
 of ``F.cross_entropy`` / ``F.log_softmax`` / ``F.kl_div`` (the reference's own
@@ -58,8 +61,34 @@ from __future__ import annotations
 
 import numpy as np
 
-__all__ = ["DIVERGENCE_DEFS", "divergence_value_and_grad", "distillation_loss_oracle", "log_softmax", "round_to",
-           "topk_dense_logits"]
+__all__ = ["DIVERGENCE_DEFS", "divergence_value_and_grad", "distillation_loss_oracle", "log_softmax",
+           "quantize_rows_e4m3", "round_e4m3", "round_to", "topk_dense_logits"]
+
+
+def round_e4m3(x: np.ndarray) -> np.ndarray:
+    """``x`` rounded to the nearest OCP FP8 E4M3 value (ties to even; |x| <=
+    448 assumed, as the callers scale it): normal values keep 3 mantissa
+    bits (spacing ``2^(E - 3)`` for ``2^E <= |x| < 2^(E + 1)``, ``E >= -6``),
+    subnormals are multiples of ``2^-9``.  Returned as float64."""
+    x = np.asarray(x, dtype=np.float64)
+    a = np.abs(x)
+    with np.errstate(divide="ignore"):
+        E = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    step = np.exp2(np.maximum(E, -6.0) - 3.0)
+    q = np.round(a / step) * step  # numpy rounds half to even
+    return np.sign(x) * np.minimum(q, 448.0)
+
+
+def quantize_rows_e4m3(x: np.ndarray) -> np.ndarray:
+    """Each row scaled by the power of two ``2^-e`` that puts its amax in
+    ``(224, 448]`` (``e = 0`` for a zero row), rounded to E4M3, and scaled back
+    (dequantised, float64): the operands of the fp8 logits GEMM."""
+    x = np.asarray(x, dtype=np.float64)
+    amax = np.abs(x).max(axis=1)
+    m, k = np.frexp(np.where(amax > 0, amax, 1.0))
+    e = np.where(amax > 0, k - 9 + (m > 0.875), 0).astype(np.float64)
+    sc = np.exp2(e)[:, None]
+    return round_e4m3(x / sc) * sc
 
 
 def topk_dense_logits(indices: np.ndarray, logprobs: np.ndarray, V: int) -> np.ndarray:
@@ -248,6 +277,7 @@ def distillation_loss_oracle(
     student_norm_weight: np.ndarray | None = None,
     norm_eps: float = 1e-6,
     normed_dtype: str | None = None,
+    fp8_operands: bool = False,
 ) -> dict:
     """Loss components and gradients, float64.
 
@@ -281,8 +311,21 @@ def distillation_loss_oracle(
     else:
         ht = np.asarray(teacher_hidden, dtype=np.float64)
         Wt = np.asarray(teacher_weight, dtype=np.float64)
-    x_s = hs @ W.T
-    x_t = np.asarray(teacher_logits, dtype=np.float64) if (ht is None) else ht @ Wt.T
+    if fp8_operands:
+        # the fp8 logits GEMM: its operands rounded per row to E4M3 (the
+        # student's, and the tied teacher's, which shares W); the gradient
+        # GEMMs keep the unrounded operands
+        W8, hs8 = quantize_rows_e4m3(W), quantize_rows_e4m3(hs)
+        x_s = hs8 @ W8.T
+        if mode == "tied":
+            x_t = quantize_rows_e4m3(ht) @ W8.T
+        elif ht is None:
+            x_t = np.asarray(teacher_logits, dtype=np.float64)
+        else:
+            x_t = ht @ Wt.T
+    else:
+        x_s = hs @ W.T
+        x_t = np.asarray(teacher_logits, dtype=np.float64) if (ht is None) else ht @ Wt.T
 
     ignored = y == ignore_index
     y_eff = np.where((y >= 0) & (y < V), y, 0)

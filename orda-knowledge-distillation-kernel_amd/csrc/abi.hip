@@ -89,6 +89,9 @@ struct Plan {
   int64_t fldh;
   // the student's final RMSNorm in front of the loss
   bool norm, need_gnw, need_dy;
+  // fp8 logits GEMM: e4m3 copies of W and of the chunk's hidden rows
+  bool f8;
+  size_t off_w8, off_ew, off_b8, off_eb;
   int64_t norm_dim;
   int norm_groups;
   size_t off_hn, off_rstd, off_dy, off_gpart, off_gacc;
@@ -150,6 +153,8 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     if (!(p->flags & ORDA_GRADS_IN_FORWARD))
       return fail(ORDA_EINVAL, "a top-k teacher runs the gradients-in-forward schedule (ORDA_GRADS_IN_FORWARD)");
   }
+  if ((p->flags & ORDA_FP8_LOGITS) && !(p->flags & ORDA_GRADS_IN_FORWARD))
+    return fail(ORDA_EINVAL, "ORDA_FP8_LOGITS runs the gradients-in-forward schedule (ORDA_GRADS_IN_FORWARD)");
   pl.norm = (p->flags & ORDA_STUDENT_RMSNORM) != 0;
   pl.need_gnw = pl.norm && (p->flags & ORDA_NEED_GRAD_STUDENT_NORM_WEIGHT) != 0;
   if (!pl.norm && (p->flags & ORDA_NEED_GRAD_STUDENT_NORM_WEIGHT))
@@ -402,6 +407,25 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.off_dy = (pl.need_gnw && !pl.need_gs) ? carve(fo, (size_t)pl.fnP * pl.H * pl.eb) : 0;
     pl.off_gpart = pl.need_gnw ? carve(fo, (size_t)pl.norm_groups * pl.H * 4) : 0;
     pl.off_gacc = pl.need_gnw ? carve(fo, (size_t)pl.H * 4) : 0;
+    // fp8 logits: W (V x H bytes + V scale bytes) once per call, the chunk's
+    // student (and tied teacher) rows per chunk
+    pl.f8 = (p->flags & ORDA_FP8_LOGITS) != 0;
+    if (pl.f8) {
+      if (pl.eb != 2) return fail(ORDA_EUNSUPPORTED, "ORDA_FP8_LOGITS needs a 16-bit compute dtype");
+      if (pl.H % 16 != 0 || pl.H <= 128)
+        return fail(ORDA_EUNSUPPORTED, "ORDA_FP8_LOGITS needs hidden a multiple of 16 and > 128, got %lld",
+                    (long long)pl.H);
+      if (pl.topk) return fail(ORDA_EUNSUPPORTED, "ORDA_FP8_LOGITS does not support a top-k teacher");
+      const bool ring = (pl.tclass == TC_TIED) || (pl.f_tmem && pl.fam != FAM_POW) || pl.f_sring;
+      if (!ring)
+        return fail(ORDA_EUNSUPPORTED, "ORDA_FP8_LOGITS supports a tied teacher, precomputed logits read in place "
+                    "(not the power-family divergences) or no teacher term");
+      const int64_t nb = pl.tsrc == TSRC_SHARED ? 2 : 1;
+      pl.off_w8 = carve(fo, (size_t)pl.V * pl.H);
+      pl.off_ew = carve(fo, (size_t)pl.V);
+      pl.off_b8 = carve(fo, (size_t)nb * pl.fnP * pl.H);
+      pl.off_eb = carve(fo, (size_t)nb * pl.fnP);
+    }
     pl.fwd_bytes = fo + kAlign;
     pl.bwd_bytes = 0;
   }
@@ -718,6 +742,16 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
 
   if (pl.f_tmem && reinterpret_cast<uintptr_t>(t->teacher_logits) % 16 != 0)
     return fail(ORDA_EINVAL, "precomputed teacher logits must be 16-byte aligned when the vocabulary is a multiple of 8");
+  uint8_t* w8 = nullptr;
+  uint8_t* ew = nullptr;
+  if (pl.f8) {
+    // W in e4m3 with its row scales, once per call
+    w8 = reinterpret_cast<uint8_t*>(ws + pl.off_w8);
+    ew = reinterpret_cast<uint8_t*>(ws + pl.off_ew);
+    QuantParams Q{W, V, H, w8, ew};
+    Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+    ORDA_CHECK_LAUNCH(launch_quant_f8<T>(Q, s));
+  }
   // mean scale first: the chunks' dlogits need it before the loss rows exist
   { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_count(t->labels, N, p->ignore_index, reduction_sum, scal, s)); }
 
@@ -738,6 +772,24 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       hsc = reinterpret_cast<const T*>(ws + pl.off_hn);
     }
 
+    // fp8: the chunk's student (and tied teacher) rows in e4m3
+    uint8_t* hs8 = nullptr;
+    uint8_t* ht8 = nullptr;
+    uint8_t *es = nullptr, *et = nullptr;
+    if (pl.f8) {
+      hs8 = reinterpret_cast<uint8_t*>(ws + pl.off_b8);
+      es = reinterpret_cast<uint8_t*>(ws + pl.off_eb);
+      QuantParams Q{hsc, nc, H, hs8, es};
+      { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_quant_f8<T>(Q, s)); }
+      if (pl.tsrc == TSRC_SHARED) {
+        ht8 = hs8 + nP * H;
+        et = es + nP;
+        QuantParams Qt{ht + r0 * H, nc, H, ht8, et};
+        Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+        ORDA_CHECK_LAUNCH(launch_quant_f8<T>(Qt, s));
+      }
+    }
+
     LabelParams Lb{};
     // the chunk's rows of precomputed teacher logits [N x V] (logits dtype)
     const void* Ltc = t->teacher_logits
@@ -747,6 +799,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     Lb.labels = t->labels + r0;
     Lb.N = nc; Lb.V = V; Lb.H = H; Lb.Ht = Ht; Lb.ignore_index = p->ignore_index;
     Lb.tsrc = pl.tsrc; Lb.lt_dtype = p->logits_dtype; Lb.out = labelx;
+    Lb.W8 = w8; Lb.hs8 = hs8; Lb.ht8 = ht8; Lb.eW = ew; Lb.eS = es; Lb.eT = et;
     { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_label<T>(Lb, s)); }
 
     FusedParams F{};
@@ -767,6 +820,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     F.partial = part; F.rowp = rowp;
     F.Lout = L; F.ldL = ldL; F.tcolL = nP; F.store_t = pl.store_t;
     F.student_ring = pl.f_sring ? 1 : 0;
+    F.W8 = w8; F.hs8 = hs8; F.ht8 = ht8; F.eW = ew; F.eS = es; F.eT = et;
     if (pl.f_sring) F.n_ttiles = (int)cdiv(nc, 256);
     // teacher logits from memory are no GEMM
     bool tgemm = pl.tsrc == TSRC_SHARED || pl.tsrc == TSRC_SEP;
@@ -790,7 +844,19 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       tgemm = false;
     }
     const double scan_flops = 2.0 * (double)nc * (double)V * ((double)H + (tgemm ? (double)Ht : 0.0));
-    { Timed tm_(ORDA_K_SCAN, s, scan_flops, scan_flops); ORDA_CHECK_LAUNCH(launch_scan_store<T>(F, F.n_ttiles * pl.f_nvr, s)); }
+    if (pl.f8) {
+      if (F.tsrc != TSRC_SHARED && F.tsrc != TSRC_MEM_RING && F.tsrc != TSRC_NONE)
+        return fail(ORDA_EUNSUPPORTED, "ORDA_FP8_LOGITS: this teacher's logits do not reach the fp8 ring scan");
+      if constexpr (sizeof(T) == 2) {
+        Timed tm_(ORDA_K_SCAN, s, scan_flops, scan_flops);
+        ORDA_CHECK_LAUNCH(launch_scan_store_f8<T>(F, F.n_ttiles * pl.f_nvr, s));
+      } else {
+        return fail(ORDA_EUNSUPPORTED, "ORDA_FP8_LOGITS needs a 16-bit compute dtype");
+      }
+    } else {
+      Timed tm_(ORDA_K_SCAN, s, scan_flops, scan_flops);
+      ORDA_CHECK_LAUNCH(launch_scan_store<T>(F, F.n_ttiles * pl.f_nvr, s));
+    }
 
     MergeParams M{};
     M.partial = part; M.n_vranges = pl.f_nvr; M.N = nc; M.V = V; M.ignore_index = p->ignore_index;
@@ -1045,19 +1111,19 @@ int orda_abi_version(void) { return ORDA_ABI_VERSION; }
 const char* orda_last_error(void) { return g_err.c_str(); }
 
 size_t orda_saved_bytes(const orda_problem_t* p) {
-  Plan pl;
+  Plan pl{};
   if (make_plan(p, pl) != ORDA_OK) return 0;
   return pl.saved_bytes;
 }
 
 size_t orda_forward_workspace_bytes(const orda_problem_t* p) {
-  Plan pl;
+  Plan pl{};
   if (make_plan(p, pl) != ORDA_OK) return 0;
   return pl.fwd_bytes;
 }
 
 size_t orda_backward_workspace_bytes(const orda_problem_t* p) {
-  Plan pl;
+  Plan pl{};
   if (make_plan(p, pl) != ORDA_OK) return 0;
   return pl.bwd_bytes;
 }
@@ -1065,7 +1131,7 @@ size_t orda_backward_workspace_bytes(const orda_problem_t* p) {
 int orda_plan_info(const orda_problem_t* p, orda_plan_info_t* out) {
   g_err.clear();
   if (!out) return fail(ORDA_EINVAL, "out is NULL");
-  Plan pl;
+  Plan pl{};
   ORDA_TRY(make_plan(p, pl));
   *out = orda_plan_info_t{};
   out->grads_in_forward = pl.fused ? 1 : 0;
@@ -1101,14 +1167,14 @@ int orda_plan_info(const orda_problem_t* p, orda_plan_info_t* out) {
 int orda_forward(const orda_problem_t* p, const orda_tensors_t* t, void* workspace, size_t workspace_bytes,
                  void* stream) {
   g_err.clear();
-  Plan pl;
+  Plan pl{};
   ORDA_TRY(make_plan(p, pl));
   return forward_with(pl, p, t, workspace, workspace_bytes, stream);
 }
 
 int orda_forward_static(const orda_problem_t* p, const orda_tensors_t* t, void* stream) {
   g_err.clear();
-  Plan pl;
+  Plan pl{};
   ORDA_TRY(make_plan(p, pl));
   if (pl.fwd_bytes > kStaticScratchBytes)
     return fail(ORDA_EWORKSPACE,
@@ -1123,7 +1189,7 @@ int orda_forward_static(const orda_problem_t* p, const orda_tensors_t* t, void* 
 int orda_backward(const orda_problem_t* p, const orda_tensors_t* t, void* workspace, size_t workspace_bytes,
                   void* stream) {
   g_err.clear();
-  Plan pl;
+  Plan pl{};
   ORDA_TRY(make_plan(p, pl));
   ORDA_TRY(check_operands(pl, t));
   if (!t->grad_output) return fail(ORDA_EINVAL, "grad_output is required");

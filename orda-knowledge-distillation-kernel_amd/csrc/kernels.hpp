@@ -5,6 +5,7 @@
 #include "launch.hpp"
 #include "orda_core.hpp"
 #include "ring4.hpp"
+#include "ring4_f8.hpp"
 
 namespace orda {
 
@@ -643,7 +644,7 @@ struct AccPairTL {  // student from accumulator block nb, teacher from registers
 //  TL_FROM_L / TL_FROM_MEM (teacher logits from memory, see
 //    issue_teacher4): 256 tokens per workgroup, B = 256 student hidden rows;
 //    each lane holds four tokens (blocks 0..3).
-template <class T, int SV, bool STORE, int TL>
+template <class T, int SV, bool STORE, int TL, bool F8 = false>
 __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   static_assert(TL == TL_NONE || (!sv_phase1(SV) && STORE), "teacher logits from memory: one-pass, stored");
   static_assert(TL != TL_STUDENT || SV == SV_STUDENT || SV == SV_STUDENT_T, "student-only tiles: no teacher");
@@ -677,16 +678,42 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
   const T* W = static_cast<const T*>(P.W);
   const T* hs = static_cast<const T*>(P.hs);
   const T* ht = static_cast<const T*>(P.ht);
-  const KOp4 bop = TL ? kop4(hs + t0 * P.H, P.H, P.N - t0)
-                      : kop4_split(hs + t0 * P.H, P.N - t0, ht + t0 * P.H, P.N - t0, P.H);
+  KOp4 bop;
+  int sb[4];  // fp8: E8M0 scale byte of B row col4(nb, wn) + lane % 32
+  if constexpr (F8) {
+    const uint8_t* hs8 = static_cast<const uint8_t*>(P.hs8);
+    const uint8_t* ht8 = static_cast<const uint8_t*>(P.ht8);
+    bop = TL ? kop4(hs8 + t0 * P.H, P.H, P.N - t0)
+             : kop4_split(hs8 + t0 * P.H, P.N - t0, ht8 + t0 * P.H, P.N - t0, P.H);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int j = col4(nb, wn) + (lane & 31);
+      const bool teacher_row = !TL && j >= 128;
+      const int64_t t = t0 + (teacher_row ? j - 128 : j);
+      sb[nb] = t < P.N ? (int)(teacher_row ? P.eT : P.eS)[t] : 127;
+    }
+  } else {
+    bop = TL ? kop4(hs + t0 * P.H, P.H, P.N - t0)
+             : kop4_split(hs + t0 * P.H, P.N - t0, ht + t0 * P.H, P.N - t0, P.H);
+  }
   struct TI {
     int v0;
     KOp4 a;
+    int sa[4];  // fp8: E8M0 scale byte of A row wm * 128 + mb * 32 + lane % 32
   };
   auto tile_info = [&](int i) {
     TI x;
     x.v0 = (vt_begin + (i < ntiles ? i : 0)) * 256;
-    x.a = kop4(W + (int64_t)x.v0 * P.H, P.H, P.V - x.v0);
+    if constexpr (F8) {
+      x.a = kop4(static_cast<const uint8_t*>(P.W8) + (int64_t)x.v0 * P.H, P.H, P.V - x.v0);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const int64_t v = x.v0 + wm * 128 + mb * 32 + (lane & 31);
+        x.sa[mb] = v < P.V ? (int)P.eW[v] : 127;
+      }
+    } else {
+      x.a = kop4(W + (int64_t)x.v0 * P.H, P.H, P.V - x.v0);
+    }
     return x;
   };
   auto opnd = [&](const TI& x, int op) { return op == 0 ? x.a : bop; };
@@ -721,7 +748,10 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
       });
     }
   };
-  pipeline4<T, KMAJ, KMAJ, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
+  if constexpr (F8)
+    pipeline4_f8(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue, sb);
+  else
+    pipeline4<T, KMAJ, KMAJ, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
 
   // combine lane l with l^32 (other vocabulary rows of the same tokens), then
   // the two waves sharing the tokens (wm 0 / 1)
@@ -1780,6 +1810,69 @@ __device__ __forceinline__ float row_dot(const T* a, const T* b, int64_t H, int 
   return (acc[0] + acc[1]) + (acc[2] + acc[3]);
 }
 
+// ------------------------------------------------------------ fp8 operands
+// One wave per row (see QuantParams): the row's amax, the E8M0 exponent e
+// with amax 2^-e in (224, 448] (amax = m 2^k, m in [0.5, 1): e = k - 9, or
+// k - 8 when m > 0.875), and the row scaled by 2^-e (exact) and rounded to
+// e4m3 with v_cvt_pk_fp8_f32.
+template <class T>
+__global__ __launch_bounds__(256) void k_quant_f8(QuantParams P) {
+  static_assert(sizeof(T) == 2, "16-bit rows");
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= P.rows) return;  // whole waves
+  const T* x = static_cast<const T*>(P.x) + r * P.H;
+  const int64_t nc = P.H / 8;  // 16-byte pieces of 8 elements
+  float amax = 0.f;
+  for (int64_t c = lane; c < nc; c += 64) {
+    union { uint4 u; T e[8]; } v;
+    v.u = *reinterpret_cast<const uint4*>(x + c * 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(to_f32(v.e[i])));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  int e = 0;
+  if (amax > 0.f) {
+    int k;
+    const float m = frexpf(amax, &k);
+    e = k - 9 + (m > 0.875f ? 1 : 0);
+    e = e < -127 ? -127 : (e > 127 ? 127 : e);
+  }
+  const float sc = ldexpf(1.0f, -e);
+  uint8_t* q = P.q + r * P.H;
+  for (int64_t c = lane; c < nc; c += 64) {
+    union { uint4 u; T e[8]; } v;
+    v.u = *reinterpret_cast<const uint4*>(x + c * 8);
+    int w0 = 0, w1 = 0;
+    w0 = __builtin_amdgcn_cvt_pk_fp8_f32(to_f32(v.e[0]) * sc, to_f32(v.e[1]) * sc, w0, false);
+    w0 = __builtin_amdgcn_cvt_pk_fp8_f32(to_f32(v.e[2]) * sc, to_f32(v.e[3]) * sc, w0, true);
+    w1 = __builtin_amdgcn_cvt_pk_fp8_f32(to_f32(v.e[4]) * sc, to_f32(v.e[5]) * sc, w1, false);
+    w1 = __builtin_amdgcn_cvt_pk_fp8_f32(to_f32(v.e[6]) * sc, to_f32(v.e[7]) * sc, w1, true);
+    *reinterpret_cast<uint2*>(q + c * 8) = make_uint2((uint32_t)w0, (uint32_t)w1);
+  }
+  if (lane == 0) P.e[r] = (uint8_t)(e + 127);
+}
+
+// Lane share of the dot product of two e4m3 rows of H bytes (16-byte
+// pieces; unscaled).
+__device__ __forceinline__ float row_dot_f8(const uint8_t* a, const uint8_t* b, int64_t H, int lane) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  float acc = 0.f;
+  for (int64_t c = lane; c < H / 16; c += 64) {
+    const uint4 va = *reinterpret_cast<const uint4*>(a + c * 16);
+    const uint4 vb = *reinterpret_cast<const uint4*>(b + c * 16);
+    const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f2v a0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)wa[i], false), a1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)wa[i], true);
+      const f2v b0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)wb[i], false), b1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)wb[i], true);
+      acc += a0.x * b0.x + a0.y * b0.y + a1.x * b1.x + a1.y * b1.y;
+    }
+  }
+  return acc;
+}
+
 template <class T>
 __global__ __launch_bounds__(256) void k_label(LabelParams P) {
   const int lane = threadIdx.x & 63;
@@ -1789,16 +1882,27 @@ __global__ __launch_bounds__(256) void k_label(LabelParams P) {
   const int64_t yc = (y >= 0 && y < P.V) ? y : 0;
   const bool ignored = (y == P.ignore_index);
   float xs = 0.f, xt = 0.f;
+  const bool f8 = P.W8 != nullptr;  // the scan's fp8 rows and scales (tied teacher: both)
   if (!ignored) {
-    xs = row_dot(static_cast<const T*>(P.hs) + t * P.H, static_cast<const T*>(P.W) + yc * P.H, P.H, lane);
-    if (P.tsrc == TSRC_SHARED || P.tsrc == TSRC_SEP)
-      xt = row_dot(static_cast<const T*>(P.ht) + t * P.Ht,
-                   static_cast<const T*>(P.tsrc == TSRC_SHARED ? P.W : P.Wt) + yc * P.Ht, P.Ht, lane);
+    if (f8) {
+      const uint8_t* w8 = static_cast<const uint8_t*>(P.W8) + yc * P.H;
+      xs = row_dot_f8(static_cast<const uint8_t*>(P.hs8) + t * P.H, w8, P.H, lane);
+      if (P.tsrc == TSRC_SHARED) xt = row_dot_f8(static_cast<const uint8_t*>(P.ht8) + t * P.H, w8, P.H, lane);
+    } else {
+      xs = row_dot(static_cast<const T*>(P.hs) + t * P.H, static_cast<const T*>(P.W) + yc * P.H, P.H, lane);
+      if (P.tsrc == TSRC_SHARED || P.tsrc == TSRC_SEP)
+        xt = row_dot(static_cast<const T*>(P.ht) + t * P.Ht,
+                     static_cast<const T*>(P.tsrc == TSRC_SHARED ? P.W : P.Wt) + yc * P.Ht, P.Ht, lane);
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     xs += __shfl_xor(xs, o);
     xt += __shfl_xor(xt, o);
+  }
+  if (f8 && !ignored) {
+    xs = ldexpf(xs, (int)P.eW[yc] + (int)P.eS[t] - 254);
+    if (P.tsrc == TSRC_SHARED) xt = ldexpf(xt, (int)P.eW[yc] + (int)P.eT[t] - 254);
   }
   if (lane == 0) {
     if (P.tsrc == TSRC_MEM && !ignored) {
@@ -2191,6 +2295,49 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
     return hipGetLastError();                                                              \
   }
 
+// fp8 logits: the ring scans with e4m3 operands (tied teacher, precomputed
+// logits read by the ring scan, no teacher).
+#define ORDA_SCANF8_CASE(T, SV)                                                                  \
+  case SV:                                                                                       \
+    if (P.tsrc == TSRC_NONE) {                                                                   \
+      if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T)                                      \
+        hipLaunchKernelGGL((k_scan4<T, SV, true, TL_STUDENT, true>), dim3(grid), dim3(kThreads4), 0, s, P); \
+      else                                                                                       \
+        return hipErrorInvalidValue;                                                             \
+    } else if (P.tsrc == TSRC_MEM_RING) {                                                        \
+      if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T || SV == SV_POW)                      \
+        return hipErrorInvalidValue;                                                             \
+      else                                                                                       \
+        hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_MEM, true>), dim3(grid), dim3(kThreads4), 0, s, P); \
+    } else if (P.tsrc == TSRC_SHARED) {                                                          \
+      if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T)                                      \
+        return hipErrorInvalidValue;                                                             \
+      else if (!P.ht8 || !P.eT)                                                                  \
+        return hipErrorInvalidValue;                                                             \
+      else                                                                                       \
+        hipLaunchKernelGGL((k_scan4<T, SV, true, TL_NONE, true>), dim3(grid), dim3(kThreads4), 0, s, P); \
+    } else {                                                                                     \
+      return hipErrorInvalidValue;                                                               \
+    }                                                                                            \
+    break;
+#define ORDA_INSTANTIATE_SCAN_F8(T)                                                        \
+  template <> hipError_t launch_scan_store_f8<T>(const FusedParams& P, int grid, hipStream_t s) { \
+    if (P.phase != 0 || !P.W8 || !P.hs8 || !P.eW || !P.eS || P.H % 16 != 0 || P.H <= 128) \
+      return hipErrorInvalidValue;                                                         \
+    if (P.tsrc == TSRC_MEM_RING && P.V % 4 != 0) return hipErrorInvalidValue;              \
+    switch (scan_variant_of(P)) {                                                          \
+      ORDA_SCANF8_CASE(T, SV_STUDENT)                                                      \
+      ORDA_SCANF8_CASE(T, SV_STUDENT_T)                                                    \
+      ORDA_SCANF8_CASE(T, SV_TCE_T1)                                                       \
+      ORDA_SCANF8_CASE(T, SV_TCE)                                                          \
+      ORDA_SCANF8_CASE(T, SV_LIN_T1)                                                       \
+      ORDA_SCANF8_CASE(T, SV_LIN)                                                          \
+      ORDA_SCANF8_CASE(T, SV_POW)                                                          \
+      default: return hipErrorInvalidValue;                                                \
+    }                                                                                      \
+    return hipGetLastError();                                                              \
+  }
+
 // General GEMM: the (layout, layout, mode) combinations the library uses.
 // Persistent grid: one workgroup per CU (a 128 KiB-LDS workgroup fills a CU).
 inline int persistent_groups() {
@@ -2276,6 +2423,16 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
     dlm_go<T, D, false>(P, s);                                   \
   }
 #define ORDA_INSTANTIATE_FB(T)                                                             \
+  template <> hipError_t launch_quant_f8<T>(const QuantParams& P, hipStream_t s) {         \
+    if constexpr (sizeof(T) != 2) {                                                        \
+      return hipErrorInvalidValue;                                                         \
+    } else {                                                                               \
+      if (!P.x || !P.q || !P.e || P.H % 16 != 0) return hipErrorInvalidValue;              \
+      if (P.rows <= 0) return hipSuccess;                                                  \
+      hipLaunchKernelGGL(k_quant_f8<T>, dim3((unsigned)((P.rows + 3) / 4)), dim3(256), 0, s, P); \
+      return hipGetLastError();                                                            \
+    }                                                                                      \
+  }                                                                                        \
   template <> hipError_t launch_rmsnorm_fwd<T>(const NormParams& P, hipStream_t s) {       \
     if (!P.x || !P.gamma || !P.y || !P.rstd || P.H % 4 != 0 || P.D < 1 || P.D > P.H)       \
       return hipErrorInvalidValue;                                                         \

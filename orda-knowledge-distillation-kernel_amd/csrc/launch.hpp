@@ -67,6 +67,15 @@ struct FusedParams {
   int store_t;
   // no teacher (TSRC_NONE) on the ring scan: 256 student tokens per workgroup
   int student_ring;
+  // fp8 logits GEMM (launch_scan_store_f8): OCP e4m3 copies of W [V x H] and
+  // of the chunk's student / teacher hidden rows [N x H], with one E8M0 scale
+  // byte per row (eW, eS, eT)
+  const void* W8;
+  const void* hs8;
+  const void* ht8;
+  const uint8_t* eW;
+  const uint8_t* eS;
+  const uint8_t* eT;
 };
 
 struct GemmParams {
@@ -169,6 +178,24 @@ struct LabelParams {
   int64_t N, V, H, Ht, ignore_index;
   int tsrc, lt_dtype;
   float* out;  // [2][N]
+  // fp8 logits: the label logits from the same e4m3 rows and row scales as
+  // the scan's (see FusedParams); W8 null otherwise
+  const void* W8;
+  const void* hs8;
+  const void* ht8;
+  const uint8_t* eW;
+  const uint8_t* eS;
+  const uint8_t* eT;
+};
+
+// Rows [rows x H] (compute dtype, pitch H) to OCP e4m3 bytes q [rows x H]
+// and one E8M0 scale byte per row: e = the smallest power of two with
+// amax(row) 2^-e <= 448 (biased by 127), q = RNE(x 2^-e).
+struct QuantParams {
+  const void* x;
+  int64_t rows, H;
+  uint8_t* q;
+  uint8_t* e;
 };
 
 template <class T> hipError_t launch_scan(const FusedParams& P, int grid, hipStream_t s);
@@ -176,6 +203,8 @@ template <class T> hipError_t launch_dl(const FusedParams& P, int grid, hipStrea
 template <class T> hipError_t launch_gemm(const GemmParams& P, hipStream_t s);
 template <class T> hipError_t launch_label(const LabelParams& P, hipStream_t s);
 template <class T> hipError_t launch_scan_store(const FusedParams& P, int grid, hipStream_t s);
+template <class T> hipError_t launch_scan_store_f8(const FusedParams& P, int grid, hipStream_t s);
+template <class T> hipError_t launch_quant_f8(const QuantParams& P, hipStream_t s);
 template <class T> hipError_t launch_gemm2(const GemmParams& P, hipStream_t s);
 template <class T> hipError_t launch_dlm(const DlmParams& P, hipStream_t s);
 template <class T> hipError_t launch_topk_rows(const TopKParams& P, hipStream_t s);

@@ -35,6 +35,7 @@ FLAG = {
     "grads_in_forward": 1 << 7,
     "student_rmsnorm": 1 << 8,
     "need_grad_student_norm_weight": 1 << 9,
+    "fp8_logits": 1 << 10,
 }
 
 

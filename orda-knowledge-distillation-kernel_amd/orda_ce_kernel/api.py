@@ -20,7 +20,9 @@ term; see :mod:`orda_ce_kernel.divergences`.
 teacher kept as its k most likely ids and their log-probabilities per token;
 see :mod:`orda_ce_kernel.ops.topk_teacher`.  ``student_norm=StudentRMSNorm(w,
 eps)`` (new) fuses the student's final RMSNorm in front of the loss:
-``student_hidden`` is then the norm's input; see
+``student_hidden`` is then the norm's input; ``logits_gemm="fp8"`` (new) runs
+the logits GEMM on gfx950's fp8 MFMA (e4m3 operands, one power-of-two scale
+per row; gradient GEMMs unchanged); see
 :mod:`orda_ce_kernel.ops.rmsnorm_prologue`.
 """
 from __future__ import annotations
@@ -112,6 +114,26 @@ class StudentRMSNorm:
 def _rmsnorm_torch(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """The reference producer's RMSNorm (``test/benchmark/src/core.py:13-14``)."""
     return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * weight
+
+
+def _e4m3_rows(x: torch.Tensor) -> torch.Tensor:
+    """Rows scaled by the power of two that puts their amax in (224, 448],
+    rounded to ``float8_e4m3fn`` and scaled back (the fp8 logits GEMM's
+    operands; no gradient)."""
+    x = x.detach()
+    amax = x.abs().amax(dim=1)
+    m, k = torch.frexp(torch.where(amax > 0, amax, torch.ones_like(amax)))
+    e = torch.where(amax > 0, k - 9 + (m > 0.875).to(k.dtype), torch.zeros_like(k))
+    sc = torch.ldexp(torch.ones_like(amax), e)[:, None]
+    return (x / sc).to(torch.float8_e4m3fn).to(x.dtype) * sc
+
+
+def _logits_fp8(h: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``h w^T`` with the value of the fp8 GEMM and the gradient of the exact
+    one (the kernels form the dlogits from the fp8 logits and run the
+    gradient GEMMs on the unrounded operands)."""
+    exact = h @ w.t()
+    return (_e4m3_rows(h) @ _e4m3_rows(w).t()).detach() + exact - exact.detach()
 
 
 # ── Config and output types (reference api.py:56-76) ────────────────────────
@@ -277,15 +299,18 @@ def _validate_teacher(*, mode, teacher_hidden, teacher_weight, teacher_logits, s
 
 # ── Unfused torch formulation (reference api.py:274-335) ────────────────────
 def _torch_reference(*, student_hidden, weight, labels, teacher, student_ce_weight, teacher_ce_weight, kl_weight,
-                     kl_temperature, ignore_index, reduction, divergence: Divergence | None = None):
+                     kl_temperature, ignore_index, reduction, divergence: Divergence | None = None,
+                     fp8_logits: bool = False):
     """Materialises full logits and lets autograd differentiate.  Used for
     ``backend="torch"`` and CPU tensors; the divergence term is computed even
-    when ``kl_weight == 0`` (reported, not weighted), as in the reference."""
+    when ``kl_weight == 0`` (reported, not weighted), as in the reference.
+    ``fp8_logits``: the student's (and a tied teacher's) logits take the fp8
+    GEMM's values (``_logits_fp8``)."""
     div = resolve_divergence(divergence)
     mode, t_hidden, t_weight, t_logits = _teacher_mode_and_tensors(teacher)
-    logits_s = student_hidden @ weight.t()
+    logits_s = _logits_fp8(student_hidden, weight) if fp8_logits else student_hidden @ weight.t()
     if mode == "tied":
-        logits_t = t_hidden @ weight.t()
+        logits_t = _logits_fp8(t_hidden, weight) if fp8_logits else t_hidden @ weight.t()
     elif mode == "separate":
         logits_t = t_hidden @ t_weight.t()
     elif t_logits is not None:
@@ -379,26 +404,39 @@ def _topk_loss(*, student_hidden, weight, labels, teacher: TopKTeacher, teacher_
     return DistillationLossOutput(*out)
 
 
-def _normed_loss(*, x, weight, labels, teacher, norm: StudentRMSNorm, kw: dict, profile, backend,
-                 resolved: KernelConfig, divergence: Divergence) -> DistillationLossOutput:
-    """``student_norm=`` given: the unfused torch formulation on CPU tensors
-    (or ``backend="torch"``), else the fused HIP prologue."""
-    if not isinstance(norm, StudentRMSNorm):
-        raise TypeError(f"student_norm must be a StudentRMSNorm, got {type(norm).__name__}")
-    nw = norm.weight
-    H = x.shape[1]
-    if not isinstance(nw, torch.Tensor) or nw.ndim != 1 or nw.shape[0] != H or not nw.is_floating_point():
-        raise ValueError(f"StudentRMSNorm.weight must be a floating tensor of shape ({H},), got "
-                         f"{getattr(nw, 'shape', None)}")
-    if nw.device != x.device:
-        raise ValueError("StudentRMSNorm.weight must be on the student's device")
-    eps = float(norm.eps)
-    if not (eps >= 0.0) or eps == float("inf"):
-        raise ValueError(f"StudentRMSNorm.eps must be finite and >= 0, got {norm.eps}")
+def _extended_loss(*, x, weight, labels, teacher, norm: StudentRMSNorm | None, fp8: bool, kw: dict, profile,
+                   backend, resolved: KernelConfig, divergence: Divergence) -> DistillationLossOutput:
+    """``student_norm=`` and/or ``logits_gemm="fp8"``: the unfused torch
+    formulation on CPU tensors (or ``backend="torch"``), else the extension
+    Function on the HIP path."""
+    nw, eps = None, 1e-6
+    if norm is not None:
+        if not isinstance(norm, StudentRMSNorm):
+            raise TypeError(f"student_norm must be a StudentRMSNorm, got {type(norm).__name__}")
+        nw = norm.weight
+        H = x.shape[1]
+        if not isinstance(nw, torch.Tensor) or nw.ndim != 1 or nw.shape[0] != H or not nw.is_floating_point():
+            raise ValueError(f"StudentRMSNorm.weight must be a floating tensor of shape ({H},), got "
+                             f"{getattr(nw, 'shape', None)}")
+        if nw.device != x.device:
+            raise ValueError("StudentRMSNorm.weight must be on the student's device")
+        eps = float(norm.eps)
+        if not (eps >= 0.0) or eps == float("inf"):
+            raise ValueError(f"StudentRMSNorm.eps must be finite and >= 0, got {norm.eps}")
+    if fp8 and isinstance(teacher, TopKTeacher):
+        raise ValueError("logits_gemm='fp8' does not support a TopKTeacher")
     if backend == "torch" or (backend == "auto" and x.device.type != "cuda"):
-        y = _rmsnorm_torch(x, nw, eps)
-        return distillation_loss(y, weight, labels, teacher, profile=profile, backend="torch", config=resolved,
-                                 divergence=divergence, **kw)
+        y = _rmsnorm_torch(x, nw, eps) if nw is not None else x
+        if not fp8:
+            return distillation_loss(y, weight, labels, teacher, profile=profile, backend="torch", config=resolved,
+                                     divergence=divergence, **kw)
+        mode = _teacher_mode_and_tensors(teacher)[0]
+        return _torch_reference(
+            student_hidden=y, weight=weight, labels=labels, teacher=teacher,
+            student_ce_weight=kw["student_ce_weight"], teacher_ce_weight=_resolve_teacher_ce_weight(
+                mode, kw["teacher_ce_weight"]), kl_weight=kw["kl_weight"], kl_temperature=kw["kl_temperature"],
+            ignore_index=kw["ignore_index"], reduction=kw["reduction"], divergence=divergence, fp8_logits=True,
+        )
     if not _supports_native(x):
         raise RuntimeError(
             f"backend={backend!r} on {x.device} tensors requires the HIP extension liborda_ce.so "
@@ -434,7 +472,7 @@ def _normed_loss(*, x, weight, labels, teacher, norm: StudentRMSNorm, kw: dict, 
         student_ce_weight=float(kw["student_ce_weight"]), teacher_ce_weight=float(w_t),
         kl_weight=float(kw["kl_weight"]), kl_temperature=float(kw["kl_temperature"]),
         ignore_index=int(kw["ignore_index"]), reduction=kw["reduction"], divergence=divergence,
-        token_chunk=int(cs), eps=eps,
+        token_chunk=int(cs), eps=eps, fp8_logits=fp8,
     )
     out = RMSNormPrologueFunction.apply(x, nw, weight, t_hidden, t_weight, labels, spec)
     return DistillationLossOutput(*out)
@@ -463,6 +501,7 @@ def distillation_loss(
     config: KernelConfig | None = None,
     divergence: str | Divergence = "forward_kl",
     student_norm: StudentRMSNorm | None = None,
+    logits_gemm: Literal["default", "fp8"] = "default",
 ) -> DistillationLossOutput:
     """Fused LM-head CE + distillation loss.
 
@@ -479,11 +518,14 @@ def distillation_loss(
         backend=backend, config=resolved,
     )
     div = resolve_divergence(divergence)
-    if student_norm is not None:
+    if logits_gemm not in ("default", "fp8"):
+        raise ValueError(f"logits_gemm must be 'default' or 'fp8', got {logits_gemm!r}")
+    if student_norm is not None or logits_gemm == "fp8":
         kw = dict(student_ce_weight=student_ce_weight, teacher_ce_weight=teacher_ce_weight, kl_weight=kl_w,
                   kl_temperature=kl_t, ignore_index=ignore_index, reduction=reduction)
-        return _normed_loss(x=student_hidden, weight=weight, labels=labels, teacher=teacher, norm=student_norm,
-                            kw=kw, profile=profile, backend=backend, resolved=resolved, divergence=div)
+        return _extended_loss(x=student_hidden, weight=weight, labels=labels, teacher=teacher, norm=student_norm,
+                              fp8=logits_gemm == "fp8", kw=kw, profile=profile, backend=backend, resolved=resolved,
+                              divergence=div)
     if isinstance(teacher, TopKTeacher):
         return _topk_loss(
             student_hidden=student_hidden, weight=weight, labels=labels, teacher=teacher,
@@ -557,8 +599,10 @@ class DistillationLoss(nn.Module):
         backend: Backend = "auto",
         config: KernelConfig | None = None,
         divergence: str | Divergence = "forward_kl",
+        logits_gemm: Literal["default", "fp8"] = "default",
     ) -> None:
         super().__init__()
+        self.logits_gemm = logits_gemm
         self.student_ce_weight = student_ce_weight
         self.teacher_ce_weight = teacher_ce_weight
         self.kl_weight = kl_weight
@@ -576,5 +620,5 @@ class DistillationLoss(nn.Module):
             student_ce_weight=self.student_ce_weight, teacher_ce_weight=self.teacher_ce_weight,
             kl_weight=self.kl_weight, kl_temperature=self.kl_temperature, ignore_index=self.ignore_index,
             reduction=self.reduction, profile=self.profile, backend=self.backend, config=self.config,
-            divergence=self.divergence, student_norm=student_norm,
+            divergence=self.divergence, student_norm=student_norm, logits_gemm=self.logits_gemm,
         )

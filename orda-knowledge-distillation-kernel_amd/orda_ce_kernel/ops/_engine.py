@@ -143,6 +143,8 @@ class FusedCall:
     student_norm_weight: torch.Tensor | None = None
     norm_eps: float = 1e-6
     need_grad_student_norm_weight: bool = False
+    # the scan's logits GEMM on e4m3 operands with per-row power-of-two scales
+    fp8_logits: bool = False
 
 
 def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None) -> _native.Problem:
@@ -163,6 +165,8 @@ def _problem(call: FusedCall, H: int, Ht: int, logits_dtype: torch.dtype | None)
         flags |= _native.FLAG["reduction_sum"]
     if call.grads_in_forward:
         flags |= _native.FLAG["grads_in_forward"]
+    if call.fp8_logits:
+        flags |= _native.FLAG["fp8_logits"]
     if call.student_norm_weight is not None:
         flags |= _native.FLAG["student_rmsnorm"]
         if call.need_grad_student_norm_weight:

@@ -1,4 +1,5 @@
-"""The student's final RMSNorm fused in front of the loss.
+"""The extension entry: the student's final RMSNorm fused in front of the
+loss, and/or the scan's logits GEMM on fp8 operands.
 
 The reference's producer normalises the last hidden states before the LM
 head, ``y = x * rsqrt(mean(x^2) + eps) * w`` (reference
@@ -19,6 +20,13 @@ token chunk of the gradients-in-forward schedule:
 Every teacher mode and divergence works unchanged (only the student's rows
 are transformed).  No counterpart in the reference's loss API: an extension
 (``distillation_loss(..., student_norm=StudentRMSNorm(weight, eps))``).
+
+``logits_gemm="fp8"`` (``ORDA_FP8_LOGITS``): the scan's logits GEMM takes W
+and the chunk's hidden rows rounded to OCP e4m3 with one power-of-two scale
+per row (``v_mfma_scale_f32_32x32x64_f8f6f4`` applies the scales), so the
+losses, softmax statistics and dlogits come from those logits; the gradient
+GEMMs keep the compute dtype.  With or without the norm; ``norm_weight`` may
+be None.
 """
 from __future__ import annotations
 
@@ -50,6 +58,7 @@ class NormedCall:
     divergence: object
     token_chunk: int
     eps: float
+    fp8_logits: bool = False
 
 
 class RMSNormPrologueFunction(torch.autograd.Function):
@@ -59,12 +68,13 @@ class RMSNormPrologueFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, norm_weight, weight, teacher_hidden, teacher_weight, labels, spec: NormedCall):
-        require_native("the fused RMSNorm prologue")
+        require_native("the fused RMSNorm prologue / fp8 logits")
         trainable_teacher = spec.mode in ("tied", "separate")
         ht_grad = trainable_teacher and teacher_hidden is not None and teacher_hidden.requires_grad
         wt_grad = spec.mode == "separate" and teacher_weight is not None and teacher_weight.requires_grad
-        ctx.compute_grad = x.requires_grad or norm_weight.requires_grad or weight.requires_grad or ht_grad or wt_grad
-        ctx.dtypes = (x.dtype, norm_weight.dtype, weight.dtype,
+        nw_grad = norm_weight is not None and norm_weight.requires_grad
+        ctx.compute_grad = x.requires_grad or nw_grad or weight.requires_grad or ht_grad or wt_grad
+        ctx.dtypes = (x.dtype, None if norm_weight is None else norm_weight.dtype, weight.dtype,
                       None if teacher_hidden is None else teacher_hidden.dtype,
                       None if teacher_weight is None else teacher_weight.dtype)
         ops = [t for t in (weight, x, teacher_hidden, teacher_weight) if t is not None]
@@ -101,9 +111,10 @@ class RMSNormPrologueFunction(torch.autograd.Function):
             topk_indices=None if spec.topk_indices is None else spec.topk_indices.contiguous().to(torch.int64),
             topk_logprobs=None if spec.topk_logprobs is None
             else spec.topk_logprobs.detach().contiguous().to(torch.float32),
-            student_norm_weight=cast(norm_weight.detach()),
+            student_norm_weight=None if norm_weight is None else cast(norm_weight.detach()),
             norm_eps=float(spec.eps),
-            need_grad_student_norm_weight=norm_weight.requires_grad,
+            need_grad_student_norm_weight=nw_grad,
+            fp8_logits=bool(spec.fp8_logits),
         )
         loss, ce_s, ce_t, kl = fused_forward(ctx, call)
         ctx.mark_non_differentiable(ce_s, ce_t, kl)
