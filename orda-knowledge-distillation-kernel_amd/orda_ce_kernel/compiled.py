@@ -16,7 +16,10 @@ so a compiled training step traces through it in one graph:
 
 Differences from the drop-in entry: no OOM retry with more chunks (the chunk
 is the reference's auto chunk, or ``chunk_size``), and the compute dtype comes
-from the inputs, not from an enclosing autocast region.
+from the inputs, not from an enclosing autocast region.  The drop-in's
+extensions come along: ``TopKTeacher``, ``student_norm=StudentRMSNorm(w,
+eps)`` (the norm weight is an op input with its own gradient) and
+``logits_gemm="fp8"``.
 """
 from __future__ import annotations
 
@@ -25,12 +28,14 @@ from typing import Optional
 
 import torch
 
-from .api import (DistillationLossOutput, _resolve_teacher_ce_weight, _teacher_mode_and_tensors, _validate_teacher)
+from .api import (DistillationLossOutput, StudentRMSNorm, TopKTeacher, _resolve_teacher_ce_weight,
+                  _teacher_mode_and_tensors, _validate_teacher)
 from .divergences import Divergence, resolve_divergence
 
 __all__ = ["distillation_loss"]
 
-_GRAD_SLOTS = 4  # student hidden, weight, teacher hidden, teacher weight
+_GRAD_SLOTS = 5  # student hidden, weight, teacher hidden, teacher weight, student norm weight
+_TENSOR_INPUTS = 9  # student hidden, weight, labels, teacher hidden / weight / logits, top-k ids / log-probs, norm weight
 
 
 def _mode_name(mode: str, teacher_logits) -> str:
@@ -60,6 +65,9 @@ def fused_loss(
     teacher_hidden: Optional[torch.Tensor],
     teacher_weight: Optional[torch.Tensor],
     teacher_logits: Optional[torch.Tensor],
+    topk_indices: Optional[torch.Tensor],
+    topk_logprobs: Optional[torch.Tensor],
+    norm_weight: Optional[torch.Tensor],
     mode: str,
     student_ce_weight: float,
     teacher_ce_weight: float,
@@ -72,10 +80,13 @@ def fused_loss(
     div_beta: float,
     need_grads: list[bool],
     chunk_size: int,
+    norm_eps: float,
+    fp8_logits: bool,
 ) -> list[torch.Tensor]:
     """Loss components and gradients of one fused evaluation (see module doc).
     ``div_alpha`` / ``div_beta`` NaN = the divergence's default;
-    ``chunk_size`` 0 = the reference's auto chunk."""
+    ``chunk_size`` 0 = the reference's auto chunk; ``need_grads``: student
+    hidden, weight, teacher hidden, teacher weight, norm weight."""
     from .ops._engine import FusedCall, run_fused_call, token_chunk_for
     from .utils.resolver import resolve_chunk_size
 
@@ -86,14 +97,15 @@ def fused_loss(
     cs = chunk_size if chunk_size > 0 else resolve_chunk_size(BT, None, V=V)[0]
     nan_none = lambda x: None if math.isnan(x) else float(x)  # noqa: E731
     div = resolve_divergence(Divergence(divergence, nan_none(div_alpha), nan_none(div_beta)))
-    grads_teacher = mode in ("tied", "separate") and teacher_ce_weight != 0.0
-    need = [bool(need_grads[0]), bool(need_grads[1]), bool(need_grads[2]) and grads_teacher,
-            bool(need_grads[3]) and grads_teacher and mode == "separate"]
+    need = _need(mode, teacher_ce_weight, need_grads, norm_weight)
     cast = lambda t: None if t is None else t.detach().contiguous().to(dtype)  # noqa: E731
+    extended = mode == "topk" or norm_weight is not None or fp8_logits
     lt = None
     if teacher_logits is not None:
         lt = teacher_logits.detach()
-        if lt.dtype != dtype and lt.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        if extended and lt.dtype != dtype:
+            lt = lt.to(dtype)  # (as the reference casts them, ops/precomputed_teacher.py:340-348)
+        elif lt.dtype != dtype and lt.dtype not in (torch.bfloat16, torch.float16, torch.float32):
             lt = lt.float()
     call = FusedCall(
         mode=mode, student_hidden=cast(student_hidden), weight=cast(weight), labels=labels.contiguous(),
@@ -104,9 +116,14 @@ def fused_loss(
         need_grad_student_hidden=need[0], need_grad_weight=need[1], need_grad_teacher_hidden=need[2],
         need_grad_teacher_weight=need[3],
         # gradients inside forward; given logits of another dtype take the
-        # two-phase schedule, which computes no gradients here
-        grads_in_forward=any(need) and (lt is None or lt.dtype == dtype),
+        # two-phase schedule, which computes no gradients here (the
+        # extensions always run the gradients-in-forward schedule)
+        grads_in_forward=extended or (any(need) and (lt is None or lt.dtype == dtype)),
         token_chunk=token_chunk_for(cs),
+        topk_indices=None if topk_indices is None else topk_indices.contiguous().to(torch.int64),
+        topk_logprobs=None if topk_logprobs is None else topk_logprobs.detach().contiguous().to(torch.float32),
+        student_norm_weight=cast(norm_weight), norm_eps=float(norm_eps), need_grad_student_norm_weight=need[4],
+        fp8_logits=bool(fp8_logits),
     )
     if any(need) and not call.grads_in_forward:
         raise ValueError("orda_ce::fused_loss: precomputed teacher logits must be in the compute dtype "
@@ -115,25 +132,33 @@ def fused_loss(
     widths = (H, H, H if mode == "tied" else (teacher_hidden.shape[1] if teacher_hidden is not None else 0),
               teacher_hidden.shape[1] if teacher_hidden is not None else 0)
     res = list(outs)
-    for g, width in zip(grads, widths):
+    for g, width in zip(grads[:4], widths):
         if g is None:
             res.append(student_hidden.new_empty((0,), dtype=dtype))
         else:
             res.append(g[:, :width] if g.shape[1] != width else g)
+    g_nw = grads[4]
+    res.append(student_hidden.new_empty((0,), dtype=dtype) if g_nw is None else g_nw[:H])
     return res
 
 
+def _need(mode, teacher_ce_weight, need_grads, norm_weight):
+    grads_teacher = mode in ("tied", "separate") and teacher_ce_weight != 0.0
+    return [bool(need_grads[0]), bool(need_grads[1]), bool(need_grads[2]) and grads_teacher,
+            bool(need_grads[3]) and grads_teacher and mode == "separate",
+            bool(need_grads[4]) and norm_weight is not None]
+
+
 @fused_loss.register_fake
-def _fused_loss_fake(student_hidden, weight, labels, teacher_hidden, teacher_weight, teacher_logits, mode,
-                     student_ce_weight, teacher_ce_weight, kl_weight, kl_temperature, ignore_index, reduction,
-                     divergence, div_alpha, div_beta, need_grads, chunk_size):
+def _fused_loss_fake(student_hidden, weight, labels, teacher_hidden, teacher_weight, teacher_logits, topk_indices,
+                     topk_logprobs, norm_weight, mode, student_ce_weight, teacher_ce_weight, kl_weight,
+                     kl_temperature, ignore_index, reduction, divergence, div_alpha, div_beta, need_grads,
+                     chunk_size, norm_eps, fp8_logits):
     use_teacher = kl_weight != 0.0 or teacher_ce_weight != 0.0
     dtype = _compute_dtype(student_hidden, weight, teacher_hidden, teacher_weight, teacher_logits, use_teacher)
-    grads_teacher = mode in ("tied", "separate") and teacher_ce_weight != 0.0
-    need = [need_grads[0], need_grads[1], need_grads[2] and grads_teacher,
-            need_grads[3] and grads_teacher and mode == "separate"]
+    need = _need(mode, teacher_ce_weight, need_grads, norm_weight)
     res = [student_hidden.new_empty((), dtype=torch.float32) for _ in range(4)]
-    for flag, ref in zip(need, (student_hidden, weight, teacher_hidden, teacher_weight)):
+    for flag, ref in zip(need, (student_hidden, weight, teacher_hidden, teacher_weight, norm_weight)):
         res.append(ref.new_empty(ref.shape, dtype=dtype) if (flag and ref is not None)
                    else student_hidden.new_empty((0,), dtype=dtype))
     return res
@@ -141,7 +166,7 @@ def _fused_loss_fake(student_hidden, weight, labels, teacher_hidden, teacher_wei
 
 def _setup_context(ctx, inputs, output):
     ctx.save_for_backward(*output[4:4 + _GRAD_SLOTS])
-    ctx.input_dtypes = tuple(None if inputs[i] is None else inputs[i].dtype for i in (0, 1, 3, 4))
+    ctx.input_dtypes = tuple(None if inputs[i] is None else inputs[i].dtype for i in (0, 1, 3, 4, 8))
 
 
 def _backward(ctx, grads):
@@ -155,9 +180,10 @@ def _backward(ctx, grads):
             # (grad_output is applied in the gradient's dtype: no fp32 copy of
             # a [V x H] gradient)
             res.append((g * g_loss).to(dt))
-    d_hs, d_w, d_ht, d_wt = res
-    # one gradient per op input (None for labels, logits and the scalars)
-    return (d_hs, d_w, None, d_ht, d_wt) + (None,) * 13
+    d_hs, d_w, d_ht, d_wt, d_nw = res
+    # one gradient per op input (None for labels, logits, top-k pairs and the
+    # scalars)
+    return (d_hs, d_w, None, d_ht, d_wt, None, None, None, d_nw) + (None,) * 14
 
 
 fused_loss.register_autograd(_backward, setup_context=_setup_context)
@@ -177,6 +203,8 @@ def distillation_loss(
     reduction: str = "mean",
     divergence: str | Divergence = "forward_kl",
     chunk_size: int | None = None,
+    student_norm: StudentRMSNorm | None = None,
+    logits_gemm: str = "default",
 ) -> DistillationLossOutput:
     """:func:`orda_ce_kernel.distillation_loss` (same loss, arguments and
     defaults; ``chunk_size`` as ``KernelConfig.chunk_size``) as custom ops
@@ -189,20 +217,47 @@ def distillation_loss(
         raise ValueError("loss weights must be >= 0.0")
     if labels.dtype != torch.long:
         raise ValueError(f"labels must have dtype torch.long, got {labels.dtype}")
-    mode, t_hidden, t_weight, t_logits = _teacher_mode_and_tensors(teacher)
-    _validate_teacher(mode=mode, teacher_hidden=t_hidden, teacher_weight=t_weight, teacher_logits=t_logits,
-                      student_hidden=student_hidden, weight=weight)
-    w_t = _resolve_teacher_ce_weight(mode, teacher_ce_weight)
-    if mode == "precomputed" and w_t != 0.0:
-        raise ValueError("a PrecomputedTeacher has no gradient path: teacher_ce_weight must be 0.0")
+    if logits_gemm not in ("default", "fp8"):
+        raise ValueError(f"logits_gemm must be 'default' or 'fp8', got {logits_gemm!r}")
     div = resolve_divergence(divergence)
+    tk_i = tk_lp = None
+    if isinstance(teacher, TopKTeacher):
+        from .ops.topk_teacher import check_topk_teacher
+
+        if teacher_ce_weight not in (None, 0.0):
+            raise ValueError("a TopKTeacher has no teacher CE: teacher_ce_weight must be None or 0.0")
+        if logits_gemm == "fp8":
+            raise ValueError("logits_gemm='fp8' does not support a TopKTeacher")
+        check_topk_teacher(teacher.indices, teacher.logprobs, student_hidden.shape[0], weight.shape[0], div)
+        mode, t_hidden, t_weight, t_logits, w_t = "topk", None, None, None, 0.0
+        tk_i, tk_lp = teacher.indices, teacher.logprobs
+    else:
+        mode, t_hidden, t_weight, t_logits = _teacher_mode_and_tensors(teacher)
+        _validate_teacher(mode=mode, teacher_hidden=t_hidden, teacher_weight=t_weight, teacher_logits=t_logits,
+                          student_hidden=student_hidden, weight=weight)
+        w_t = _resolve_teacher_ce_weight(mode, teacher_ce_weight)
+        if mode == "precomputed" and w_t != 0.0:
+            raise ValueError("a PrecomputedTeacher has no gradient path: teacher_ce_weight must be 0.0")
+        mode = _mode_name(mode, t_logits)
+    nw, eps = None, 1e-6
+    if student_norm is not None:
+        if not isinstance(student_norm, StudentRMSNorm):
+            raise TypeError(f"student_norm must be a StudentRMSNorm, got {type(student_norm).__name__}")
+        nw, eps = student_norm.weight, float(student_norm.eps)
+        if nw.ndim != 1 or nw.shape[0] != student_hidden.shape[1]:
+            raise ValueError(f"StudentRMSNorm.weight must have shape ({student_hidden.shape[1]},), got "
+                             f"{tuple(nw.shape)}")
+        if not (eps >= 0.0) or eps == float("inf"):
+            raise ValueError(f"StudentRMSNorm.eps must be finite and >= 0, got {student_norm.eps}")
     need = [student_hidden.requires_grad, weight.requires_grad,
-            t_hidden is not None and t_hidden.requires_grad and mode != "precomputed",
-            t_weight is not None and t_weight.requires_grad and mode == "separate"]
+            t_hidden is not None and t_hidden.requires_grad and mode in ("tied", "separate"),
+            t_weight is not None and t_weight.requires_grad and mode == "separate",
+            nw is not None and nw.requires_grad]
     outs = fused_loss(
-        student_hidden, weight, labels, t_hidden, t_weight, t_logits, _mode_name(mode, t_logits),
+        student_hidden, weight, labels, t_hidden, t_weight, t_logits, tk_i, tk_lp, nw, mode,
         float(student_ce_weight), float(w_t), float(kl_weight), float(kl_temperature), int(ignore_index),
         reduction, div.name, float("nan") if div.alpha is None else float(div.alpha),
-        float("nan") if div.beta is None else float(div.beta), need, int(chunk_size or 0),
+        float("nan") if div.beta is None else float(div.beta), need, int(chunk_size or 0), eps,
+        logits_gemm == "fp8",
     )
     return DistillationLossOutput(outs[0], outs[1].detach(), outs[2].detach(), outs[3].detach())

@@ -64,3 +64,39 @@ def test_compiled_entry_validates_like_the_drop_in():
         compiled.distillation_loss(hs, W, y, TiedTeacher(_meta(7, 16)))
     with pytest.raises(ValueError, match="teacher_ce_weight"):
         compiled.distillation_loss(hs, W, y, PrecomputedTeacher(logits=_meta(8, 50)), teacher_ce_weight=1.0)
+
+
+@pytest.mark.parametrize("ext", ["topk", "norm", "fp8", "norm_topk"])
+def test_compiled_entry_traces_the_extensions(ext):
+    """The top-k teacher, the fused RMSNorm (its weight gets a gradient) and
+    the fp8 logits GEMM trace in one graph too."""
+    from orda_ce_kernel import StudentRMSNorm, TopKTeacher
+
+    torch._dynamo.reset()
+    N, H, V, k = 48, 256, 100, 8
+    hs, W = _meta(N, H, grad=True), _meta(V, H, grad=True)
+    y = torch.empty(N, dtype=torch.long, device="meta")
+    nw = _meta(H, grad=True)
+    if "topk" in ext:
+        idx = torch.empty(N, k, dtype=torch.long, device="meta")
+        lp = torch.empty(N, k, dtype=torch.float32, device="meta")
+        make = lambda: TopKTeacher(idx, lp)  # noqa: E731
+    else:
+        ht = _meta(N, H, grad=True)
+        make = lambda: TiedTeacher(ht)  # noqa: E731
+    kw = {}
+    if "norm" in ext:
+        kw["student_norm"] = StudentRMSNorm(nw, eps=1e-5)
+    if ext == "fp8":
+        kw["logits_gemm"] = "fp8"
+
+    def step(hs, W, y):
+        return compiled.distillation_loss(hs, W, y, make(), kl_weight=0.5, kl_temperature=2.0, **kw).loss
+
+    loss = torch.compile(step, fullgraph=True, backend="aot_eager")(hs, W, y)
+    loss.backward()
+    assert hs.grad.shape == (N, H) and W.grad.shape == (V, H)
+    if "norm" in ext:
+        assert nw.grad.shape == (H,)
+    else:
+        assert nw.grad is None
