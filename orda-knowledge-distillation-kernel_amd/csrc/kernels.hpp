@@ -126,8 +126,8 @@ struct AccPair4 {  // ring engine, the lane's token j: acc[mb][j] student, acc[m
 
 // Phase 0: online softmax statistics of this lane's token over its 64
 // vocabulary rows of the tile.  Template flags remove work that the problem
-// does not need.
-template <bool HAS_T, int FAM, bool T1, bool MASK, class AP>
+// does not need (NPOW: the power family's terms, 1 or up to 3, P.npow).
+template <bool HAS_T, int FAM, bool T1, bool MASK, class AP, int NPOW = 3>
 __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0, int64_t vlimit,
                                           const FusedParams& P) {
   const float invT = P.invT;
@@ -144,8 +144,8 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
         tmt = fmaxf(tmt, xt);
         if (FAM == FAM_POW) {
           tmu0 = fmaxf(tmu0, P.pa[0] * xt + P.pb[0] * xs);
-          if (P.npow > 1) tmu1 = fmaxf(tmu1, P.pa[1] * xt + P.pb[1] * xs);
-          if (P.npow > 2) tmu2 = fmaxf(tmu2, P.pa[2] * xt + P.pb[2] * xs);
+          if (NPOW > 1 && P.npow > 1) tmu1 = fmaxf(tmu1, P.pa[1] * xt + P.pb[1] * xs);
+          if (NPOW > 2 && P.npow > 2) tmu2 = fmaxf(tmu2, P.pa[2] * xt + P.pb[2] * xs);
         }
       }
     }
@@ -182,12 +182,12 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
     nmu0 = fmaxf(S.x[0], tmu0 * invT);
     S.x[1] *= fexp(S.x[0] - nmu0);
     S.x[0] = nmu0;
-    if (P.npow > 1) {
+    if (NPOW > 1 && P.npow > 1) {
       nmu1 = fmaxf(S.x[2], tmu1 * invT);
       S.x[3] *= fexp(S.x[2] - nmu1);
       S.x[2] = nmu1;
     }
-    if (P.npow > 2) {
+    if (NPOW > 2 && P.npow > 2) {
       nmu2 = fmaxf(S.x[4], tmu2 * invT);
       S.x[5] *= fexp(S.x[4] - nmu2);
       S.x[4] = nmu2;
@@ -226,8 +226,8 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
         }
         if (FAM == FAM_POW) {
           S.x[1] += fexp((P.pa[0] * xt + P.pb[0] * xs) * invT - nmu0);
-          if (P.npow > 1) S.x[3] += fexp((P.pa[1] * xt + P.pb[1] * xs) * invT - nmu1);
-          if (P.npow > 2) S.x[5] += fexp((P.pa[2] * xt + P.pb[2] * xs) * invT - nmu2);
+          if (NPOW > 1 && P.npow > 1) S.x[3] += fexp((P.pa[1] * xt + P.pb[1] * xs) * invT - nmu1);
+          if (NPOW > 2 && P.npow > 2) S.x[5] += fexp((P.pa[2] * xt + P.pb[2] * xs) * invT - nmu2);
         }
       }
     }
@@ -316,7 +316,8 @@ enum ScanVariant {
   SV_SKEW_F = 7,
   SV_SKEW_R = 8,
   SV_TVD = 9,
-  SV_STUDENT_T = 10  // no teacher term, the student also at T != 1 (top-k teachers)
+  SV_STUDENT_T = 10,  // no teacher term, the student also at T != 1 (top-k teachers)
+  SV_POW1 = 11        // power-sum divergences with one power term (P.npow == 1)
 };
 // Second-pass variants (row sums given the first pass's normalisers).
 constexpr bool sv_phase1(int sv) { return sv >= SV_JSD && sv <= SV_TVD; }
@@ -345,6 +346,9 @@ __device__ __forceinline__ void scan_variant(RowState& S, const AP& acc, int vla
   } else if constexpr (SV == SV_POW) {
     if (full) scan_tile<true, FAM_POW, false, false>(S, acc, vlane0, vlimit, P);
     else scan_tile<true, FAM_POW, false, true>(S, acc, vlane0, vlimit, P);
+  } else if constexpr (SV == SV_POW1) {
+    if (full) scan_tile<true, FAM_POW, false, false, AP, 1>(S, acc, vlane0, vlimit, P);
+    else scan_tile<true, FAM_POW, false, true, AP, 1>(S, acc, vlane0, vlimit, P);
   } else {
     constexpr int DIV = SV == SV_JSD ? DIV_JSD : SV == SV_SKEW_F ? DIV_SKEW_F : SV == SV_SKEW_R ? DIV_SKEW_R : DIV_TVD;
     if (full) rowsum_tile<DIV, false>(S, acc, vlane0, vlimit, lse_sT, lse_tT, P);
@@ -1929,7 +1933,7 @@ inline int scan_variant_of(const FusedParams& P) {
   }
   if (P.tsrc == TSRC_NONE) return P.t_is_one ? SV_STUDENT : SV_STUDENT_T;
   if (P.fam == FAM_LIN) return P.t_is_one ? SV_LIN_T1 : SV_LIN;
-  if (P.fam == FAM_POW) return SV_POW;
+  if (P.fam == FAM_POW) return P.npow == 1 ? SV_POW1 : SV_POW;
   return P.t_is_one ? SV_TCE_T1 : SV_TCE;
 }
 
@@ -1967,6 +1971,7 @@ inline bool scan_on_ring(const FusedParams& P) {
       ORDA_SCAN_CASE(T, SV_LIN_T1)                                                   \
       ORDA_SCAN_CASE(T, SV_LIN)                                                      \
       ORDA_SCAN_CASE(T, SV_POW)                                                      \
+      ORDA_SCAN_CASE(T, SV_POW1)                                                     \
       ORDA_SCAN_CASE(T, SV_JSD)                                                      \
       ORDA_SCAN_CASE(T, SV_SKEW_F)                                                   \
       ORDA_SCAN_CASE(T, SV_SKEW_R)                                                   \
@@ -2261,7 +2266,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
         break;                                                                                   \
       }                                                                                          \
       if (P.tsrc == TSRC_L || P.tsrc == TSRC_MEM_RING) {                                         \
-        if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T || SV == SV_POW)                    \
+        if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T || SV == SV_POW || SV == SV_POW1) \
           return hipErrorInvalidValue;                                                           \
         else if (P.tsrc == TSRC_L)                                                               \
           hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_L>), dim3(grid), dim3(kThreads4), 0, s, P); \
@@ -2290,6 +2295,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
       ORDA_SCANST_CASE(T, SV_LIN_T1)                                                       \
       ORDA_SCANST_CASE(T, SV_LIN)                                                          \
       ORDA_SCANST_CASE(T, SV_POW)                                                          \
+      ORDA_SCANST_CASE(T, SV_POW1)                                                         \
       default: return hipErrorInvalidValue;                                                \
     }                                                                                      \
     return hipGetLastError();                                                              \
@@ -2305,7 +2311,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
       else                                                                                       \
         return hipErrorInvalidValue;                                                             \
     } else if (P.tsrc == TSRC_MEM_RING) {                                                        \
-      if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T || SV == SV_POW)                      \
+      if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T || SV == SV_POW || SV == SV_POW1)      \
         return hipErrorInvalidValue;                                                             \
       else                                                                                       \
         hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_MEM, true>), dim3(grid), dim3(kThreads4), 0, s, P); \
@@ -2333,6 +2339,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
       ORDA_SCANF8_CASE(T, SV_LIN_T1)                                                       \
       ORDA_SCANF8_CASE(T, SV_LIN)                                                          \
       ORDA_SCANF8_CASE(T, SV_POW)                                                          \
+      ORDA_SCANF8_CASE(T, SV_POW1)                                                         \
       default: return hipErrorInvalidValue;                                                \
     }                                                                                      \
     return hipGetLastError();                                                              \
