@@ -33,6 +33,13 @@ int fail(int code, const char* fmt, ...) {
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// The mixture weight of the two-pass divergences (beta for JSD, alpha for
+// the skew KLs) and 1 - weight, formed in double.
+inline void set_mix(float& w, float& w1, const orda_problem_t* p) {
+  const double m = p->divergence == ORDA_DIV_JSD ? (double)p->div_beta : (double)p->div_alpha;
+  w = (float)m;
+  w1 = (float)(1.0 - m);
+}
 inline int64_t dtype_bytes(int32_t d) { return d == ORDA_F32 ? 4 : 2; }
 
 constexpr size_t kAlign = 256;
@@ -521,8 +528,7 @@ int run_forward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t
   F.div = pl.div; F.fam = pl.fam; F.t_is_one = pl.t1; F.tgrad = 0;
   F.temperature = p->temperature; F.invT = 1.0f / p->temperature;
   F.alpha = p->div_alpha; F.beta = p->div_beta;
-  F.log_alpha = std::log(p->div_alpha); F.log_1m_alpha = std::log1p(-p->div_alpha);
-  F.log_beta = std::log(p->div_beta); F.log_1m_beta = std::log1p(-p->div_beta);
+  set_mix(F.mix_w, F.mix_w1, p);
   for (int i = 0; i < 3; ++i) { F.pa[i] = pl.pa[i]; F.pb[i] = pl.pb[i]; }
   F.npow = pl.npow;
   F.phase = 0; F.n_ttiles = pl.n_ttiles; F.n_vranges = pl.n_vranges;
@@ -630,8 +636,7 @@ int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* 
   F.div = pl.div; F.fam = pl.fam; F.t_is_one = pl.t1; F.tgrad = pl.bwd_teacher;
   F.temperature = p->temperature; F.invT = 1.0f / p->temperature;
   F.alpha = p->div_alpha; F.beta = p->div_beta;
-  F.log_alpha = std::log(p->div_alpha); F.log_1m_alpha = std::log1p(-p->div_alpha);
-  F.log_beta = std::log(p->div_beta); F.log_1m_beta = std::log1p(-p->div_beta);
+  set_mix(F.mix_w, F.mix_w1, p);
   F.n_ttiles = pl.n_ttiles; F.rowp = rowp;
   F.w_s = p->student_ce_weight; F.w_t = p->teacher_ce_weight; F.w_kl = pl.div_on ? p->kl_weight : 0.f;
   F.grad_output = t->grad_output; F.mean_scale = scal;
@@ -811,8 +816,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     F.div = pl.div; F.fam = pl.topk ? FAM_NONE : pl.fam; F.t_is_one = pl.t1; F.tgrad = 0;
     F.temperature = p->temperature; F.invT = 1.0f / p->temperature;
     F.alpha = p->div_alpha; F.beta = p->div_beta;
-    F.log_alpha = std::log(p->div_alpha); F.log_1m_alpha = std::log1p(-p->div_alpha);
-    F.log_beta = std::log(p->div_beta); F.log_1m_beta = std::log1p(-p->div_beta);
+    set_mix(F.mix_w, F.mix_w1, p);
     for (int i = 0; i < 3; ++i) { F.pa[i] = pl.pa[i]; F.pb[i] = pl.pb[i]; }
     F.npow = pl.npow;
     F.phase = 0; F.n_ttiles = (int)cdiv(nc, 128); F.n_vranges = pl.f_nvr;
@@ -890,14 +894,17 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       // merge of their partial states into D and the dlogits row constants
       TwoParams Q{};
       Q.L = L; Q.ldL = ldL; Q.tcol = nP; Q.rowp = rowp; Q.partial = part;
-      Q.N = nc; Q.V = V; Q.rows_per_range = (int64_t)pl.f_tpr * 256; Q.n_ranges = pl.f_nvr; Q.div = pl.div;
+      // vocabulary ranges of 64-row multiples, as many as the scan's partial
+      // states hold as dense pairs (f_nvr * kNStat / 2)
+      Q.N = nc; Q.V = V; Q.div = pl.div;
+      Q.rows_per_range = round_up(cdiv(V, (int64_t)pl.f_nvr * (kNStat / 2)), 64);
+      Q.n_ranges = (int)cdiv(V, Q.rows_per_range);
       Q.invT = F.invT;
-      Q.lw = pl.div == DIV_JSD ? F.log_beta : F.log_alpha;
-      Q.l1mw = pl.div == DIV_JSD ? F.log_1m_beta : F.log_1m_alpha;
+      Q.mix_w = F.mix_w; Q.mix_w1 = F.mix_w1;
       Q.Ltm = pl.f_tmem ? Ltc : nullptr;
       Q.ldtm = V;
       { Timed tm_(ORDA_K_DLOGITS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_two<T>(Q, s)); }
-      M.phase = 1;
+      M.phase = 1; M.two_dense = 1; M.n_vranges = Q.n_ranges;
       { Timed tm_(ORDA_K_ROWS, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_merge(M, s)); }
     }
 

@@ -9,8 +9,16 @@
 
 namespace orda {
 
+constexpr float kMinNormal = 1.17549435e-38f;  // 2^-126
+
+// 1 / x on the hardware reciprocal (v_rcp_f32); x a normal float.
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
 // Per-element divergence gradient dD/dz_s (z = x/T) given normalised log
 // probabilities at temperature T and the row constants c[] from the merge.
+// The two-pass divergences form their mixture m in linear space from the
+// probabilities (log m = log(w p + (1 - w) q)); an element whose mixture
+// underflows (both probabilities below 2^-126) has a zero gradient.
 template <int DIV>
 __device__ __forceinline__ float div_grad(float lps, float lpt, float psT, float ptT,
                                           const float* c, float alpha, float beta) {
@@ -37,14 +45,18 @@ __device__ __forceinline__ float div_grad(float lps, float lpt, float psT, float
     const float q3 = fexp((alpha + beta) * lps);
     return -((q1 - psT * fexp(c[0])) - (q3 - psT * fexp(c[2]))) / alpha;
   } else if constexpr (DIV == DIV_JSD) {
-    const float lm = logaddexp(flog(beta) + lpt, flog(1.0f - beta) + lps);
-    return (1.0f - beta) * psT * (lps - lm - c[1]);
+    const float m = beta * ptT + (1.0f - beta) * psT;
+    const bool ok = m >= kMinNormal;
+    return ok ? (1.0f - beta) * psT * (lps - flog(ok ? m : 1.0f) - c[1]) : 0.0f;
   } else if constexpr (DIV == DIV_SKEW_F) {
-    const float lm = logaddexp(flog(alpha) + lpt, flog(1.0f - alpha) + lps);
-    return -(1.0f - alpha) * psT * (fexp(lpt - lm) - c[1]);
+    const float m = alpha * ptT + (1.0f - alpha) * psT;
+    const bool ok = m >= kMinNormal;
+    return ok ? -(1.0f - alpha) * psT * (ptT * frcp(ok ? m : 1.0f) - c[1]) : 0.0f;
   } else if constexpr (DIV == DIV_SKEW_R) {
-    const float lm = logaddexp(flog(alpha) + lps, flog(1.0f - alpha) + lpt);
-    return psT * (lps - lm - alpha * fexp(lps - lm) - c[0] + alpha * c[1]);
+    const float m = alpha * psT + (1.0f - alpha) * ptT;
+    const bool ok = m >= kMinNormal;
+    const float mm = ok ? m : 1.0f;
+    return ok ? psT * (lps - flog(mm) - alpha * psT * frcp(mm) - c[0] + alpha * c[1]) : 0.0f;
   } else {  // DIV_TVD
     const float sg = (psT > ptT) ? 1.0f : ((psT < ptT) ? -1.0f : 0.0f);
     return 0.5f * psT * (sg - c[1]);
@@ -234,33 +246,36 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
   if (HAS_T && FAM == FAM_LIN) S.x[2] += lx2 * kLn2;
 }
 
-// Phase 1 (two-pass divergences): sums of terms of the normalised
-// probabilities, given the row log-normalisers from phase 0.
-// One vocabulary row's terms of the two-pass divergences' row sums (x0, x1),
-// from normalised log-probabilities at temperature T.  lw, l1mw: log w and
-// log(1 - w) of the mixture weight (beta for JSD, alpha for the skew KLs).
+// Phase-1 terms of the two-pass divergences for one vocabulary element,
+// from normalised log-probabilities at temperature T.  w, w1: the mixture
+// weight (beta for JSD, alpha for the skew KLs) and 1 - w.  The mixture m is
+// formed in linear space (one log instead of a log-sum-exp); an element whose
+// mixture underflows (both probabilities below 2^-126) adds nothing.
 //   JSD:    x0 += p_t (l_t - l_m), x1 += p_s (l_s - l_m), m = b p_t + (1-b) p_s
 //   skew-F: x0 += p_t (l_t - l_m), x1 += p_s p_t / m,     m = a p_t + (1-a) p_s
 //   skew-R: x0 += p_s (l_s - l_m), x1 += p_s p_s / m,     m = a p_s + (1-a) p_t
 //   TVD:    x0 += |p_t - p_s|,     x1 += p_s sign(p_s - p_t)
 template <int DIV>
-__device__ __forceinline__ void two_term(float lps, float lpt, float lw, float l1mw, float& s0, float& s1) {
+__device__ __forceinline__ void two_term(float lps, float lpt, float w, float w1, float& s0, float& s1) {
   const float ps = fexp(lps), pt = fexp(lpt);
-  if constexpr (DIV == DIV_JSD) {
-    const float lm = logaddexp(lw + lpt, l1mw + lps);
-    s0 += pt * (lpt - lm);
-    s1 += ps * (lps - lm);
-  } else if constexpr (DIV == DIV_SKEW_F) {
-    const float lm = logaddexp(lw + lpt, l1mw + lps);
-    s0 += pt * (lpt - lm);
-    s1 += ps * fexp(lpt - lm);
-  } else if constexpr (DIV == DIV_SKEW_R) {
-    const float lm = logaddexp(lw + lps, l1mw + lpt);
-    s0 += ps * (lps - lm);
-    s1 += ps * fexp(lps - lm);
-  } else {  // TVD
+  if constexpr (DIV == DIV_TVD) {
     s0 += fabsf(pt - ps);
     s1 += (ps > pt) ? ps : ((ps < pt) ? -ps : 0.f);
+  } else {
+    const float m = DIV == DIV_SKEW_R ? w * ps + w1 * pt : w * pt + w1 * ps;
+    const bool ok = m >= kMinNormal;
+    const float mm = ok ? m : 1.f;
+    if constexpr (DIV == DIV_JSD) {
+      const float lm = flog(mm);
+      s0 += ok ? pt * (lpt - lm) : 0.f;
+      s1 += ok ? ps * (lps - lm) : 0.f;
+    } else if constexpr (DIV == DIV_SKEW_F) {
+      s0 += ok ? pt * (lpt - flog(mm)) : 0.f;
+      s1 += ok ? ps * pt * frcp(mm) : 0.f;
+    } else {  // DIV_SKEW_R
+      s0 += ok ? ps * (lps - flog(mm)) : 0.f;
+      s1 += ok ? ps * ps * frcp(mm) : 0.f;
+    }
   }
 }
 
@@ -276,8 +291,7 @@ __device__ __forceinline__ void rowsum_tile(RowState& S, const AP& acc, int vlan
       if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
       const float lps = acc.s(mb, r) * invT - lse_sT;
       const float lpt = acc.t(mb, r) * invT - lse_tT;
-      two_term<DIV>(lps, lpt, DIV == DIV_JSD ? P.log_beta : P.log_alpha,
-                    DIV == DIV_JSD ? P.log_1m_beta : P.log_1m_alpha, s0, s1);
+      two_term<DIV>(lps, lpt, P.mix_w, P.mix_w1, s0, s1);
     }
   S.x[0] += s0;
   S.x[1] += s1;
@@ -1434,25 +1448,120 @@ __global__ __launch_bounds__(256) void k_scale(T* __restrict__ x, int64_t n, con
   }
 }
 
+// ------------------------------------------- token-major teacher tiles
+// A kTmTok-token x kTmRows-row block of the caller's token-major [N x ldtm]
+// 16-bit teacher logits, staged in LDS by token quads:
+//   tile[q * kTmPitch + r * 4 + i] = Tm[tb + 4 q + i][v0 + r]
+// (a quad's 4 values of one row are one 8-byte word; the quad pitch of 130
+// dwords puts the 32 lanes of a half-wave reading rows of consecutive quads
+// on distinct banks).  Loader: thread -> 16-byte piece j = tid % 8 (rows
+// 8 j .. 8 j + 7) of the 4 token rows of quads tid / 8 and tid / 8 + 32 (8
+// lanes cover a token's 128 contiguous bytes), transposed in registers
+// (v_perm_b32) into 8 rows x 4 tokens before the LDS writes.  Requires V a
+// multiple of 8 and 16-byte aligned rows (a piece is wholly in or out of V).
+constexpr int kTmTok = 256, kTmRows = 64, kTmPitch = kTmRows * 4 + 4;
+constexpr int kTmTileElems = (kTmTok / 4) * kTmPitch;
+
+__device__ __forceinline__ uint32_t u4_word(const uint4& v, int k) {
+  return k == 0 ? v.x : (k == 1 ? v.y : (k == 2 ? v.z : v.w));
+}
+
+template <class T>
+struct TmTile {
+  uint4 w[2][4];  // [quad half][token of the quad]: piece j of the token's row
+  __device__ __forceinline__ void load(const T* Tm, int64_t ldtm, int64_t tb, int64_t v0, int64_t N, int64_t V) {
+    const int j = threadIdx.x & 7, q0 = threadIdx.x >> 3;
+    const int64_t v = v0 + j * 8;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t t = tb + (q0 + 32 * h) * 4 + i;
+        w[h][i] = make_uint4(0u, 0u, 0u, 0u);
+        if (t < N && v < V) w[h][i] = *reinterpret_cast<const uint4*>(Tm + t * ldtm + v);
+      }
+  }
+  __device__ __forceinline__ void put(T* tile) const {
+    const int j = threadIdx.x & 7, q0 = threadIdx.x >> 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      T* base = tile + (q0 + 32 * h) * kTmPitch + j * 8 * 4;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // element e of the 4 tokens' pieces: low or high half of word e / 2
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t lo = __builtin_amdgcn_perm(u4_word(w[h][1], e >> 1), u4_word(w[h][0], e >> 1), sel);
+        const uint32_t hi = __builtin_amdgcn_perm(u4_word(w[h][3], e >> 1), u4_word(w[h][2], e >> 1), sel);
+        *reinterpret_cast<uint2*>(base + e * 4) = make_uint2(lo, hi);
+      }
+    }
+  }
+  // the 4 tokens of quad q at row r of the tile
+  __device__ __forceinline__ static void read(const T* tile, int q, int r, float (&x)[4]) {
+    const uint2 u = *reinterpret_cast<const uint2*>(tile + q * kTmPitch + r * 4);
+    x[0] = lo16<T>(u.x);
+    x[1] = hi16<T>(u.x);
+    x[2] = lo16<T>(u.y);
+    x[3] = hi16<T>(u.y);
+  }
+};
+
+// 4 consecutive elements as raw bits (one 8- or 16-byte load when n == 4;
+// elements past n read as zero bits), converted to fp32 at their use: the
+// streaming passes keep a 16-bit row in two registers instead of four.
+template <class T> struct Raw4 { typedef uint2 type; };
+template <> struct Raw4<float> { typedef uint4 type; };
+template <class T>
+__device__ __forceinline__ typename Raw4<T>::type load_raw4(const T* p, int n) {
+  if constexpr (sizeof(T) == 2) {
+    if (n == 4) return *reinterpret_cast<const uint2*>(p);
+    uint32_t e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = i < n ? (uint32_t)__builtin_bit_cast(unsigned short, p[i]) : 0u;
+    return make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+  } else {
+    if (n == 4) return *reinterpret_cast<const uint4*>(p);
+    uint32_t e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = i < n ? __float_as_uint(p[i]) : 0u;
+    return make_uint4(e[0], e[1], e[2], e[3]);
+  }
+}
+template <class T>
+__device__ __forceinline__ void unpack4(const typename Raw4<T>::type& u, float (&x)[4]) {
+  if constexpr (sizeof(T) == 2) {
+    x[0] = lo16<T>(u.x);
+    x[1] = hi16<T>(u.x);
+    x[2] = lo16<T>(u.y);
+    x[3] = hi16<T>(u.y);
+  } else {
+    x[0] = __uint_as_float(u.x);
+    x[1] = __uint_as_float(u.y);
+    x[2] = __uint_as_float(u.z);
+    x[3] = __uint_as_float(u.w);
+  }
+}
+
 // ------------------------------------- two-pass row sums on stored logits
 // Phase 1 of the two-pass divergences (JSD, skew KLs, TVD) for the
 // gradients-in-forward schedule: the row sums x0, x1 over a token chunk's
 // stored logits L[v][t] (student columns [0, N), teacher columns
 // [tcol, tcol + N)), normalised with phase 0's log-sum-exps (rowp rows 1
 // and 3), with the same per-row terms as the two-phase scan (two_term).
-// One partial state (slots x0, x1) per (vocabulary range, token) for
-// k_merge's phase 1.  Block: 16 token quads x 64 row lanes (1024 threads:
-// enough waves in flight for a latency-bound stream), grid: (groups of 64
-// tokens, vocabulary ranges); a thread reads 4 tokens of every 64th row of
-// its range (8-byte loads for 16-bit logits; a wave covers 4 rows x 128
-// contiguous bytes), 4 rows in flight, and the 64 row lanes' sums are added
-// in a fixed order (bit-stable).
-constexpr int kTwoLanes = 64;
+// One partial pair per (vocabulary range, token), dense: x0 at
+// partial[(range * 2) * N + t], x1 at partial[(range * 2 + 1) * N + t]
+// (k_merge's phase 1 with two_dense).  Block: 4 waves over kTwoTok tokens
+// (a lane's 4 consecutive tokens: 8-byte loads of 16-bit logits, 512
+// contiguous bytes per wave and row); wave w takes rows w, w + 4, ... of the
+// range, 4 rows per step with the next step's loads issued before this
+// step's math, and the four waves' sums are added in a fixed order
+// (bit-stable).
+constexpr int kTwoTok = 256;
 template <class T, int DIV>
-__global__ __launch_bounds__(16 * kTwoLanes) void k_two_rows(TwoParams P) {
-  __shared__ float xch[2][kTwoLanes][64];
-  const int tq = threadIdx.x & 15, rl = threadIdx.x >> 4;
-  const int64_t tb = (int64_t)blockIdx.x * 64 + tq * 4;
+__global__ __launch_bounds__(256) void k_two_rows(TwoParams P) {
+  __shared__ float xch[2][4][kTwoTok];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t tb = (int64_t)blockIdx.x * kTwoTok + lane * 4;
   const int64_t v0 = (int64_t)blockIdx.y * P.rows_per_range;
   const int64_t v1 = min<int64_t>(P.V, v0 + P.rows_per_range);
   const int64_t rem = P.N - tb;
@@ -1469,135 +1578,125 @@ __global__ __launch_bounds__(16 * kTwoLanes) void k_two_rows(TwoParams P) {
   }
   const T* Ls = static_cast<const T*>(P.L) + (nt > 0 ? tb : 0);
   const T* Lt = Ls + P.tcol;
-  auto rows = [&](const float (&xs)[4], const float (&xt)[4]) {
+  using Raw = typename Raw4<T>::type;
+  auto rows = [&](const Raw& us, const Raw& ut) {
+    float xs[4], xt[4];
+    unpack4<T>(us, xs);
+    unpack4<T>(ut, xt);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      two_term<DIV>(xs[i] * invT - lse_sT[i], xt[i] * invT - lse_tT[i], P.lw, P.l1mw, s0[i], s1[i]);
+      two_term<DIV>(xs[i] * invT - lse_sT[i], xt[i] * invT - lse_tT[i], P.mix_w, P.mix_w1, s0[i], s1[i]);
   };
   if (nt > 0) {
-    int64_t v = v0 + rl;
+    int64_t v = v0 + w;
     constexpr int R = 4;
-    for (; v + kTwoLanes * (R - 1) < v1; v += kTwoLanes * R) {
-      float xs[R][4], xt[R][4];
+    Raw xs[R], xt[R];
+    auto load_rows = [&](int64_t vv) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        load4(Ls + (v + kTwoLanes * r) * P.ldL, xs[r], nt == 4, nt);
-        load4(Lt + (v + kTwoLanes * r) * P.ldL, xt[r], nt == 4, nt);
+        xs[r] = load_raw4(Ls + (vv + 4 * r) * P.ldL, nt);
+        xt[r] = load_raw4(Lt + (vv + 4 * r) * P.ldL, nt);
       }
+    };
+    if (v + 4 * (R - 1) < v1) load_rows(v);
+    for (; v + 4 * (R - 1) < v1; v += 4 * R) {
+      Raw cs[R], ct[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) rows(xs[r], xt[r]);
+      for (int r = 0; r < R; ++r) {
+        cs[r] = xs[r];
+        ct[r] = xt[r];
+      }
+      if (v + 4 * R + 4 * (R - 1) < v1) load_rows(v + 4 * R);
+#pragma unroll
+      for (int r = 0; r < R; ++r) rows(cs[r], ct[r]);
     }
-    for (; v < v1; v += kTwoLanes) {
-      float xs[4], xt[4];
-      load4(Ls + v * P.ldL, xs, nt == 4, nt);
-      load4(Lt + v * P.ldL, xt, nt == 4, nt);
-      rows(xs, xt);
-    }
+    for (; v < v1; v += 4) rows(load_raw4(Ls + v * P.ldL, nt), load_raw4(Lt + v * P.ldL, nt));
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    xch[0][rl][tq * 4 + i] = s0[i];
-    xch[1][rl][tq * 4 + i] = s1[i];
+    xch[0][w][lane * 4 + i] = s0[i];
+    xch[1][w][lane * 4 + i] = s1[i];
   }
   __syncthreads();
-  if (threadIdx.x < 64) {
-    const int tk = threadIdx.x;
-    const int64_t t = (int64_t)blockIdx.x * 64 + tk;
-    float a = 0.f, b = 0.f;
-#pragma unroll 8
-    for (int r = 0; r < kTwoLanes; ++r) {
-      a += xch[0][r][tk];
-      b += xch[1][r][tk];
-    }
-    if (t < P.N) {
-      float* dst = P.partial + (int64_t)blockIdx.y * kNStat * P.N + t;
-      dst[6 * P.N] = a;  // RowState x[0]
-      dst[7 * P.N] = b;  // RowState x[1]
-    }
+  const int tk = threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * kTwoTok + tk;
+  if (t < P.N) {
+    float* dst = P.partial + (int64_t)blockIdx.y * 2 * P.N + t;
+    dst[0] = (xch[0][0][tk] + xch[0][1][tk]) + (xch[0][2][tk] + xch[0][3][tk]);
+    dst[P.N] = (xch[1][0][tk] + xch[1][1][tk]) + (xch[1][2][tk] + xch[1][3][tk]);
   }
 }
 
 // k_two_rows with the teacher's logits read in place from the caller's
-// precomputed [N x ldtm] tensor (token-major): per iteration the block loads
-// the teacher's 64 tokens x 256 rows with 32-byte loads (16 lanes per
-// token's 512 contiguous bytes) into LDS, and each row lane takes rows
-// rl, rl + 64, rl + 128, rl + 192 of it for its 4 tokens, beside the
-// student's 8-byte loads from L issued in the same iteration.  Same partial
-// states and fixed-order reduction as k_two_rows.
+// precomputed [N x ldtm] tensor (token-major): the block walks its range in
+// tiles of kTmRows rows; per tile the teacher's kTmTok x kTmRows block is
+// staged in LDS by token quads (TmTile) and wave w takes rows w, w + 4, ...
+// of it beside the student's 8-byte loads from L, all of a tile's loads
+// issued before its staging barrier.  Same partial pairs and fixed-order
+// reduction as k_two_rows; rows_per_range a multiple of kTmRows.
 template <class T, int DIV>
-__global__ __launch_bounds__(16 * kTwoLanes) void k_two_rows_tm(TwoParams P) {
-  constexpr int kIt = 4 * kTwoLanes;            // rows per iteration
-  __shared__ T tt[64][kIt + 8];                 // 64 tokens x 264 (rows of 528 B)
-  __shared__ float xch[2][kTwoLanes][64];
-  const int tid = threadIdx.x;
-  const int tq = tid & 15, rl = tid >> 4;
-  const int64_t tb = (int64_t)blockIdx.x * 64 + tq * 4;
+__global__ __launch_bounds__(256) void k_two_rows_tm(TwoParams P) {
+  __shared__ __align__(16) T tile[kTmTileElems];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t tb = (int64_t)blockIdx.x * kTmTok;
+  const int64_t t0 = tb + lane * 4;
   const int64_t v0 = (int64_t)blockIdx.y * P.rows_per_range;
   const int64_t v1 = min<int64_t>(P.V, v0 + P.rows_per_range);
-  const int64_t rem = P.N - tb;
+  const int64_t rem = P.N - t0;
   const int nt = rem <= 0 ? 0 : (rem >= 4 ? 4 : (int)rem);
   const float invT = P.invT;
   float lse_sT[4], lse_tT[4], s0[4], s1[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t t = i < nt ? tb + i : 0;
+    const int64_t t = i < nt ? t0 + i : 0;
     lse_sT[i] = P.rowp[1 * P.N + t];
     lse_tT[i] = P.rowp[3 * P.N + t];
     s0[i] = 0.f;
     s1[i] = 0.f;
   }
-  const T* Ls = static_cast<const T*>(P.L) + (nt > 0 ? tb : 0);
-  // teacher load: thread -> token tk, rows pr .. pr + 15 of the iteration
-  const int tk = tid >> 4, pr = (tid & 15) * 16;
-  const int64_t tglob = (int64_t)blockIdx.x * 64 + tk;
-  const bool tk_ok = tglob < P.N;
-  const T* tsrc = static_cast<const T*>(P.Ltm) + (tk_ok ? tglob : 0) * P.ldtm;
-  for (int64_t vb = v0; vb < v1; vb += kIt) {
-    union { T e[8]; uint4 u; } w0, w1;
-    w0.u = make_uint4(0u, 0u, 0u, 0u);
-    w1.u = make_uint4(0u, 0u, 0u, 0u);
-    if (tk_ok && vb + pr < P.V) w0.u = *reinterpret_cast<const uint4*>(tsrc + vb + pr);
-    if (tk_ok && vb + pr + 8 < P.V) w1.u = *reinterpret_cast<const uint4*>(tsrc + vb + pr + 8);
-    float xs[4][4];
+  const T* Ls = static_cast<const T*>(P.L) + (nt > 0 ? t0 : 0);
+  const T* Tm = static_cast<const T*>(P.Ltm);
+  constexpr int M = kTmRows / 4;  // rows per wave and tile
+  TmTile<T> tm;
+  for (int64_t vb = v0; vb < v1; vb += kTmRows) {
+    tm.load(Tm, P.ldtm, tb, vb, P.N, P.V);
+    typename Raw4<T>::type xs[M];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t v = vb + rl + r * kTwoLanes;
-      if (nt > 0 && v < v1) load4(Ls + v * P.ldL, xs[r], nt == 4, nt);
+    for (int m = 0; m < M; ++m) {
+      const int64_t v = vb + w + 4 * m;
+      xs[m] = {};
+      if (nt > 0 && v < v1) xs[m] = load_raw4(Ls + v * P.ldL, nt);
     }
-    __syncthreads();  // the previous iteration's LDS reads are done
-    *reinterpret_cast<uint4*>(&tt[tk][pr]) = w0.u;
-    *reinterpret_cast<uint4*>(&tt[tk][pr + 8]) = w1.u;
+    __syncthreads();  // the previous tile's LDS reads are done
+    tm.put(tile);
     __syncthreads();
     if (nt == 0) continue;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t v = vb + rl + r * kTwoLanes;
-      if (v >= v1) break;
+    for (int m = 0; m < M; ++m) {
+      const int r = w + 4 * m;
+      if (vb + r >= v1) break;
+      float xsf[4], xt[4];
+      unpack4<T>(xs[m], xsf);
+      TmTile<T>::read(tile, lane, r, xt);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        two_term<DIV>(xs[r][i] * invT - lse_sT[i], to_f32(tt[tq * 4 + i][rl + r * kTwoLanes]) * invT - lse_tT[i],
-                      P.lw, P.l1mw, s0[i], s1[i]);
+        two_term<DIV>(xsf[i] * invT - lse_sT[i], xt[i] * invT - lse_tT[i], P.mix_w, P.mix_w1, s0[i], s1[i]);
     }
   }
+  __syncthreads();  // the tile's LDS becomes the exchange buffer
+  float* xch = reinterpret_cast<float*>(tile);  // [2][4][kTmTok] (8 KiB)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    xch[0][rl][tq * 4 + i] = s0[i];
-    xch[1][rl][tq * 4 + i] = s1[i];
+    xch[(0 * 4 + w) * kTmTok + lane * 4 + i] = s0[i];
+    xch[(1 * 4 + w) * kTmTok + lane * 4 + i] = s1[i];
   }
   __syncthreads();
-  if (tid < 64) {
-    const int64_t t = (int64_t)blockIdx.x * 64 + tid;
-    float a = 0.f, b = 0.f;
-#pragma unroll 8
-    for (int r = 0; r < kTwoLanes; ++r) {
-      a += xch[0][r][tid];
-      b += xch[1][r][tid];
-    }
-    if (t < P.N) {
-      float* dst = P.partial + (int64_t)blockIdx.y * kNStat * P.N + t;
-      dst[6 * P.N] = a;  // RowState x[0]
-      dst[7 * P.N] = b;  // RowState x[1]
-    }
+  const int tk = threadIdx.x;
+  const int64_t t = tb + tk;
+  if (t < P.N) {
+    float* dst = P.partial + (int64_t)blockIdx.y * 2 * P.N + t;
+    dst[0] = (xch[0 * kTmTok + tk] + xch[1 * kTmTok + tk]) + (xch[2 * kTmTok + tk] + xch[3 * kTmTok + tk]);
+    dst[P.N] = (xch[4 * kTmTok + tk] + xch[5 * kTmTok + tk]) + (xch[6 * kTmTok + tk] + xch[7 * kTmTok + tk]);
   }
 }
 
@@ -1677,21 +1776,20 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
   if (nt == 4) {
     // interior: R rows per iteration, every load issued before any use
     constexpr int R = 8;
+    using Raw = typename Raw4<T>::type;
     for (; v + R <= v1; v += R) {
-      float xs[R][4], xt[R][4];
+      Raw us[R], ut[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        load4(Ls + (v + r) * P.ldL, xs[r], true, 4);
-        if (need_t) load4(Lt + (v + r) * P.ldL, xt[r], true, 4);
-        else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) xt[r][i] = 0.f;
-        }
+        us[r] = load_raw4(Ls + (v + r) * P.ldL, 4);
+        ut[r] = need_t ? load_raw4(Lt + (v + r) * P.ldL, 4) : Raw{};
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        float ds[4], dt[4];
-        q.row(v + r, xs[r], xt[r], ds, dt);
+        float xs[4], xt[4], ds[4], dt[4];
+        unpack4<T>(us[r], xs);
+        unpack4<T>(ut[r], xt);
+        q.row(v + r, xs, xt, ds, dt);
         store4(Ls + (v + r) * P.ldL, ds, true, 4);
         if (P.tgrad) store4(Lt + (v + r) * P.ldL, dt, true, 4);
       }
@@ -1710,61 +1808,48 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
 
 // The same dlogits with the teacher's logits read in place from the caller's
 // precomputed [N x ldtm] tensor (token-major; no teacher gradient): a block
-// takes 64 tokens and walks kDlmTmTiles tiles of 64 vocabulary rows.  Per
-// tile, the teacher's 64 x 64 block is loaded with 32-byte loads, 4 lanes per
-// token covering its 128 contiguous bytes, and put in LDS; each thread then
-// takes 4 tokens x 4 rows of it transposed, beside the student's 8-byte
-// loads of 4 tokens per row from L (16 lanes per row), which are issued
-// together with the teacher's.  Requires ldtm a multiple of 8 and 16-byte
-// aligned rows.
-constexpr int kDlmTmTok = 64, kDlmTmRows = 64, kDlmTmTiles = 8;
+// takes kTmTok tokens x kTmRows vocabulary rows.  The teacher's block is
+// staged in LDS by token quads (TmTile); the student's rows come from L with
+// 8-byte loads (a lane's 4 tokens, 512 contiguous bytes per wave and row;
+// wave w takes rows w, w + 4, ...), issued with the teacher's before the
+// staging barrier.  (Blocks of one tile: with many short blocks in flight
+// the stream runs faster than with a block walking several tiles.)
 template <class T, int DIV, bool T1>
 __global__ __launch_bounds__(256) void k_dlm_tm(DlmParams P) {
-  __shared__ T tt[kDlmTmTok][kDlmTmRows + 8];  // rows of 144 B
-  const int tid = threadIdx.x;
-  const int64_t tb = (int64_t)blockIdx.x * kDlmTmTok;
-  const int64_t vb = (int64_t)blockIdx.y * (kDlmTmRows * kDlmTmTiles);
-  const int64_t vend = min<int64_t>(P.V, vb + kDlmTmRows * kDlmTmTiles);
-  const T* Tm = static_cast<const T*>(P.Ltm);
-  // teacher load: thread -> token tk, rows rc .. rc + 15 of the tile
-  const int tk = tid >> 2, rc = (tid & 3) * 16;
-  const bool tk_ok = tb + tk < P.N;
-  const T* tsrc = Tm + (tk_ok ? tb + tk : 0) * P.ldtm;
-  // compute: thread -> token quad tq, rows rg * 4 .. + 3 of the tile
-  const int tq = tid & 15, rg = tid >> 4;
-  const int64_t t0 = tb + tq * 4;
-  const bool live = t0 < P.N;
-  const int nt = live ? (int)min<int64_t>(P.N - t0, 4) : 0;
+  __shared__ __align__(16) T tile[kTmTileElems];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t tb = (int64_t)blockIdx.x * kTmTok;
+  const int64_t v0 = (int64_t)blockIdx.y * kTmRows;
+  TmTile<T> tm;
+  tm.load(static_cast<const T*>(P.Ltm), P.ldtm, tb, v0, P.N, P.V);
+  const int64_t t0 = tb + lane * 4;
+  const int64_t rem = P.N - t0;
+  const int nt = rem <= 0 ? 0 : (rem >= 4 ? 4 : (int)rem);
+  const bool live = nt > 0;
+  T* Ls = static_cast<T*>(P.L) + (live ? t0 : 0);
+  constexpr int M = kTmRows / 4;  // rows per wave
+  typename Raw4<T>::type xs[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int64_t v = v0 + w + 4 * m;
+    xs[m] = {};
+    if (live && v < P.V) xs[m] = load_raw4(Ls + v * P.ldL, nt);
+  }
   DlmQuad<DIV, T1> q;
   q.init(P, live ? t0 : 0, nt);
-  T* Ls = static_cast<T*>(P.L) + (live ? t0 : 0);
-  for (int64_t v0 = vb; v0 < vend; v0 += kDlmTmRows) {
-    union { T e[8]; uint4 u; } w0, w1;
-    w0.u = make_uint4(0u, 0u, 0u, 0u);
-    w1.u = make_uint4(0u, 0u, 0u, 0u);
-    if (tk_ok && v0 + rc < P.V) w0.u = *reinterpret_cast<const uint4*>(tsrc + v0 + rc);
-    if (tk_ok && v0 + rc + 8 < P.V) w1.u = *reinterpret_cast<const uint4*>(tsrc + v0 + rc + 8);
-    float xs[4][4];
+  tm.put(tile);
+  __syncthreads();
+  if (!live) return;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t v = v0 + rg * 4 + r;
-      if (live && v < P.V) load4(Ls + v * P.ldL, xs[r], nt == 4, nt);
-    }
-    __syncthreads();  // the previous tile's LDS reads are done
-    *reinterpret_cast<uint4*>(&tt[tk][rc]) = w0.u;
-    *reinterpret_cast<uint4*>(&tt[tk][rc + 8]) = w1.u;
-    __syncthreads();
-    if (!live) continue;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t v = v0 + rg * 4 + r;
-      if (v >= P.V) break;
-      float xt[4], ds[4], dt[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xt[i] = to_f32(tt[tq * 4 + i][rg * 4 + r]);
-      q.row(v, xs[r], xt, ds, dt);
-      store4(Ls + v * P.ldL, ds, nt == 4, nt);
-    }
+  for (int m = 0; m < M; ++m) {
+    const int r = w + 4 * m;
+    const int64_t v = v0 + r;
+    if (v >= P.V) break;
+    float x[4], xt[4], ds[4], dt[4];
+    unpack4<T>(xs[m], x);
+    TmTile<T>::read(tile, lane, r, xt);
+    q.row(v, x, xt, ds, dt);
+    store4(Ls + v * P.ldL, ds, nt == 4, nt);
   }
 }
 
@@ -2160,29 +2245,39 @@ __global__ __launch_bounds__(256) void k_topk_scatter(TopKParams P) {
 }
 
 // ------------------------------------------------ student RMSNorm prologue
-// One wave per row: y = x * r * gamma with r = rsqrt(sum(x^2) / D + eps),
+// Sum over the 256 threads of a block, in every thread (wave sums, then the
+// four waves' partials through LDS in a fixed order).
+__device__ __forceinline__ float block_sum256(float x, float* red) {
+  x = wave_sum(x);
+  __syncthreads();  // red is free (a previous call's reads are done)
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// One block per row: y = x * r * gamma with r = rsqrt(sum(x^2) / D + eps),
 // in fp32 from the row's 4-element groups, rounded once to T (the reference
 // producer's RMSNorm, test/benchmark/src/core.py:13-14, computes the same
 // product in the activation dtype).
 template <class T>
 __global__ __launch_bounds__(256) void k_rmsnorm_fwd(NormParams P) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= P.N) return;  // whole waves
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t t = blockIdx.x;
   const T* x = static_cast<const T*>(P.x) + t * P.H;
   const T* g = static_cast<const T*>(P.gamma);
   T* y = static_cast<T*>(P.y) + t * P.H;
   const int64_t ng = P.H / 4;
   float ss = 0.f;
-  for (int64_t c = lane; c < ng; c += 64) {
+  for (int64_t c = tid; c < ng; c += 256) {
     float v[4];
     load4(x + c * 4, v, true, 4);
     ss += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
   }
-  ss = wave_sum(ss);
+  ss = block_sum256(ss, red);
   const float r = rsqrtf(ss / (float)P.D + P.eps);
-  if (lane == 0) P.rstd[t] = r;
-  for (int64_t c = lane; c < ng; c += 64) {
+  if (tid == 0) P.rstd[t] = r;
+  for (int64_t c = tid; c < ng; c += 256) {
     float v[4], w[4];
     load4(x + c * 4, v, true, 4);
     load4(g + c * 4, w, true, 4);
@@ -2198,16 +2293,27 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(NormParams P) {
 // and on the last chunk the result in T.
 template <class T>
 __global__ __launch_bounds__(256) void k_rmsnorm_dgamma(NormParams P) {
-  const int64_t h = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (h >= P.H) return;
+  // four consecutive columns per thread (one 8-byte load per row for 16-bit
+  // types), tokens of the group walked in order
+  const int64_t h = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (h >= P.H) return;  // H is a multiple of 4
   const int64_t per = (P.N + P.groups - 1) / P.groups;
   const int64_t t0 = (int64_t)blockIdx.y * per;
   const int64_t t1 = min<int64_t>(P.N, t0 + per);
   const T* dy = static_cast<const T*>(P.dxy);
   const T* x = static_cast<const T*>(P.x);
-  float acc = 0.f;
-  for (int64_t t = t0; t < t1; ++t) acc += to_f32(dy[t * P.H + h]) * to_f32(x[t * P.H + h]) * P.rstd[t];
-  P.gpart[(int64_t)blockIdx.y * P.H + h] = acc;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t t = t0; t < t1; ++t) {
+    float d[4], v[4];
+    load4(dy + t * P.H + h, d, true, 4);
+    load4(x + t * P.H + h, v, true, 4);
+    const float r = P.rstd[t];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += d[e] * v[e] * r;
+  }
+  float* o = P.gpart + (int64_t)blockIdx.y * P.H + h;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = acc[e];
 }
 template <class T>
 __global__ __launch_bounds__(256) void k_rmsnorm_gacc(NormParams P) {
@@ -2221,18 +2327,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm_gacc(NormParams P) {
 }
 
 // dloss/dx = r (gamma . dy) - x r^3 <gamma . dy, x> / D, in place over dy
-// (one wave per row; two passes over the row).
+// (one block per row; two passes over the row).
 template <class T>
 __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= P.N) return;
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t t = blockIdx.x;
   const T* x = static_cast<const T*>(P.x) + t * P.H;
   const T* g = static_cast<const T*>(P.gamma);
   T* d = static_cast<T*>(P.dxy) + t * P.H;
   const int64_t ng = P.H / 4;
   float c = 0.f;
-  for (int64_t i = lane; i < ng; i += 64) {
+  for (int64_t i = tid; i < ng; i += 256) {
     float v[4], w[4], dy[4];
     load4(x + i * 4, v, true, 4);
     load4(g + i * 4, w, true, 4);
@@ -2240,10 +2346,10 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) c += w[e] * dy[e] * v[e];
   }
-  c = wave_sum(c);
+  c = block_sum256(c, red);
   const float r = P.rstd[t];
   const float k = r * r * r * c / (float)P.D;
-  for (int64_t i = lane; i < ng; i += 64) {
+  for (int64_t i = tid; i < ng; i += 256) {
     float v[4], w[4], dy[4];
     load4(x + i * 4, v, true, 4);
     load4(g + i * 4, w, true, 4);
@@ -2406,11 +2512,12 @@ inline void gemm2_go(const GemmParams& P, hipStream_t s) {
 // In-place dlogits variants (the divergences of families LIN and POW).
 template <class T, int DIV, bool T1, bool NO_T = false>
 inline void dlm_go(const DlmParams& P, hipStream_t s) {
-  if (P.Ltm) {
-    const int64_t rows = kDlmTmRows * kDlmTmTiles;
-    const dim3 grid((unsigned)((P.N + kDlmTmTok - 1) / kDlmTmTok), (unsigned)((P.V + rows - 1) / rows));
-    hipLaunchKernelGGL((k_dlm_tm<T, DIV, T1>), grid, dim3(256), 0, s, P);
-    return;
+  if constexpr (sizeof(T) == 2) {  // (teacher logits in place: 16-bit only)
+    if (P.Ltm) {
+      const dim3 grid((unsigned)((P.N + kTmTok - 1) / kTmTok), (unsigned)((P.V + kTmRows - 1) / kTmRows));
+      hipLaunchKernelGGL((k_dlm_tm<T, DIV, T1>), grid, dim3(256), 0, s, P);
+      return;
+    }
   }
   const dim3 grid((unsigned)((P.N + 1023) / 1024), (unsigned)((P.V + P.rows_per_block - 1) / P.rows_per_block));
   hipLaunchKernelGGL((k_dlm<T, DIV, T1, NO_T>), grid, dim3(256), 0, s, P);
@@ -2444,22 +2551,22 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
     if (!P.x || !P.gamma || !P.y || !P.rstd || P.H % 4 != 0 || P.D < 1 || P.D > P.H)       \
       return hipErrorInvalidValue;                                                         \
     if (P.N <= 0) return hipSuccess;                                                       \
-    hipLaunchKernelGGL(k_rmsnorm_fwd<T>, dim3((unsigned)((P.N + 3) / 4)), dim3(256), 0, s, P); \
+    hipLaunchKernelGGL(k_rmsnorm_fwd<T>, dim3((unsigned)P.N), dim3(256), 0, s, P);         \
     return hipGetLastError();                                                              \
   }                                                                                        \
   template <> hipError_t launch_rmsnorm_dgamma<T>(const NormParams& P, hipStream_t s) {    \
     if (!P.x || !P.dxy || !P.rstd || !P.gpart || !P.gacc || P.groups < 1 || P.groups > 65535) \
       return hipErrorInvalidValue;                                                         \
-    const unsigned bx = (unsigned)((P.H + 255) / 256);                                     \
-    hipLaunchKernelGGL(k_rmsnorm_dgamma<T>, dim3(bx, (unsigned)P.groups), dim3(256), 0, s, P); \
-    hipLaunchKernelGGL(k_rmsnorm_gacc<T>, dim3(bx), dim3(256), 0, s, P);                   \
+    hipLaunchKernelGGL(k_rmsnorm_dgamma<T>, dim3((unsigned)((P.H + 1023) / 1024), (unsigned)P.groups), \
+                       dim3(256), 0, s, P);                                                \
+    hipLaunchKernelGGL(k_rmsnorm_gacc<T>, dim3((unsigned)((P.H + 255) / 256)), dim3(256), 0, s, P); \
     return hipGetLastError();                                                              \
   }                                                                                        \
   template <> hipError_t launch_rmsnorm_bwd<T>(const NormParams& P, hipStream_t s) {       \
     if (!P.x || !P.gamma || !P.dxy || !P.rstd || P.H % 4 != 0 || P.D < 1)                  \
       return hipErrorInvalidValue;                                                         \
     if (P.N <= 0) return hipSuccess;                                                       \
-    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3((unsigned)((P.N + 3) / 4)), dim3(256), 0, s, P); \
+    hipLaunchKernelGGL(k_rmsnorm_bwd<T>, dim3((unsigned)P.N), dim3(256), 0, s, P);         \
     return hipGetLastError();                                                              \
   }                                                                                        \
   template <> hipError_t launch_topk_rows<T>(const TopKParams& P, hipStream_t s) {         \
@@ -2484,6 +2591,8 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
     const bool t1 = P.t_is_one != 0;                                                       \
     if (P.no_t && (P.tgrad || (P.div != -1 && P.div != DIV_FKL && P.div != DIV_SOFT)))     \
       return hipErrorInvalidValue; /* no teacher logits to read */                         \
+    if (P.Ltm && (sizeof(T) != 2 || (P.V + kTmRows - 1) / kTmRows > 65535 || P.V % 8 != 0)) \
+      return hipErrorInvalidValue; /* grid.y of k_dlm_tm; whole 16-byte teacher pieces */  \
     switch (P.div) {                                                                       \
       case -1: dlm_go<T, -1, true>(P, s); break;                                           \
       case DIV_FKL: ORDA_DLM_T1_CASE(T, DIV_FKL) break;                                    \
@@ -2506,22 +2615,25 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
     return hipGetLastError();                                                              \
   }                                                                                        \
   template <> hipError_t launch_two<T>(const TwoParams& P, hipStream_t s) {                \
-    const dim3 grid((unsigned)((P.N + 63) / 64), (unsigned)P.n_ranges);                   \
+    if (P.n_ranges <= 0 || P.n_ranges > 65535 || P.rows_per_range <= 0) return hipErrorInvalidValue; \
+    const dim3 grid((unsigned)((P.N + kTwoTok - 1) / kTwoTok), (unsigned)P.n_ranges);     \
     if (P.Ltm) {                                                                           \
-      switch (P.div) {                                                                     \
-        case DIV_JSD: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_JSD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
-        case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_SKEW_F>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
-        case DIV_SKEW_R: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_SKEW_R>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
-        case DIV_TVD: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_TVD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+      if (sizeof(T) != 2 || P.rows_per_range % kTmRows != 0 || P.V % 8 != 0)               \
+        return hipErrorInvalidValue;                                                       \
+      if constexpr (sizeof(T) == 2) switch (P.div) {                                       \
+        case DIV_JSD: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_JSD>), grid, dim3(256), 0, s, P); break; \
+        case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_SKEW_F>), grid, dim3(256), 0, s, P); break; \
+        case DIV_SKEW_R: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_SKEW_R>), grid, dim3(256), 0, s, P); break; \
+        case DIV_TVD: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_TVD>), grid, dim3(256), 0, s, P); break; \
         default: return hipErrorInvalidValue;                                              \
       }                                                                                    \
       return hipGetLastError();                                                            \
     }                                                                                      \
     switch (P.div) {                                                                       \
-      case DIV_JSD: hipLaunchKernelGGL((k_two_rows<T, DIV_JSD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
-      case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_F>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
-      case DIV_SKEW_R: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_R>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
-      case DIV_TVD: hipLaunchKernelGGL((k_two_rows<T, DIV_TVD>), grid, dim3(16 * kTwoLanes), 0, s, P); break; \
+      case DIV_JSD: hipLaunchKernelGGL((k_two_rows<T, DIV_JSD>), grid, dim3(256), 0, s, P); break; \
+      case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_F>), grid, dim3(256), 0, s, P); break; \
+      case DIV_SKEW_R: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_R>), grid, dim3(256), 0, s, P); break; \
+      case DIV_TVD: hipLaunchKernelGGL((k_two_rows<T, DIV_TVD>), grid, dim3(256), 0, s, P); break; \
       default: return hipErrorInvalidValue;                                                \
     }                                                                                      \
     return hipGetLastError();                                                              \

@@ -42,7 +42,7 @@ struct FusedParams {
   int t_is_one;
   int tgrad;  // dlogits of the teacher are needed (teacher CE gradients)
   float invT, temperature, alpha, beta;
-  float log_alpha, log_1m_alpha, log_beta, log_1m_beta;
+  float mix_w, mix_w1;  // mixture weight of the two-pass divergences, 1 - it
   float pa[3], pb[3];
   int npow;
   // scan
@@ -157,13 +157,13 @@ struct TwoParams {
   const void* L;  // [V][ldL]; student columns [0, N), teacher columns [tcol, tcol + N)
   int64_t ldL, tcol;
   const float* rowp;  // [kNRowP][N]: rows 1 and 3 = log-sum-exps at T
-  float* partial;     // [n_ranges][kNStat][N]: slots 6, 7 written
+  float* partial;     // [n_ranges][2][N]: x0, x1 per vocabulary range (dense)
   int64_t N, V, rows_per_range;
-  int n_ranges, div;
-  float invT, lw, l1mw;  // log w, log(1 - w) of the mixture weight
+  int n_ranges, div;  // n_ranges <= 65535
+  float invT, mix_w, mix_w1;  // mixture weight (beta for JSD, alpha for skew), 1 - it
   // precomputed teacher logits read in place, token-major [N][ldtm] (16-byte
-  // aligned rows, ldtm and rows_per_range multiples of 8); else null: the
-  // teacher's logits are L's teacher columns
+  // aligned rows, V a multiple of 8, rows_per_range a multiple of 64); else
+  // null: the teacher's logits are L's teacher columns
   const void* Ltm;
   int64_t ldtm;
 };
@@ -243,6 +243,9 @@ struct MergeParams {
   // when set: the student's log-sum-exp at T per row as the losses use it
   // (fp32 statistics, no rounding adjustment) -- a top-k teacher's rows
   float* lse_sT_out;
+  // phase 1 reads k_two_rows' dense [n_vranges][2][N] pairs (else slots 6, 7
+  // of the scan's [n_vranges][kNStat][N] states)
+  int two_dense;
 };
 hipError_t launch_merge(const MergeParams& P, hipStream_t s);
 

@@ -31,9 +31,9 @@ __global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams 
     double x0 = 0.0, x1 = 0.0;
     if (live)
       for (int vr = slice; vr < P.n_vranges; vr += kMergeSlices) {
-        const float* s = P.partial + (int64_t)vr * kNStat * N + t;
-        x0 += s[6 * N];
-        x1 += s[7 * N];
+        const float* s = P.two_dense ? P.partial + (int64_t)vr * 2 * N + t : P.partial + (int64_t)vr * kNStat * N + 6 * N + t;
+        x0 += s[0];
+        x1 += s[N];
       }
     if (slice > 0) { xch1[slice - 1][0][tl] = x0; xch1[slice - 1][1][tl] = x1; }
     __syncthreads();
