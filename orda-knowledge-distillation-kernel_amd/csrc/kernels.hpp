@@ -1658,14 +1658,25 @@ __global__ __launch_bounds__(256) void k_two_rows_tm(TwoParams P) {
   const T* Tm = static_cast<const T*>(P.Ltm);
   constexpr int M = kTmRows / 4;  // rows per wave and tile
   TmTile<T> tm;
+  using Raw = typename Raw4<T>::type;
+  const bool full_tok = tb + kTmTok <= P.N;  // block-uniform
   for (int64_t vb = v0; vb < v1; vb += kTmRows) {
     tm.load(Tm, P.ldtm, tb, vb, P.N, P.V);
-    typename Raw4<T>::type xs[M];
+    Raw xs[M];
+    if (full_tok && vb + kTmRows <= v1) {  // no per-row guards
+      const T* p = Ls + (vb + w) * P.ldL;
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const int64_t v = vb + w + 4 * m;
-      xs[m] = {};
-      if (nt > 0 && v < v1) xs[m] = load_raw4(Ls + v * P.ldL, nt);
+      for (int m = 0; m < M; ++m) {
+        xs[m] = *reinterpret_cast<const Raw*>(p);
+        p += 4 * P.ldL;
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const int64_t v = vb + w + 4 * m;
+        xs[m] = {};
+        if (nt > 0 && v < v1) xs[m] = load_raw4(Ls + v * P.ldL, nt);
+      }
     }
     __syncthreads();  // the previous tile's LDS reads are done
     tm.put(tile);
@@ -1813,7 +1824,9 @@ __global__ __launch_bounds__(256) void k_dlm(DlmParams P) {
 // 8-byte loads (a lane's 4 tokens, 512 contiguous bytes per wave and row;
 // wave w takes rows w, w + 4, ...), issued with the teacher's before the
 // staging barrier.  (Blocks of one tile: with many short blocks in flight
-// the stream runs faster than with a block walking several tiles.)
+// the stream runs faster than with a block walking several tiles.)  Blocks
+// wholly inside [0, N) x [0, V) take a path without per-row guards (pointer
+// steps, packed stores): 0.35 -> 0.29 ms per 2048-token chunk at V = 128256.
 template <class T, int DIV, bool T1>
 __global__ __launch_bounds__(256) void k_dlm_tm(DlmParams P) {
   __shared__ __align__(16) T tile[kTmTileElems];
@@ -1826,20 +1839,46 @@ __global__ __launch_bounds__(256) void k_dlm_tm(DlmParams P) {
   const int64_t rem = P.N - t0;
   const int nt = rem <= 0 ? 0 : (rem >= 4 ? 4 : (int)rem);
   const bool live = nt > 0;
+  const bool interior = tb + kTmTok <= P.N && v0 + kTmRows <= P.V;  // block-uniform
   T* Ls = static_cast<T*>(P.L) + (live ? t0 : 0);
   constexpr int M = kTmRows / 4;  // rows per wave
-  typename Raw4<T>::type xs[M];
+  using Raw = typename Raw4<T>::type;
+  const int64_t step = 4 * P.ldL;
+  Raw xs[M];
+  if (interior) {
+    const T* p = Ls + (v0 + w) * P.ldL;
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const int64_t v = v0 + w + 4 * m;
-    xs[m] = {};
-    if (live && v < P.V) xs[m] = load_raw4(Ls + v * P.ldL, nt);
+    for (int m = 0; m < M; ++m) {
+      xs[m] = *reinterpret_cast<const Raw*>(p);
+      p += step;
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const int64_t v = v0 + w + 4 * m;
+      xs[m] = {};
+      if (live && v < P.V) xs[m] = load_raw4(Ls + v * P.ldL, nt);
+    }
   }
   DlmQuad<DIV, T1> q;
   q.init(P, live ? t0 : 0, nt);
   tm.put(tile);
   __syncthreads();
   if (!live) return;
+  if (interior) {
+    T* p = Ls + (v0 + w) * P.ldL;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const int r = w + 4 * m;
+      float x[4], xt[4], ds[4], dt[4];
+      unpack4<T>(xs[m], x);
+      TmTile<T>::read(tile, lane, r, xt);
+      q.row(v0 + r, x, xt, ds, dt);
+      *reinterpret_cast<uint2*>(p) = make_uint2(pack2<T>(ds[0], ds[1]), pack2<T>(ds[2], ds[3]));
+      p += step;
+    }
+    return;
+  }
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     const int r = w + 4 * m;
