@@ -296,8 +296,16 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // A separate teacher's logits (its own GEMM) or precomputed logits of the
     // model dtype are staged into L's teacher columns ahead of the scan, which
     // then runs the student GEMM alone on the ring engine, 256 tokens per
-    // workgroup (16-bit, K > 64, one-pass non-power divergences).
-    pl.f_tl = pl.eb == 2 && pl.H > 64 && pl.fam != FAM_POW &&
+    // workgroup (16-bit, K > 64; one-pass divergences, the power family only
+    // with one power term: with three its per-token state would spill in
+    // every tile).  Staged logits of a computed teacher are rounded to the
+    // compute dtype in L; a power term with a negative student exponent
+    // (chi-squared, Renyi / Amari with alpha > 1) weighs the tail where p_s is
+    // small, where that rounding moves the divergence by ~0.6% (chi-squared at
+    // T = 1, against 1e-4 for the others), so those keep the two-stage scan,
+    // which takes a computed teacher's logits at fp32.
+    const bool pow_ring = pl.npow == 1 && (pl.tsrc == TSRC_MEM || pl.pb[0] >= 0.f);
+    pl.f_tl = pl.eb == 2 && pl.H > 64 && (pl.fam != FAM_POW || pow_ring) &&
               ((pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype) || pl.tsrc == TSRC_SEP);
     // Precomputed 16-bit logits of the compute dtype with V a multiple of 8
     // are not staged at all: the scan (either engine), the two-pass

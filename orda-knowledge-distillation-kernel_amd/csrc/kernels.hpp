@@ -2411,7 +2411,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
         break;                                                                                   \
       }                                                                                          \
       if (P.tsrc == TSRC_L || P.tsrc == TSRC_MEM_RING) {                                         \
-        if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T || SV == SV_POW || SV == SV_POW1) \
+        if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T || SV == SV_POW)                  \
           return hipErrorInvalidValue;                                                           \
         else if (P.tsrc == TSRC_L)                                                               \
           hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_L>), dim3(grid), dim3(kThreads4), 0, s, P); \
