@@ -416,7 +416,7 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // RMSNorm prologue: the chunk's normalised rows, their rsqrt, dloss/dy when
     // dloss/dx is not asked for, and the norm weight's gradient sums
     pl.need_dy = pl.need_gs || pl.need_gnw;
-    pl.norm_groups = (int)std::min<int64_t>(64, cdiv(pl.fn, 8));
+    pl.norm_groups = (int)std::min<int64_t>(128, cdiv(pl.fn, 8));
     pl.off_hn = pl.norm ? carve(fo, (size_t)pl.fnP * pl.H * pl.eb) : 0;
     pl.off_rstd = pl.norm ? carve(fo, (size_t)pl.fnP * 4) : 0;
     pl.off_dy = (pl.need_gnw && !pl.need_gs) ? carve(fo, (size_t)pl.fnP * pl.H * pl.eb) : 0;

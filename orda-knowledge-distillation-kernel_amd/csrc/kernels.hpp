@@ -2342,6 +2342,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_dgamma(NormParams P) {
   const T* dy = static_cast<const T*>(P.dxy);
   const T* x = static_cast<const T*>(P.x);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
   for (int64_t t = t0; t < t1; ++t) {
     float d[4], v[4];
     load4(dy + t * P.H + h, d, true, 4);
@@ -2354,15 +2355,27 @@ __global__ __launch_bounds__(256) void k_rmsnorm_dgamma(NormParams P) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] = acc[e];
 }
+// (32 columns per block, 8 group lanes per column: lane l sums groups l,
+// l + 8, ... in order, then the 8 lane sums are added in order.)
 template <class T>
 __global__ __launch_bounds__(256) void k_rmsnorm_gacc(NormParams P) {
-  const int64_t h = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (h >= P.H) return;
+  __shared__ float red[8][32];
+  const int c = threadIdx.x & 31, gl = threadIdx.x >> 5;
+  const int64_t h = (int64_t)blockIdx.x * 32 + c;
   float s = 0.f;
-  for (int gi = 0; gi < P.groups; ++gi) s += P.gpart[(int64_t)gi * P.H + h];
-  const float a = P.first ? s : P.gacc[h] + s;
-  P.gacc[h] = a;
-  if (P.gout) static_cast<T*>(P.gout)[h] = from_f32<T>(a);
+  if (h < P.H) {
+#pragma unroll 4
+    for (int gi = gl; gi < P.groups; gi += 8) s += P.gpart[(int64_t)gi * P.H + h];
+  }
+  red[gl][c] = s;
+  __syncthreads();
+  if (gl != 0 || h >= P.H) return;
+  float a = red[0][c];
+#pragma unroll
+  for (int k = 1; k < 8; ++k) a += red[k][c];
+  const float tot = P.first ? a : P.gacc[h] + a;
+  P.gacc[h] = tot;
+  if (P.gout) static_cast<T*>(P.gout)[h] = from_f32<T>(tot);
 }
 
 // dloss/dx = r (gamma . dy) - x r^3 <gamma . dy, x> / D, in place over dy
@@ -2598,7 +2611,7 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
       return hipErrorInvalidValue;                                                         \
     hipLaunchKernelGGL(k_rmsnorm_dgamma<T>, dim3((unsigned)((P.H + 1023) / 1024), (unsigned)P.groups), \
                        dim3(256), 0, s, P);                                                \
-    hipLaunchKernelGGL(k_rmsnorm_gacc<T>, dim3((unsigned)((P.H + 255) / 256)), dim3(256), 0, s, P); \
+    hipLaunchKernelGGL(k_rmsnorm_gacc<T>, dim3((unsigned)((P.H + 31) / 32)), dim3(256), 0, s, P); \
     return hipGetLastError();                                                              \
   }                                                                                        \
   template <> hipError_t launch_rmsnorm_bwd<T>(const NormParams& P, hipStream_t s) {       \
