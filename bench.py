@@ -321,10 +321,55 @@ def copy_calibration(mib: int) -> int:
     src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    for _ in range(3):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record()
+    for i in range(3):
         torch.mul(src, 1.0, out=dst)
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes": n, "launches": 3}), flush=True)
+    ms = [ev[i].elapsed_time(ev[i + 1]) for i in (1, 2)]  # (the first launch warms up)
+    gbps = 2 * n / (sum(ms) / 2) / 1e6
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 3, "ms_per_copy": ms,
+                      "copy_gbps": gbps}), flush=True)
+    return 0
+
+
+def library_gemms() -> int:
+    """The config-2 GEMM shapes through torch.mm (hipBLASLt on ROCm) with
+    random bf16 data, as the library GEMM this build's kernels compare with:
+    one json line per shape with ms and TFLOP/s (10 timed calls after 3)."""
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    torch.manual_seed(0)
+    V, H, n = 128256, 4096, 1024
+    dev = "cuda"
+
+    def timed(f, flops, shape):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(10):
+            f()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / 10
+        print(json.dumps({"library_gemm": shape, "ms": ms, "tflops": flops / ms / 1e9}), flush=True)
+
+    L = (torch.randn(V, 2 * n, device=dev) * 1e-3).bfloat16()
+    hT = torch.randn(2 * n, H, device=dev).bfloat16()
+    C = (torch.randn(V, H, device=dev) * 1e-2).bfloat16()
+    timed(lambda: torch.mm(L, hT, out=C), 2.0 * V * H * 2 * n, "grad W store [V x 2n] @ [2n x H]")
+    timed(lambda: C.addmm_(L, hT), 2.0 * V * H * 2 * n, "grad W accumulate (addmm_) [V x 2n] @ [2n x H]")
+    W = (torch.randn(V, H, device=dev) * 0.02).bfloat16()
+    LT = L[:, :n].t()
+    timed(lambda: torch.mm(LT, W), 2.0 * n * V * H, "grad hidden [n x V] @ [V x H]")
+    X = torch.randn(2 * n, H, device=dev).bfloat16()
+    timed(lambda: torch.mm(X, W.t()), 2.0 * V * H * 2 * n, "logits [2n x H] @ [H x V]")
+    A, B = torch.randn(8192, 4096, device=dev).bfloat16(), torch.randn(4096, 4096, device=dev).bfloat16()
+    timed(lambda: torch.mm(A, B), 2.0 * 8192 * 4096 * 4096, "square 8192 x 4096 x 4096")
     return 0
 
 
@@ -412,12 +457,16 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true")
+    ap.add_argument("--library-gemms", action="store_true",
+                    help="instead of the benchmark, time the config-2 GEMM shapes through torch.mm (hipBLASLt) and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 3 plain device copies of MIB MiB (the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings into bytes) and exit")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.library_gemms:
+        return library_gemms()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box has one GPU); "
