@@ -286,6 +286,30 @@ def test_launch_table_drives_the_benchmark_configurations(cfg, entry, chunk, spl
     assert info["forward_workspace_bytes"] == _native.forward_workspace_bytes(_cfg_problem(cfg))
 
 
+# divergence codes of include/orda_ce.h
+_HELLINGER, _RENYI, _CHI2, _L2, _AB = 4, 6, 8, 9, 10
+
+
+@pytest.mark.parametrize("cfg, div, alpha, ring", [
+    ("c3", _HELLINGER, 0.5, True),  # separate teacher: staged logits, ring scan
+    ("c3", _RENYI, 0.5, True),
+    ("c3", _RENYI, 2.0, False),     # negative student exponent over bf16-staged logits
+    ("c3", _CHI2, 0.5, False),
+    ("c3", _L2, 0.5, False),        # three power terms
+    ("c4", _CHI2, 0.5, True),       # precomputed logits read in place: not rounded again
+    ("c4", _AB, 0.5, False),
+])
+def test_power_family_scan_engine(cfg, div, alpha, ring):
+    """The one-term power family runs the ring scan with a staged or in-place
+    teacher; three-term divergences, and a negative student exponent over a
+    computed teacher's logits (staged in bf16), keep the two-stage scan."""
+    p = _cfg_problem(cfg)
+    p.divergence, p.div_alpha, p.div_beta = div, alpha, 0.5
+    info = _native.plan_info(p)
+    assert info["scan_engine"] == (1 if ring else 0)
+    assert info["scan_tokens_per_tile"] == (256 if ring else 128)
+
+
 def test_launch_overrides_and_rule_for_unlisted_shapes():
     p = _cfg_problem("c2")
     p.grad_hidden_splits = 12
