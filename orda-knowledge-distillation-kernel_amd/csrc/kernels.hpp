@@ -1894,12 +1894,40 @@ __global__ __launch_bounds__(256) void k_dlm_tm(DlmParams P) {
 
 // ---------------------------------------------------------------- transpose
 // out[c * ldo + r] = in[r * ldi + c] for r < R, c < C (64 x 64 LDS tiles).
+// 16-bit tiles wholly inside [0, R) x [0, C) with 16-byte aligned rows on
+// both sides (vec) move 16 bytes per access: thread -> rows tid / 8 and
+// tid / 8 + 32, piece tid % 8 (8 columns) on the way in; output rows the same
+// on the way out, each piece gathered from 8 tile rows.
 template <class T>
 __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ in, int64_t ldi, T* __restrict__ out,
-                                                   int64_t ldo, int64_t R, int64_t C, int tiles_c) {
-  __shared__ T tile[64][65];
+                                                   int64_t ldo, int64_t R, int64_t C, int tiles_c, int vec) {
+  __shared__ __align__(16) T tile[64][72];  // (pitch 144 bytes: 16-byte aligned rows)
   const int tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
   const int64_t r0 = (int64_t)tr * 64, c0 = (int64_t)tc * 64;
+  if constexpr (sizeof(T) == 2) {
+    if (vec && r0 + 64 <= R && c0 + 64 <= C) {  // block-uniform
+      const int j = threadIdx.x & 7, i0 = threadIdx.x >> 3;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int i = i0 + 32 * h;
+        *reinterpret_cast<uint4*>(&tile[i][j * 8]) = *reinterpret_cast<const uint4*>(in + (r0 + i) * ldi + c0 + j * 8);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = i0 + 32 * h;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = __builtin_bit_cast(unsigned short, tile[j * 8 + 2 * e][c]);
+          const uint32_t hi = __builtin_bit_cast(unsigned short, tile[j * 8 + 2 * e + 1][c]);
+          w[e] = lo | (hi << 16);
+        }
+        *reinterpret_cast<uint4*>(out + (c0 + c) * ldo + r0 + j * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      return;
+    }
+  }
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int i = ty; i < 64; i += 4) {
     const int64_t r = r0 + i, c = c0 + tx;
@@ -2146,8 +2174,10 @@ template <class T>
 hipError_t launch_transpose(const void* in, int64_t ldi, void* out, int64_t ldo, int64_t R, int64_t C,
                             hipStream_t s) {
   const int tiles_r = (int)((R + 63) / 64), tiles_c = (int)((C + 63) / 64);
+  const int vec = sizeof(T) == 2 && ldi % 8 == 0 && ldo % 8 == 0 && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(out) % 16 == 0;
   hipLaunchKernelGGL(k_transpose<T>, dim3(tiles_r * tiles_c), dim3(256), 0, s, static_cast<const T*>(in), ldi,
-                     static_cast<T*>(out), ldo, R, C, tiles_c);
+                     static_cast<T*>(out), ldo, R, C, tiles_c, vec);
   return hipGetLastError();
 }
 
