@@ -313,7 +313,8 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // token-major (16-byte aligned rows), so L holds only the student's
     // logits and a chunk holds twice the tokens in the same memory (grad W
     // then runs half as many read-modify-write passes with twice the K).
-    pl.f_tmem = pl.eb == 2 && pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype && pl.V % 8 == 0;
+    pl.f_tmem = pl.eb == 2 && pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype && pl.V % 8 == 0 &&
+                pl.V <= 65535LL * 64;  // (k_dlm_tm's grid: one block row per 64 vocabulary rows)
     pl.store_t = pl.tsrc != TSRC_NONE && !pl.f_tmem;
     // no teacher on the scan (student CE only, or a top-k teacher): the ring
     // engine's student-only tiles, 256 tokens per workgroup (16-bit, K > 64)
