@@ -136,6 +136,13 @@ struct AccPair4 {  // ring engine, the lane's token j: acc[mb][j] student, acc[m
   __device__ __forceinline__ float t(int mb, int r) const { return acc_get(a[mb][j + 2], r); }
 };
 
+// Between a tile's two passes over an accessor's values: nothing, except for
+// accessors that convert packed registers on each read (AccPairTL), which
+// fence them so the converted values are formed again instead of kept live
+// across the passes.
+template <class AP>
+__device__ __forceinline__ void acc_fence(const AP&) {}
+
 // Phase 0: online softmax statistics of this lane's token over its 64
 // vocabulary rows of the tile.  Template flags remove work that the problem
 // does not need (NPOW: the power family's terms, 1 or up to 3, P.npow).
@@ -162,6 +169,7 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
       }
     }
   if (MASK && tms == -kInf) return;  // no valid vocabulary row in this lane
+  acc_fence(acc);
 
   // rescale the running state to the new maxima
   const float nms = fmaxf(S.ms, tms);
@@ -552,8 +560,11 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 
 // Teacher logits of the ring scan's student-only tiles (token block nb of the
 // lane: 4 x 16 values, rows as in the accumulator) come in two steps: 16 raw
-// 8-byte loads (issue_teacher4), then unpacking (finish_teacher4), so the
-// next block's loads are in flight while this one is scanned.
+// 8-byte loads (issue_teacher4), then putting them in accumulator order
+// (order_teacher4), so the next block's loads are in flight while this one
+// is scanned.  They stay packed (two 16-bit values per register) and are
+// converted where the scan reads them (AccPairTL), which keeps 32 registers
+// free for the power family's per-token state.
 //  TL_FROM_L: Lout's teacher columns (vocabulary-major): one load holds the
 //    quad's 4 tokens of one row; the in-quad transpose (the inverse of
 //    store_logits4) gives the lane its token's 4 rows.
@@ -564,13 +575,6 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 // tokens past N are never merged).
 enum { TL_NONE = 0, TL_FROM_L = 1, TL_FROM_MEM = 2, TL_STUDENT = 3 };
 
-template <class T>
-__device__ __forceinline__ void unpack_raw4(uint2 r, float (&x)[4]) {
-  union { uint2 u; T e[4]; } v;
-  v.u = r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = to_f32(v.e[i]);
-}
 
 template <class T, int TL>
 __device__ __forceinline__ void issue_teacher4(uint2 (&raw)[16], const FusedParams& P, int64_t v0, int64_t t0,
@@ -599,27 +603,25 @@ __device__ __forceinline__ void issue_teacher4(uint2 (&raw)[16], const FusedPara
     }
   }
 }
+// In place: raw[i] then holds rows 4 (i % 4) .. + 3 of accumulator block
+// i / 4 for the lane's token (element r of block mb: raw[4 mb + r / 4],
+// 16-bit value r % 4).
 template <class T, int TL>
-__device__ __forceinline__ void finish_teacher4(const uint2 (&raw)[16], f32x16 (&tv)[4]) {
+__device__ __forceinline__ void order_teacher4(uint2 (&raw)[16]) {
+  if constexpr (TL == TL_FROM_L) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    uint2 r = raw[i];
-    if constexpr (TL == TL_FROM_L) {
-      const uint32_t x[2] = {r.x, r.y};
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t x[2] = {raw[i].x, raw[i].y};
       uint32_t o[2];
       quad_transpose16(x, o);
-      r = make_uint2(o[0], o[1]);
+      raw[i] = make_uint2(o[0], o[1]);
     }
-    float x[4];
-    unpack_raw4<T>(r, x);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) tv[i >> 2][(i & 3) * 4 + e] = x[e];
   }
 }
-// Token block nb's teacher logits (registers, accumulator layout) to Lout's
-// teacher columns, as store_logits4 writes a tied teacher's.
+// Token block nb's teacher logits (ordered raw registers) to Lout's teacher
+// columns, as store_logits4 writes a tied teacher's.
 template <class T>
-__device__ __forceinline__ void store_teacher4(const f32x16 (&tv)[4], const FusedParams& P, int64_t v0, int64_t t0,
+__device__ __forceinline__ void store_teacher4(const uint2 (&tr)[16], const FusedParams& P, int64_t v0, int64_t t0,
                                                int nb) {
   const int lane = opaque_lane();
   const int wm = w4_m(), wn = w4_n();
@@ -630,9 +632,7 @@ __device__ __forceinline__ void store_teacher4(const f32x16 (&tv)[4], const Fuse
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane) + q;
-    const f32x16& t = tv[i >> 2];
-    const int e0 = (i & 3) * 4;
-    const uint32_t x[2] = {pack2<T>(t[e0], t[e0 + 1]), pack2<T>(t[e0 + 2], t[e0 + 3])};
+    const uint32_t x[2] = {tr[i].x, tr[i].y};
     uint32_t o[2];
     quad_transpose16(x, o);
     if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + P.tcolL + tb) = make_uint2(o[0], o[1]);
@@ -644,13 +644,24 @@ struct AccPairS {  // student only: accumulator block nb (the teacher accessor i
   __device__ __forceinline__ float s(int mb, int r) const { return acc_get(a[mb][nb], r); }
   __device__ __forceinline__ float t(int, int) const { return 0.f; }
 };
-struct AccPairTL {  // student from accumulator block nb, teacher from registers
+template <class T>
+struct AccPairTL {  // student from accumulator block nb, teacher from ordered raw registers
   const Acc4& a;
   int nb;
-  const f32x16 (&tv)[4];
+  const uint2 (&tr)[16];
   __device__ __forceinline__ float s(int mb, int r) const { return acc_get(a[mb][nb], r); }
-  __device__ __forceinline__ float t(int mb, int r) const { return tv[mb][r]; }
+  __device__ __forceinline__ float t(int mb, int r) const {
+    const uint2& u = tr[mb * 4 + (r >> 2)];
+    const uint32_t w = (r & 2) ? u.y : u.x;
+    return (r & 1) ? hi16<T>(w) : lo16<T>(w);
+  }
 };
+template <class T>
+__device__ __forceinline__ void acc_fence(const AccPairTL<T>& p) {
+  uint2* r = const_cast<uint2*>(p.tr);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(r[i].x), "+v"(r[i].y));
+}
 
 // k_scan on the four-wave ring engine for 16-bit operands: the same
 // workgroup -> (tokens, vocabulary range) mapping and partial output.  The B
@@ -751,12 +762,12 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
       static_for<0, NJ>([&](auto J) {
         constexpr int j = decltype(J)::value;
         if constexpr (j + 1 < NJ) issue_teacher4<T, TL>(raw[(j + 1) & 1], P, x.v0, t0, j + 1);
-        f32x16 tv[4];
-        finish_teacher4<T, TL>(raw[j & 1], tv);
+        order_teacher4<T, TL>(raw[j & 1]);
         if constexpr (TL == TL_FROM_MEM) {
-          if (P.store_t) store_teacher4<T>(tv, P, x.v0, t0, j);  // else the dlogits pass reads them in place
+          if (P.store_t) store_teacher4<T>(raw[j & 1], P, x.v0, t0, j);  // else the dlogits pass reads them in place
         }
-        scan_variant<SV>(st[j], AccPairTL{c, j, tv}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+        scan_variant<SV>(st[j], AccPairTL<T>{c, j, raw[j & 1]}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j],
+                         P);
       });
     } else {
       if constexpr (STORE) store_logits4<T, false>(c, P, x.v0, t0);
