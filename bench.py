@@ -111,7 +111,7 @@ def algorithmic_flops(cfg) -> float:
 
 
 def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=None, student_norm=False,
-            logits_gemm="default"):
+            logits_gemm="default", teacher_logits_fp32=False):
     import torch
 
     import orda_ce_kernel as orda
@@ -134,6 +134,8 @@ def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=N
     elif mode == "topk":
         teacher = orda.TopKTeacher(*lt)
     else:
+        if teacher_logits_fp32:  # the same log-probs held in float32 (cast to the compute dtype per chunk)
+            lt = lt.float()
         teacher = orda.PrecomputedTeacher(logits=lt)
     norm = None
     if student_norm:
@@ -454,6 +456,8 @@ def main() -> int:
                     help="fuse the student's final RMSNorm in front of the loss (StudentRMSNorm)")
     ap.add_argument("--logits-gemm", default="default", choices=("default", "fp8"),
                     help="fp8: the logits GEMM on e4m3 operands (its own tolerance; not the headline number)")
+    ap.add_argument("--teacher-logits-fp32", action="store_true",
+                    help="precomputed configurations: hold the teacher's logits in float32 (an input-format variant)")
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true")
@@ -487,7 +491,8 @@ def main() -> int:
     mode, N, H, Ht, V, dtype_name, div, T, w_s, w_t, kl_w, ignore_frac = cfg
     ms_step, peak_extra, loss_val, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, not args.no_timing,
                                                  row_tau, chunk=args.chunk, splits=args.splits,
-                                                 student_norm=args.student_norm, logits_gemm=args.logits_gemm)
+                                                 student_norm=args.student_norm, logits_gemm=args.logits_gemm,
+                                                 teacher_logits_fp32=args.teacher_logits_fp32)
     peak = PEAK_FP32_TFLOPS if dtype_name == "float32" else PEAK_BF16_TFLOPS
     alg = algorithmic_flops(cfg)
     step_tflops = alg / (ms_step / 1e3) / 1e12
@@ -512,7 +517,8 @@ def main() -> int:
                         + f", vocab={V}, {div}, T={T}, fwd+bwd (grad hidden + grad W)"
                         + (f", top-{TOPK} teacher" if mode == "topk" else "")
                         + (", student RMSNorm fused (grad x + grad norm weight)" if args.student_norm else "")
-                        + (", fp8 (e4m3) logits GEMM" if args.logits_gemm == "fp8" else ""),
+                        + (", fp8 (e4m3) logits GEMM" if args.logits_gemm == "fp8" else "")
+                        + (", teacher logits held in float32" if args.teacher_logits_fp32 else ""),
             "tokens": N, "hidden": H, "vocab": V, "teacher": mode, "divergence": div, "temperature": T,
             "student_ce_weight": w_s, "teacher_ce_weight": w_t, "kl_weight": kl_w, "ignore_frac": ignore_frac,
         },

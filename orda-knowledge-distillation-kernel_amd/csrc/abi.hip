@@ -293,8 +293,9 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // precomputed teachers: no teacher gradient; their logits (memory or the
     // frozen teacher GEMM) are stored next to the student's like a tied
     // teacher's
-    // A separate teacher's logits (its own GEMM) or precomputed logits of the
-    // model dtype are staged into L's teacher columns ahead of the scan, which
+    // A separate teacher's logits (its own GEMM) or precomputed logits (cast
+    // to the compute dtype when they have another) are staged into L's
+    // teacher columns ahead of the scan, which
     // then runs the student GEMM alone on the ring engine, 256 tokens per
     // workgroup (16-bit, K > 64; one-pass divergences, the power family only
     // with one power term: with three its per-token state would spill in
@@ -306,7 +307,7 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // which takes a computed teacher's logits at fp32.
     const bool pow_ring = pl.npow == 1 && (pl.tsrc == TSRC_MEM || pl.pb[0] >= 0.f);
     pl.f_tl = pl.eb == 2 && pl.H > 64 && (pl.fam != FAM_POW || pow_ring) &&
-              ((pl.tsrc == TSRC_MEM && p->logits_dtype == p->dtype) || pl.tsrc == TSRC_SEP);
+              (pl.tsrc == TSRC_MEM || pl.tsrc == TSRC_SEP);
     // Precomputed 16-bit logits of the compute dtype with V a multiple of 8
     // are not staged at all: the scan (either engine), the two-pass
     // divergences' second pass and the dlogits pass all read them in place,
@@ -841,13 +842,20 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       // the chunk's teacher logits go to L[:, nP + t] (vocabulary-major) ahead
       // of the scan (teacher GEMM, transpose) or through it
       char* Lt = L + nP * eb;
-      if (pl.f_tmem || (pl.tsrc == TSRC_MEM && V % 4 == 0 && reinterpret_cast<uintptr_t>(t->teacher_logits) % 8 == 0)) {
+      const bool same_dtype = p->logits_dtype == p->dtype;
+      if (pl.f_tmem || (pl.tsrc == TSRC_MEM && same_dtype && V % 4 == 0 &&
+                        reinterpret_cast<uintptr_t>(t->teacher_logits) % 8 == 0)) {
         // read token-major by the scan itself (8-byte loads of 4 rows), which
         // writes them to L on the way
         F.tsrc = TSRC_MEM_RING;
-      } else if (pl.tsrc == TSRC_MEM) {
+      } else if (pl.tsrc == TSRC_MEM && same_dtype) {
         Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
         ORDA_CHECK_LAUNCH(launch_transpose<T>(Ltc, V, Lt, ldL, nc, V, s));
+      } else if (pl.tsrc == TSRC_MEM) {
+        // logits of another dtype: cast to the compute dtype on the way into
+        // L, as the reference casts each chunk (ops/precomputed_teacher.py:343-348)
+        Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+        ORDA_CHECK_LAUNCH(launch_transpose_cast<T>(Ltc, p->logits_dtype, V, Lt, ldL, nc, V, s));
       } else {
         ORDA_TRY(gemm2<T>(KMAJ, KMAJ, Wt, Ht, ht + r0 * Ht, Ht, nullptr, 0, Ht, Ht, 0, Lt, nullptr, ldL, V, nc, Ht,
                           GEMM_STORE, 1, 0, s, ORDA_K_SCAN, 2.0 * (double)nc * (double)V * (double)Ht));

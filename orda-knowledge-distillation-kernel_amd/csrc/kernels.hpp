@@ -113,6 +113,10 @@ __device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][2], char* lds, con
 #pragma unroll
               for (int e = 0; e < 4; ++e) x[e] = (v + e < P.V) ? (float)src[e] : 0.f;
             }
+            // logits of another dtype as the compute dtype T holds them (the
+            // reference casts them per chunk; exact when the dtypes agree)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = to_f32(from_f32<T>(x[e]));
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[mb][1][g * 4 + e] = x[e];
           }
@@ -1951,6 +1955,59 @@ __global__ __launch_bounds__(256) void k_transpose(const T* __restrict__ in, int
   }
 }
 
+// out[c * ldo + r] = (TO) in[r * ldi + c] for logits of another dtype TI
+// (fp32 or the other 16-bit type), rounded once to the compute dtype TO, as
+// the reference's per-chunk cast of precomputed teacher logits does
+// (ops/precomputed_teacher.py:343-348).  fp32 into a 16-bit TO moves 16
+// bytes per access in full tiles with 16-byte aligned rows: thread -> rows
+// tid / 16 + 16 h (h < 4), 4 columns tid % 16 on the way in (converted into
+// LDS); the way out as k_transpose's 16-bit path.
+template <class TI, class TO>
+__global__ __launch_bounds__(256) void k_transpose_cast(const TI* __restrict__ in, int64_t ldi, TO* __restrict__ out,
+                                                        int64_t ldo, int64_t R, int64_t C, int tiles_c, int vec) {
+  __shared__ __align__(16) TO tile[64][72];
+  const int tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
+  const int64_t r0 = (int64_t)tr * 64, c0 = (int64_t)tc * 64;
+  if constexpr (sizeof(TI) == 4 && sizeof(TO) == 2) {
+    if (vec && r0 + 64 <= R && c0 + 64 <= C) {  // block-uniform
+      {
+        const int j = threadIdx.x & 15, i0 = threadIdx.x >> 4;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int i = i0 + 16 * h;
+          const float4 v = *reinterpret_cast<const float4*>(in + (r0 + i) * ldi + c0 + j * 4);
+          *reinterpret_cast<uint2*>(&tile[i][j * 4]) = make_uint2(pack2<TO>(v.x, v.y), pack2<TO>(v.z, v.w));
+        }
+      }
+      __syncthreads();
+      const int j = threadIdx.x & 7, i0 = threadIdx.x >> 3;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = i0 + 32 * h;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = __builtin_bit_cast(unsigned short, tile[j * 8 + 2 * e][c]);
+          const uint32_t hi = __builtin_bit_cast(unsigned short, tile[j * 8 + 2 * e + 1][c]);
+          w[e] = lo | (hi << 16);
+        }
+        *reinterpret_cast<uint4*>(out + (c0 + c) * ldo + r0 + j * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      return;
+    }
+  }
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    if (r < R && c < C) tile[i][tx] = from_f32<TO>(to_f32(in[r * ldi + c]));
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t c = c0 + i, r = r0 + tx;
+    if (r < R && c < C) out[c * ldo + r] = tile[tx][i];
+  }
+}
+
 // ------------------------------------------------------------ label logits
 // x_s[t, y_t] and x_t[t, y_t] (the logits at each row's label) as fp32 dot
 // products, one wave per row: 16-byte loads (8 bf16/f16 or 4 fp32 per lane)
@@ -2077,6 +2134,7 @@ __global__ __launch_bounds__(256) void k_label(LabelParams P) {
       if (P.lt_dtype == DT_F32) xt = static_cast<const float*>(P.Lt)[off];
       else if (P.lt_dtype == DT_BF16) xt = (float)static_cast<const bf16*>(P.Lt)[off];
       else xt = (float)static_cast<const f16*>(P.Lt)[off];
+      xt = to_f32(from_f32<T>(xt));  // as the compute dtype holds it
     }
     P.out[t] = xs;
     P.out[P.N + t] = xt;
@@ -2189,6 +2247,31 @@ hipError_t launch_transpose(const void* in, int64_t ldi, void* out, int64_t ldo,
                   reinterpret_cast<uintptr_t>(out) % 16 == 0;
   hipLaunchKernelGGL(k_transpose<T>, dim3(tiles_r * tiles_c), dim3(256), 0, s, static_cast<const T*>(in), ldi,
                      static_cast<T*>(out), ldo, R, C, tiles_c, vec);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_transpose_cast(const void* in, int in_dtype, int64_t ldi, void* out, int64_t ldo, int64_t R,
+                                 int64_t C, hipStream_t s) {
+  const int tiles_r = (int)((R + 63) / 64), tiles_c = (int)((C + 63) / 64);
+  const dim3 grid((unsigned)(tiles_r * tiles_c));
+  const int vec = ldi % 4 == 0 && ldo % 8 == 0 && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  switch (in_dtype) {
+    case DT_F32:
+      hipLaunchKernelGGL((k_transpose_cast<float, T>), grid, dim3(256), 0, s, static_cast<const float*>(in), ldi,
+                         static_cast<T*>(out), ldo, R, C, tiles_c, vec);
+      break;
+    case DT_BF16:
+      hipLaunchKernelGGL((k_transpose_cast<bf16, T>), grid, dim3(256), 0, s, static_cast<const bf16*>(in), ldi,
+                         static_cast<T*>(out), ldo, R, C, tiles_c, 0);
+      break;
+    case DT_F16:
+      hipLaunchKernelGGL((k_transpose_cast<f16, T>), grid, dim3(256), 0, s, static_cast<const f16*>(in), ldi,
+                         static_cast<T*>(out), ldo, R, C, tiles_c, 0);
+      break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -2751,6 +2834,8 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
   template hipError_t launch_gemm<T>(const GemmParams&, hipStream_t);                                \
   template hipError_t launch_label<T>(const LabelParams&, hipStream_t);                              \
   template hipError_t launch_transpose<T>(const void*, int64_t, void*, int64_t, int64_t, int64_t,    \
-                                          hipStream_t);
+                                          hipStream_t);                                              \
+  template hipError_t launch_transpose_cast<T>(const void*, int, int64_t, void*, int64_t, int64_t, int64_t, \
+                                               hipStream_t);
 
 }  // namespace orda

@@ -220,6 +220,10 @@ template <class T> hipError_t launch_scale(void* x, int64_t n, const float* g, h
 template <class T>
 hipError_t launch_transpose(const void* in, int64_t ldi, void* out, int64_t ldo, int64_t R, int64_t C,
                             hipStream_t s);
+// The same for logits of dtype in_dtype (DT_*), rounded once to T.
+template <class T>
+hipError_t launch_transpose_cast(const void* in, int in_dtype, int64_t ldi, void* out, int64_t ldo, int64_t R,
+                                 int64_t C, hipStream_t s);
 
 // dtype-independent kernels (rows.hip)
 struct MergeParams {

@@ -70,11 +70,10 @@ def _forward(ctx, student_hidden, weight, logits_teacher, labels, student_ce_wei
         compute_teacher_ce=float(teacher_ce_weight) != 0.0,
         need_grad_student_hidden=student_hidden.requires_grad,
         need_grad_weight=weight.requires_grad,
-        # gradients inside forward store the teacher's logits in the compute
-        # dtype: only when that loses nothing (given logits of another dtype
-        # take the two-phase schedule, which reads them as given)
-        grads_in_forward=(grads_in_forward(mode, use_fp32_accum, divergence, ctx.compute_grad)
-                          and (logits_teacher is None or logits_teacher.dtype == dtype)),
+        # (logits of another dtype are taken as the compute dtype holds them
+        # in either schedule, as the reference casts each chunk,
+        # ops/precomputed_teacher.py:343-348)
+        grads_in_forward=grads_in_forward(mode, use_fp32_accum, divergence, ctx.compute_grad),
         token_chunk=token_chunk_for(chunk_size),
     )
     loss, ce_s, ce_t, kl = fused_forward(ctx, call)

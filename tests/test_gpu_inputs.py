@@ -4,9 +4,9 @@
   reference tests them (``test/correctness/test_public_api_cuda.py:397-504``:
   BT=16, Hs=32, Ht=48, V=257, fp16, every 4th label ignored, T=1.4,
   chunk_size=7); here with the divergence term isolated as well;
-* precomputed teacher logits in float32 with a bf16 student (the two-phase
-  schedule reads them as given; the reference casts them to the compute
-  dtype first, ``ops/precomputed_teacher.py:340-348``);
+* precomputed teacher logits in float32 with a bf16 student, in both
+  schedules: taken as the compute dtype holds them, as the reference casts
+  them to the compute dtype first (``ops/precomputed_teacher.py:340-348``);
 * autocast to bf16 / fp16 around float32 inputs (compute dtype from the
   autocast, ``_runtime.py:41-80``; gradients come back in float32);
 * a second backward through a retained graph (and ``autograd.grad`` then
@@ -114,22 +114,34 @@ def test_noncontiguous_inputs(mode, isolated):
         _check_grad(t.grad, ref[key], dtype, f"{mode} {key}")
 
 
+@pytest.mark.parametrize("profile", ["balanced", "debug"], ids=["grads_in_forward", "two_phase"])
 @pytest.mark.parametrize("div, T", [("forward_kl", 1.0), ("reverse_kl", 2.0), ("jsd", 2.0), ("hellinger", 4.0),
                                     ("tvd", 1.0)])
-def test_float32_teacher_logits_with_bf16_student(div, T):
-    """fp32 logits and a bf16 student: the teacher is read in fp32 (no cast),
-    the student runs in bf16.  Divergence term isolated, and all terms."""
+def test_float32_teacher_logits_with_bf16_student(div, T, profile):
+    """fp32 logits and a bf16 student: the teacher's logits are taken as the
+    compute dtype holds them -- the reference casts each chunk into a bf16
+    buffer (ops/precomputed_teacher.py:343-348) -- in both schedules (the
+    default one stages them through a cast-transpose), the student runs in
+    bf16.  Against the oracle on the bf16-rounded logits, and within the loss
+    tolerance of the unrounded ones (the reference's unfused torch path keeps
+    them in fp32).  Divergence term isolated, and all terms."""
     o = _orda()
     hs, W, _, hts, Wt, y = D.make_inputs(29, torch.bfloat16, n=200)
     lt = hts.float() @ Wt.float().t()  # float32, not representable in bf16
+    lt16 = lt.to(torch.bfloat16)
     for w_s, kl_w in ((0.0, 1.0), (0.7, 0.5)):
         hs_d, W_d = hs.cuda().requires_grad_(True), W.cuda().requires_grad_(True)
         out = o.distillation_loss(hs_d, W_d, y.cuda(), o.PrecomputedTeacher(logits=lt.cuda()), student_ce_weight=w_s,
-                                  kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div)
+                                  kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div,
+                                  profile=profile)
         out.loss.backward()
         torch.cuda.synchronize()
-        ref = distillation_loss_oracle("precomputed", _np(hs), _np(W), y.numpy(), teacher_logits=_np(lt),
-                                       student_ce_weight=w_s, kl_weight=kl_w, kl_temperature=T, divergence=div)
+        kw = dict(student_ce_weight=w_s, kl_weight=kl_w, kl_temperature=T, divergence=div)
+        exact = distillation_loss_oracle("precomputed", _np(hs), _np(W), y.numpy(), teacher_logits=_np(lt), **kw)
+        for key in ("loss", "kl"):
+            got = float(getattr(out, key).detach())
+            assert abs(got - exact[key]) <= 1e-3 * abs(exact[key]) + 1e-5, (key, got, exact[key])
+        ref = distillation_loss_oracle("precomputed", _np(hs), _np(W), y.numpy(), teacher_logits=_np(lt16), **kw)
         _check_scalars(out, ref, div)
         _check_grad(hs_d.grad, ref["grad_student_hidden"], torch.bfloat16, f"{div} grad_student_hidden", div)
         _check_grad(W_d.grad, ref["grad_weight"], torch.bfloat16, f"{div} grad_weight", div)
