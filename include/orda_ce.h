@@ -175,7 +175,9 @@ typedef struct orda_tensors {
                                 * ORDA_GRADS_IN_FORWARD, a 16-bit compute dtype
                                 * and V a multiple of 8 they are read in place
                                 * and must be 16-byte aligned (else
-                                * ORDA_EINVAL)                                */
+                                * ORDA_EINVAL); logits of another dtype than
+                                * the compute dtype are used rounded to it
+                                * (ops/precomputed_teacher.py:343-348)        */
   const int64_t* labels;       /* [N]                                        */
   /* forward outputs: fp32 scalars */
   float* out_loss;
