@@ -1646,8 +1646,8 @@ __global__ __launch_bounds__(256) void k_two_rows(TwoParams P) {
 // precomputed [N x ldtm] tensor (token-major): the block walks its range in
 // tiles of kTmRows rows; per tile the teacher's kTmTok x kTmRows block is
 // staged in LDS by token quads (TmTile) and wave w takes rows w, w + 4, ...
-// of it beside the student's 8-byte loads from L, all of a tile's loads
-// issued before its staging barrier.  Same partial pairs and fixed-order
+// of it beside the student's 8-byte loads from L, the next tile's loads
+// issued while this tile is summed.  Same partial pairs and fixed-order
 // reduction as k_two_rows; rows_per_range a multiple of kTmRows.
 template <class T, int DIV>
 __global__ __launch_bounds__(256) void k_two_rows_tm(TwoParams P) {
@@ -1675,9 +1675,12 @@ __global__ __launch_bounds__(256) void k_two_rows_tm(TwoParams P) {
   TmTile<T> tm;
   using Raw = typename Raw4<T>::type;
   const bool full_tok = tb + kTmTok <= P.N;  // block-uniform
-  for (int64_t vb = v0; vb < v1; vb += kTmRows) {
+  Raw xs[M];
+  // one tile's loads (teacher block and the student's rows), issued for the
+  // next tile right after this tile's staging, so they are in flight during
+  // this tile's arithmetic
+  auto load = [&](int64_t vb) {
     tm.load(Tm, P.ldtm, tb, vb, P.N, P.V);
-    Raw xs[M];
     if (full_tok && vb + kTmRows <= v1) {  // no per-row guards
       const T* p = Ls + (vb + w) * P.ldL;
 #pragma unroll
@@ -1693,16 +1696,23 @@ __global__ __launch_bounds__(256) void k_two_rows_tm(TwoParams P) {
         if (nt > 0 && v < v1) xs[m] = load_raw4(Ls + v * P.ldL, nt);
       }
     }
+  };
+  if (v0 < v1) load(v0);
+  for (int64_t vb = v0; vb < v1; vb += kTmRows) {
     __syncthreads();  // the previous tile's LDS reads are done
     tm.put(tile);
+    Raw cs[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) cs[m] = xs[m];
     __syncthreads();
+    if (vb + kTmRows < v1) load(vb + kTmRows);
     if (nt == 0) continue;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const int r = w + 4 * m;
       if (vb + r >= v1) break;
       float xsf[4], xt[4];
-      unpack4<T>(xs[m], xsf);
+      unpack4<T>(cs[m], xsf);
       TmTile<T>::read(tile, lane, r, xt);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
