@@ -147,6 +147,30 @@ def test_float32_teacher_logits_with_bf16_student(div, T, profile):
         _check_grad(W_d.grad, ref["grad_weight"], torch.bfloat16, f"{div} grad_weight", div)
 
 
+@pytest.mark.parametrize("logits_dtype", [torch.bfloat16, torch.float32], ids=["bf16_logits", "f32_logits"])
+@pytest.mark.parametrize("profile", ["balanced", "debug"], ids=["grads_in_forward", "two_phase"])
+def test_teacher_logits_cast_to_an_f16_student(logits_dtype, profile):
+    """An fp16 student with bf16 or fp32 teacher logits: the logits are
+    rounded to fp16 (the compute dtype), as the reference's per-chunk cast
+    does, on the element path of the cast-transpose (bf16 into fp16) and its
+    16-byte path (fp32 into fp16)."""
+    o = _orda()
+    hs, W, _, hts, Wt, y = D.make_inputs(37, torch.float16, n=300, v=1032)
+    lt = (hts.float() @ Wt.float().t()).to(logits_dtype)
+    lt16 = lt.to(torch.float16)
+    hs_d, W_d = hs.cuda().requires_grad_(True), W.cuda().requires_grad_(True)
+    out = o.distillation_loss(hs_d, W_d, y.cuda(), o.PrecomputedTeacher(logits=lt.cuda()), student_ce_weight=0.5,
+                              kl_weight=1.0, kl_temperature=2.0, backend="triton", divergence="forward_kl",
+                              profile=profile)
+    out.loss.backward()
+    torch.cuda.synchronize()
+    ref = distillation_loss_oracle("precomputed", _np(hs), _np(W), y.numpy(), teacher_logits=_np(lt16),
+                                   student_ce_weight=0.5, kl_weight=1.0, kl_temperature=2.0, divergence="forward_kl")
+    _check_scalars(out, ref, f"{logits_dtype} {profile}")
+    _check_grad(hs_d.grad, ref["grad_student_hidden"], torch.float16, "grad_student_hidden")
+    _check_grad(W_d.grad, ref["grad_weight"], torch.float16, "grad_weight")
+
+
 @pytest.mark.parametrize("ac_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("mode", ["tied", "separate", "precomputed-logits"])
 def test_autocast_sets_the_compute_dtype(mode, ac_dtype):
