@@ -406,7 +406,7 @@ TABLE_SWEEP = {
     "c2": [(c, s) for c in (256, 512) for s in (4, 8, 12, 16)],
     "c3": [(c, s) for c in (512, 1024) for s in (4, 8, 16)],
     "c4": [(c, s) for c in (256, 512) for s in (2, 4, 8)],
-    "c5": [(c, s) for c in (512, 1024) for s in (8, 16)],
+    "c5": [(256, 16), (512, 4), (512, 8), (512, 16), (1024, 8)],
 }
 
 

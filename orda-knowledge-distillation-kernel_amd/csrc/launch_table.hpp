@@ -61,9 +61,11 @@ constexpr LaunchEntry kLaunchTable[] = {
     // 2048-token chunks: 25.7 ms/step vs 27.8 with 1024; split 2 = 4 within noise,
     // 67 MB less split-K scratch
     {TC_INPLACE, 0, 128256, 4096, 4, 2, 256, "c4: chunk 512 x 4, split 2"},
-    // config 5: tied, N = 32768, H = 5120, V = 152064.  16 splits fill whole
-    // rounds (80 tiles x 16 = 5 x 256): 240.3 ms/step vs 241.9 (12), 245.5 (8)
-    {TC_TIED, 0, 152064, 5120, 2, 16, 256, "c5: chunk 512 x 2, split 16"},
+    // config 5: tied, N = 32768, H = 5120, V = 152064 (no memory ceiling
+    // beyond reporting it).  2048-token chunks, 8 splits (160 tiles x 8 = 5
+    // full rounds of 256): 216.4 ms/step, peak extra 3.52 GB, vs 229.4 with
+    // 1024-token chunks and 16 splits (2.88 GB); 4 splits 224.5, 16 218.2
+    {TC_TIED, 0, 152064, 5120, 4, 8, 256, "c5: chunk 512 x 4, split 8"},
 };
 constexpr int kLaunchTableSize = (int)(sizeof(kLaunchTable) / sizeof(kLaunchTable[0]));
 

@@ -270,7 +270,7 @@ def _cfg_problem(cfg):
 
 
 @pytest.mark.parametrize("cfg, entry, chunk, splits, tclass", [
-    ("c2", 0, 1024, 4, 0), ("c3", 1, 2048, 4, 1), ("c4", 2, 2048, 2, 2), ("c5", 3, 1024, 16, 0)])
+    ("c2", 0, 1024, 4, 0), ("c3", 1, 2048, 4, 1), ("c4", 2, 2048, 2, 2), ("c5", 3, 2048, 8, 0)])
 def test_launch_table_drives_the_benchmark_configurations(cfg, entry, chunk, splits, tclass):
     """Each benchmark configuration finds its row of the gfx950 launch table
     (csrc/launch_table.hpp) and takes its chunk scale and split count."""
