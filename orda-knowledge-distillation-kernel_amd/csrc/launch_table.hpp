@@ -50,16 +50,17 @@ struct LaunchEntry {
 // dtype 0 = bf16 (orda_dtype).
 constexpr LaunchEntry kLaunchTable[] = {
     // config 2: tied, N = 8192, H = 4096, V = 128256.  1024-token chunks
-    // (2048 would pass the 2 GB memory ceiling); 4 splits: 41.5 ms/step vs
-    // 41.8-42.2 for 8-16 and 46.2-49.1 with 512-token chunks
+    // (2048 would pass the 2 GB memory ceiling); 4 splits: 38.7 ms/step vs
+    // 38.9-39.3 for 8-16 and 42.5-45.3 with 512-token chunks
     {TC_TIED, 0, 128256, 4096, 2, 4, 256, "c2: chunk 512 x 2, split 4"},
     // config 3: separate, Hs = 2048 (teacher 4096), V = 128256.  2048-token
-    // chunks: 22.6 ms/step vs 24.3 with 1024 (grad W K twice as deep); 4
-    // splits (8, 16 within noise, more scratch)
+    // chunks: 20.9 ms/step at 1.69 GB peak extra (4096-token chunks: 20.3 at
+    // 2.82 GB, past the 2 GB the tied config keeps to); 4 splits (8, 16
+    // within noise, more scratch)
     {TC_STAGED, 0, 128256, 2048, 4, 4, 256, "c3: chunk 512 x 4, split 4"},
     // config 4: precomputed logits read in place, H = 4096, V = 128256.
-    // 2048-token chunks: 25.7 ms/step vs 27.8 with 1024; split 2 = 4 within noise,
-    // 67 MB less split-K scratch
+    // 2048-token chunks: 24.0 ms/step vs 25.8-30.2 with 1024; split 2 = 4
+    // within noise, 67 MB less split-K scratch
     {TC_INPLACE, 0, 128256, 4096, 4, 2, 256, "c4: chunk 512 x 4, split 2"},
     // config 5: tied, N = 32768, H = 5120, V = 152064 (no memory ceiling
     // beyond reporting it).  2048-token chunks, 8 splits (160 tiles x 8 = 5
