@@ -198,6 +198,22 @@ def test_ragged_shapes_and_padding():
         _check(out, ref, hs, W, torch.bfloat16)
 
 
+@pytest.mark.parametrize("profile", ["balanced", "debug"])
+@pytest.mark.parametrize("div", ["reverse_kl", "jsd", "hellinger"])
+@pytest.mark.parametrize("mode", ["separate", "precomputed_logits", "precomputed_hidden"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_ragged_shapes_every_teacher_mode(dtype, mode, div, profile):
+    """The ragged shapes above for the teachers that are not tied: a single
+    token, vocabularies below one tile and not a multiple of 4 (teacher
+    logits staged by transposition), hidden sizes the host pads, teacher
+    hidden sizes that differ from the student's; a one-pass, a two-pass and a
+    power-family divergence; both schedules."""
+    for N, H, Ht, V in ((9, 36, 44, 17), (130, 40, 24, 257), (1, 8, 16, 5)):
+        out, ref, hs, W, _ = _run(mode, dtype, N=N, H=H, Ht=Ht, V=V, T=1.4, div=div, kl_w=1.0, ignore_frac=0.0,
+                                  profile=profile)
+        _check(out, ref, hs, W, dtype)
+
+
 def test_grad_output_scaling():
     out, ref, hs, W, _ = _run("tied", torch.bfloat16, grad_output=3.5, reduction="sum")
     _check(out, ref, hs, W, torch.bfloat16)
