@@ -7,6 +7,9 @@
 * precomputed teacher logits in float32 with a bf16 student, in both
   schedules: taken as the compute dtype holds them, as the reference casts
   them to the compute dtype first (``ops/precomputed_teacher.py:340-348``);
+* precomputed teacher log-probs with part of the vocabulary masked to a
+  large finite negative value, for every divergence and each way the
+  teacher's logits reach the kernels;
 * autocast to bf16 / fp16 around float32 inputs (compute dtype from the
   autocast, ``_runtime.py:41-80``; gradients come back in float32);
 * a second backward through a retained graph (and ``autograd.grad`` then
@@ -169,6 +172,44 @@ def test_teacher_logits_cast_to_an_f16_student(logits_dtype, profile):
     _check_scalars(out, ref, f"{logits_dtype} {profile}")
     _check_grad(hs_d.grad, ref["grad_student_hidden"], torch.float16, "grad_student_hidden")
     _check_grad(W_d.grad, ref["grad_weight"], torch.float16, "grad_weight")
+
+
+DIVS = [
+    "forward_kl", "reverse_kl", "symmetric_kl", "soft_target_ce", "hellinger", "bhattacharyya", "renyi",
+    "amari_alpha", "chi_squared", "squared_l2", "ab", "jsd", "skew_forward_kl", "skew_reverse_kl", "tvd",
+]
+
+
+@pytest.mark.parametrize("profile, V", [("balanced", 1032), ("balanced", 1028), ("balanced", 1030), ("debug", 1032)],
+                         ids=["in_place", "staged_ring", "staged_transposed", "two_phase"])
+@pytest.mark.parametrize("T", [1.0, 4.0])
+@pytest.mark.parametrize("div", DIVS)
+def test_masked_teacher_vocabulary(div, T, profile, V):
+    """Precomputed teacher log-probs with 30% of each row masked to a finite
+    -1e4 (how a teacher that rules tokens out stores them in a 16-bit
+    tensor): those entries carry no teacher mass (their exponentials
+    underflow to 0 inside the kernels' sums), every divergence stays finite
+    and matches the oracle on the same bf16 values; divergence term isolated
+    (no student CE).  V picks how the teacher's logits reach the passes
+    after the scan: read in place (V % 8 == 0), copied into the chunk buffer
+    by the scan that reads them token-major (V % 4 == 0), or transposed into
+    the chunk buffer ahead of the scan."""
+    o = _orda()
+    hs, W, _, hts, Wt, y = D.make_inputs(43, torch.bfloat16, n=200, v=V)
+    lt = torch.log_softmax(hts.float() @ Wt.float().t(), dim=-1)
+    mask = torch.rand(lt.shape, generator=torch.Generator().manual_seed(7)) < 0.3
+    lt16 = lt.masked_fill(mask, -1e4).to(torch.bfloat16)
+    hs_d, W_d = hs.cuda().requires_grad_(True), W.cuda().requires_grad_(True)
+    out = o.distillation_loss(hs_d, W_d, y.cuda(), o.PrecomputedTeacher(logits=lt16.cuda()), student_ce_weight=0.0,
+                              kl_weight=1.0, kl_temperature=T, backend="triton", divergence=div, profile=profile)
+    out.loss.backward()
+    torch.cuda.synchronize()
+    ref = distillation_loss_oracle("precomputed", _np(hs), _np(W), y.numpy(), teacher_logits=_np(lt16),
+                                   student_ce_weight=0.0, kl_weight=1.0, kl_temperature=T, divergence=div)
+    assert np.isfinite(ref["loss"])
+    _check_scalars(out, ref, f"{div} T={T}")
+    _check_grad(hs_d.grad, ref["grad_student_hidden"], torch.bfloat16, f"{div} grad_student_hidden", div)
+    _check_grad(W_d.grad, ref["grad_weight"], torch.bfloat16, f"{div} grad_weight", div)
 
 
 @pytest.mark.parametrize("ac_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
