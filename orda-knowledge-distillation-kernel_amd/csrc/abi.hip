@@ -843,9 +843,10 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
       // of the scan (teacher GEMM, transpose) or through it
       char* Lt = L + nP * eb;
       const bool same_dtype = p->logits_dtype == p->dtype;
-      if (pl.f_tmem || (pl.tsrc == TSRC_MEM && same_dtype && V % 4 == 0 &&
+      if (pl.f_tmem || (pl.tsrc == TSRC_MEM && same_dtype && V % 4 == 0 && V <= 65535 * 64 &&
                         reinterpret_cast<uintptr_t>(t->teacher_logits) % 8 == 0)) {
-        // read token-major by the scan itself (8-byte loads of 4 rows), which
+        // read token-major by the scan itself (8-byte loads of 4 rows through
+        // a buffer resource over 256 tokens: 256 V sizeof(T) < 2^31), which
         // writes them to L on the way
         F.tsrc = TSRC_MEM_RING;
       } else if (pl.tsrc == TSRC_MEM && same_dtype) {

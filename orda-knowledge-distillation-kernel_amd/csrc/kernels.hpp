@@ -565,20 +565,74 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 // Teacher logits of the ring scan's student-only tiles (token block nb of the
 // lane: 4 x 16 values, rows as in the accumulator) come in two steps: 16 raw
 // 8-byte loads (issue_teacher4), then putting them in accumulator order
-// (order_teacher4), so the next block's loads are in flight while this one
-// is scanned.  They stay packed (two 16-bit values per register) and are
+// (order_teacher4).  Two blocks are in flight ahead of the one being
+// scanned.  They stay packed (two 16-bit values per register) and are
 // converted where the scan reads them (AccPairTL), which keeps 32 registers
 // free for the power family's per-token state.
 //  TL_FROM_L: Lout's teacher columns (vocabulary-major): one load holds the
 //    quad's 4 tokens of one row; the in-quad transpose (the inverse of
 //    store_logits4) gives the lane its token's 4 rows.
-//  TL_FROM_MEM: precomputed logits [N x V] (token-major, V a multiple of 4):
-//    one load holds the lane's token's 4 consecutive rows directly; the tile
-//    then writes them to Lout's teacher columns for the dlogits pass.
+//  TL_FROM_MEM: precomputed logits [N x V] (token-major, V a multiple of 4,
+//    256 V sizeof(T) < 2^31): one load holds the lane's token's 4
+//    consecutive rows directly; the tile then writes them to Lout's teacher
+//    columns for the dlogits pass.
 // Rows past V and tokens past N read as 0 (the scan masks rows past V;
-// tokens past N are never merged).
+// tokens past N are never merged).  Loads and stores here are buffer
+// instructions over the tile's block of rows, and a lane with nothing to
+// move points past the resource (kOob) instead of branching round the
+// instruction: every block issues the same 16 instructions, so the waits the
+// compiler places before a block's use count exactly the younger ones and
+// never the stores or loads of the blocks after it.
 enum { TL_NONE = 0, TL_FROM_L = 1, TL_FROM_MEM = 2, TL_STUDENT = 3 };
 
+typedef unsigned int u2v_t __attribute__((ext_vector_type(2)));
+
+// A buffer resource over [p, p + bytes) with base and size read through
+// readfirstlane, so it is scalar (p and bytes are wave-uniform, which the
+// compiler cannot always see); bytes < 2^31.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, int64_t bytes) {
+  const uint64_t base = reinterpret_cast<uint64_t>(p);
+  const uint64_t ub = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(base >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  return rsrc_bytes(reinterpret_cast<const void*>(ub), __builtin_amdgcn_readfirstlane((int)bytes));
+}
+
+// The quad's 4 tokens x 1 row of accumulator block (mb, nb), group g,
+// packed and transposed in the quad (lane q of the quad holds row q).
+template <class T>
+__device__ __forceinline__ uint2 quad_row4(const Acc4& acc, int mb, int nb, int g) {
+  uint32_t x[2], o[2];
+  x[0] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 0), acc_get(acc[mb][nb], g * 4 + 1));
+  x[1] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 2), acc_get(acc[mb][nb], g * 4 + 3));
+  quad_transpose16(x, o);
+  return make_uint2(o[0], o[1]);
+}
+
+// Vocabulary-major tile rows of L from v0 (columns from col0): the resource,
+// and the lane's byte offset of token block nb (rows wm * 128 + 4 (lane / 32)
+// + q, the quad's first token), or kOob when that token is at or past N.
+// Row group (mb, g) is then a scalar offset of (mb * 32 + g * 8) rows.
+struct TileRowsL {
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t ldb;
+};
+template <class T>
+__device__ __forceinline__ TileRowsL tile_rows_l(const void* Lbase, const FusedParams& P, int64_t v0, int64_t col0) {
+  TileRowsL r;
+  const int64_t ldb = P.ldL * (int64_t)sizeof(T);
+  const int64_t rows = min<int64_t>(P.V - v0, 256);
+  r.rs = uniform_rsrc(static_cast<const T*>(Lbase) + v0 * P.ldL + col0, rows * ldb);
+  r.ldb = (uint32_t)ldb;
+  return r;
+}
+template <class T>
+__device__ __forceinline__ uint32_t quad_off_l(const TileRowsL& r, const FusedParams& P, int64_t t0, int nb) {
+  const int lane = opaque_lane();
+  const int q = lane & 3;
+  const int tq = col4(nb, w4_n()) + (lane & 31) - q;  // quad's first token, from t0
+  return t0 + tq < P.N ? (uint32_t)(w4_m() * 128 + (lane >> 5) * 4 + q) * r.ldb + (uint32_t)tq * (uint32_t)sizeof(T)
+                       : kOob;
+}
 
 template <class T, int TL>
 __device__ __forceinline__ void issue_teacher4(uint2 (&raw)[16], const FusedParams& P, int64_t v0, int64_t t0,
@@ -586,24 +640,33 @@ __device__ __forceinline__ void issue_teacher4(uint2 (&raw)[16], const FusedPara
   const int lane = opaque_lane();
   const int wm = w4_m(), wn = w4_n();
   if constexpr (TL == TL_FROM_L) {
-    const int q = lane & 3;
-    const T* L = static_cast<const T*>(P.Lout);
-    const int64_t tb = t0 + col4(nb, wn) + (lane & 31) - q;  // quad's first token
-    const bool tok_ok = tb < P.N;  // full loads: tokens past N are never merged
+    const TileRowsL r = tile_rows_l<T>(P.Lout, P, v0, P.tcolL + t0);
+    const uint32_t off = quad_off_l<T>(r, P, t0, nb);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane) + q;
-      raw[i] = (v < P.V && tok_ok) ? *reinterpret_cast<const uint2*>(L + v * P.ldL + P.tcolL + tb)
-                                   : make_uint2(0u, 0u);
+      const u2v_t d = __builtin_amdgcn_raw_buffer_load_b64(r.rs, off, (int)((uint32_t)((i >> 2) * 32 + (i & 3) * 8) * r.ldb), 0);
+      raw[i] = make_uint2(d.x, d.y);
     }
   } else {
-    const T* Lt = static_cast<const T*>(P.Lt);
-    const int64_t tok = t0 + col4(nb, wn) + (lane & 31);
-    const bool live = tok < P.N;
+    // tokens t0 .. t0 + 255 of the [N x V] logits from row v0 on
+    const int64_t ntok = min<int64_t>(P.N - t0, 256);
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(static_cast<const T*>(P.Lt) + t0 * P.V + v0,
+                                                   (ntok * P.V - v0) * (int64_t)sizeof(T));
+    const int tk = col4(nb, wn) + (lane & 31);  // the lane's token, from t0
+    const int r0 = wm * 128 + (lane >> 5) * 4;  // the lane's row of group 0, from v0
+    // offsets formed arithmetically (a select here becomes a branch round
+    // each load): kOob or-ed in for a token at or past N, and for rows at or
+    // past V (rows r0 + d .. + 3 with d < rowlim are in range, V % 4 == 0)
+    const uint32_t dead = (t0 + tk < P.N) ? 0u : kOob;
+    const int rowlim = (int)min<int64_t>(P.V - v0 - r0, 1 << 20);
+    const uint32_t base = ((uint32_t)tk * (uint32_t)P.V + (uint32_t)r0) * (uint32_t)sizeof(T);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane);  // rows v .. v + 3
-      raw[i] = (live && v < P.V) ? *reinterpret_cast<const uint2*>(Lt + tok * P.V + v) : make_uint2(0u, 0u);
+      const int d = (i >> 2) * 32 + (i & 3) * 8;
+      const uint32_t past = (uint32_t)((rowlim - d - 1) >> 31) & kOob;  // d >= rowlim
+      const uint32_t off = (base + (uint32_t)d * (uint32_t)sizeof(T)) | past | dead;
+      const u2v_t x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+      raw[i] = make_uint2(x.x, x.y);
     }
   }
 }
@@ -623,24 +686,39 @@ __device__ __forceinline__ void order_teacher4(uint2 (&raw)[16]) {
   }
 }
 // Token block nb's teacher logits (ordered raw registers) to Lout's teacher
-// columns, as store_logits4 writes a tied teacher's.
+// columns, as store_logits4 writes a tied teacher's (full 8-byte stores by
+// each quad whose first token is below N).
 template <class T>
 __device__ __forceinline__ void store_teacher4(const uint2 (&tr)[16], const FusedParams& P, int64_t v0, int64_t t0,
                                                int nb) {
-  const int lane = opaque_lane();
-  const int wm = w4_m(), wn = w4_n();
-  const int q = lane & 3;
-  T* L = static_cast<T*>(P.Lout);
-  const int64_t tb = t0 + col4(nb, wn) + (lane & 31) - q;
-  const bool tok_ok = tb < P.N;  // full stores, as in store_logits4
+  const TileRowsL r = tile_rows_l<T>(P.Lout, P, v0, P.tcolL + t0);
+  const uint32_t off = quad_off_l<T>(r, P, t0, nb);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int64_t v = v0 + wm * 128 + acc_row(i >> 2, (i & 3) * 4, lane) + q;
     const uint32_t x[2] = {tr[i].x, tr[i].y};
     uint32_t o[2];
     quad_transpose16(x, o);
-    if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + P.tcolL + tb) = make_uint2(o[0], o[1]);
+    const u2v_t d = {o[0], o[1]};
+    __builtin_amdgcn_raw_buffer_store_b64(d, r.rs, off, (int)((uint32_t)((i >> 2) * 32 + (i & 3) * 8) * r.ldb), 0);
   }
+}
+// Token block nb's student logits of a student-only tile (256 tokens) to
+// Lout's student columns: full 8-byte stores by each quad whose first token
+// is below N (a quad straddling N writes into the padding columns [N, nP),
+// as store_logits4).
+template <class T>
+__device__ __forceinline__ void store_block4(const Acc4& acc, const FusedParams& P, int64_t v0, int64_t t0, int nb) {
+  const TileRowsL r = tile_rows_l<T>(P.Lout, P, v0, t0);
+  const uint32_t off = quad_off_l<T>(r, P, t0, nb);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint2 o = quad_row4<T>(acc, mb, nb, g);
+      const u2v_t d = {o.x, o.y};
+      __builtin_amdgcn_raw_buffer_store_b64(d, r.rs, off, (int)((uint32_t)(mb * 32 + g * 8) * r.ldb), 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 }
 struct AccPairS {  // student only: accumulator block nb (the teacher accessor is never used)
   const Acc4& a;
@@ -760,18 +838,22 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
         scan_variant<SV>(st[j], AccPairS{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
       });
     } else if constexpr (TL != TL_NONE) {
+      // blocks j and j + 1 in flight while block j is scanned; block j's
+      // student logits stored after its scan (their stores are younger than
+      // the loads of block j + 1, so its wait does not cover them)
       uint2 raw[2][16];
       issue_teacher4<T, TL>(raw[0], P, x.v0, t0, 0);
-      store_logits4<T, true>(c, P, x.v0, t0);
+      issue_teacher4<T, TL>(raw[1], P, x.v0, t0, 1);
       static_for<0, NJ>([&](auto J) {
         constexpr int j = decltype(J)::value;
-        if constexpr (j + 1 < NJ) issue_teacher4<T, TL>(raw[(j + 1) & 1], P, x.v0, t0, j + 1);
         order_teacher4<T, TL>(raw[j & 1]);
         if constexpr (TL == TL_FROM_MEM) {
           if (P.store_t) store_teacher4<T>(raw[j & 1], P, x.v0, t0, j);  // else the dlogits pass reads them in place
         }
         scan_variant<SV>(st[j], AccPairTL<T>{c, j, raw[j & 1]}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j],
                          P);
+        store_block4<T>(c, P, x.v0, t0, j);
+        if constexpr (j + 2 < NJ) issue_teacher4<T, TL>(raw[j & 1], P, x.v0, t0, j + 2);
       });
     } else {
       if constexpr (STORE) store_logits4<T, false>(c, P, x.v0, t0);
