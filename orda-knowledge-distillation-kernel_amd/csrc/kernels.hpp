@@ -487,6 +487,29 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
 }
 
 // Logits of a ring-engine tile to Lout[v][t] (see store_logits): block
+typedef unsigned int u2v_t __attribute__((ext_vector_type(2)));
+
+// A buffer resource over [p, p + bytes) with base and size read through
+// readfirstlane, so it is scalar (p and bytes are wave-uniform, which the
+// compiler cannot always see); bytes < 2^31.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, int64_t bytes) {
+  const uint64_t base = reinterpret_cast<uint64_t>(p);
+  const uint64_t ub = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(base >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  return rsrc_bytes(reinterpret_cast<const void*>(ub), __builtin_amdgcn_readfirstlane((int)bytes));
+}
+
+// The quad's 4 tokens x 1 row of accumulator block (mb, nb), group g,
+// packed and transposed in the quad (lane q of the quad holds row q).
+template <class T>
+__device__ __forceinline__ uint2 quad_row4(const Acc4& acc, int mb, int nb, int g) {
+  uint32_t x[2], o[2];
+  x[0] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 0), acc_get(acc[mb][nb], g * 4 + 1));
+  x[1] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 2), acc_get(acc[mb][nb], g * 4 + 3));
+  quad_transpose16(x, o);
+  return make_uint2(o[0], o[1]);
+}
+
 // acc[mb][nb] holds vocabulary rows wm * 128 + mb * 32 + acc_row.  Tokens:
 // tied (TL false) wn * 64 + (nb & 1) * 32 + lane % 32, student for nb < 2,
 // teacher for nb >= 2; student-only tiles (TL) col4(nb, wn) + lane % 32.
@@ -502,28 +525,13 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
   const int q = lane & 3;
   T* L = static_cast<T*>(P.Lout);
   constexpr int kTok = TL ? 256 : 128;
-  // the quad's packed transposed row (4 tokens) of block (mb, nb), group g
-  auto quad_row = [&](int mb, int nb, int g) __attribute__((always_inline)) {
-    uint32_t x[2], o[2];
-    x[0] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 0), acc_get(acc[mb][nb], g * 4 + 1));
-    x[1] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 2), acc_get(acc[mb][nb], g * 4 + 3));
-    quad_transpose16(x, o);
-    return make_uint2(o[0], o[1]);
-  };
   if (t0 + kTok <= P.N) {
     // Every token of the block is valid: stores through a buffer resource
     // over the tile's rows of L, whose range check drops the rows past V,
     // with 32-bit offsets -- no per-store address arithmetic or guard.
-    typedef unsigned int u2v __attribute__((ext_vector_type(2)));
     const int64_t ldb = P.ldL * (int64_t)sizeof(T);
     const int64_t rows = min<int64_t>(P.V - v0, 256);
-    // (v0, t0 are wave-uniform, which the compiler cannot always see: read
-    // the base and size through readfirstlane so the resource is scalar)
-    const uint64_t base = reinterpret_cast<uint64_t>(L + v0 * P.ldL + t0);
-    const uint64_t ubase = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(base >> 32)) << 32) |
-                           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
-    const int nbytes = __builtin_amdgcn_readfirstlane((int)(rows * ldb));
-    const __amdgpu_buffer_rsrc_t rs = rsrc_bytes(reinterpret_cast<const void*>(ubase), nbytes);
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(L + v0 * P.ldL + t0, rows * ldb);
     const uint32_t lane_off = (uint32_t)(wm * 128 + (lane >> 5) * 4 + q) * (uint32_t)ldb +
                               (uint32_t)(wn * 64 + (lane & 31) - q) * (uint32_t)sizeof(T);
 #pragma unroll
@@ -535,8 +543,8 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const uint2 o = quad_row(mb, nb, g);
-          const u2v d = {o.x, o.y};
+          const uint2 o = quad_row4<T>(acc, mb, nb, g);
+          const u2v_t d = {o.x, o.y};
           __builtin_amdgcn_raw_buffer_store_b64(d, rs, (int)(nb_off + (uint32_t)(mb * 32 + g * 8) * (uint32_t)ldb), 0,
                                                 0);
           __builtin_amdgcn_sched_barrier(0);
@@ -555,7 +563,7 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int64_t v = v0 + wm * 128 + acc_row(mb, g * 4, lane) + q;
-        const uint2 o = quad_row(mb, nb, g);
+        const uint2 o = quad_row4<T>(acc, mb, nb, g);
         if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + col) = o;
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -584,29 +592,6 @@ __device__ __forceinline__ void store_logits4(const Acc4& acc, const FusedParams
 // compiler places before a block's use count exactly the younger ones and
 // never the stores or loads of the blocks after it.
 enum { TL_NONE = 0, TL_FROM_L = 1, TL_FROM_MEM = 2, TL_STUDENT = 3 };
-
-typedef unsigned int u2v_t __attribute__((ext_vector_type(2)));
-
-// A buffer resource over [p, p + bytes) with base and size read through
-// readfirstlane, so it is scalar (p and bytes are wave-uniform, which the
-// compiler cannot always see); bytes < 2^31.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* p, int64_t bytes) {
-  const uint64_t base = reinterpret_cast<uint64_t>(p);
-  const uint64_t ub = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(base >> 32)) << 32) |
-                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
-  return rsrc_bytes(reinterpret_cast<const void*>(ub), __builtin_amdgcn_readfirstlane((int)bytes));
-}
-
-// The quad's 4 tokens x 1 row of accumulator block (mb, nb), group g,
-// packed and transposed in the quad (lane q of the quad holds row q).
-template <class T>
-__device__ __forceinline__ uint2 quad_row4(const Acc4& acc, int mb, int nb, int g) {
-  uint32_t x[2], o[2];
-  x[0] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 0), acc_get(acc[mb][nb], g * 4 + 1));
-  x[1] = pack2<T>(acc_get(acc[mb][nb], g * 4 + 2), acc_get(acc[mb][nb], g * 4 + 3));
-  quad_transpose16(x, o);
-  return make_uint2(o[0], o[1]);
-}
 
 // Vocabulary-major tile rows of L from v0 (columns from col0): the resource,
 // and the lane's byte offset of token block nb (rows wm * 128 + 4 (lane / 32)
