@@ -36,6 +36,11 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // The mixture weight of the two-pass divergences (beta for JSD, alpha for
 // the skew KLs) and 1 - weight, formed in double.
 inline void set_mix(float& w, float& w1, const orda_problem_t* p) {
+  if (p->divergence == ORDA_DIV_AB) {  // the second pass's exponents
+    w = p->div_alpha;
+    w1 = p->div_beta;
+    return;
+  }
   const double m = p->divergence == ORDA_DIV_JSD ? (double)p->div_beta : (double)p->div_alpha;
   w = (float)m;
   w1 = (float)(1.0 - m);
@@ -297,14 +302,26 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // to the compute dtype when they have another) are staged into L's
     // teacher columns ahead of the scan, which
     // then runs the student GEMM alone on the ring engine, 256 tokens per
-    // workgroup (16-bit, K > 64; one-pass divergences, the power family only
-    // with one power term: with three its per-token state would spill in
-    // every tile).  Staged logits of a computed teacher are rounded to the
+    // workgroup (16-bit, K > 64; one-pass and two-pass divergences, the power
+    // family with one power term: with three its per-token state would spill
+    // in every tile).  Staged logits of a computed teacher are rounded to the
     // compute dtype in L; a power term with a negative student exponent
     // (chi-squared, Renyi / Amari with alpha > 1) weighs the tail where p_s is
     // small, where that rounding moves the divergence by ~0.6% (chi-squared at
     // T = 1, against 1e-4 for the others), so those keep the two-stage scan,
     // which takes a computed teacher's logits at fp32.
+    // The three-term power divergences (squared L2, AB) with such a teacher
+    // run as two-pass divergences instead: the first pass only normalises
+    // (no power sums in the scan's per-token state), the second pass over
+    // the stored logits sums the divergence and the one row constant its
+    // gradient needs (k_two_rows); computed teachers only with non-negative
+    // student exponents, for the reason above.  (At C4: 29.5-31.1 ms per
+    // step on the two-stage scan, 24.9-25.5 so.)
+    if (pl.fam == FAM_POW && pl.npow == 3 && pl.eb == 2 && pl.H > 64 &&
+        (pl.tsrc == TSRC_MEM || (pl.tsrc == TSRC_SEP && pl.pb[0] >= 0.f && pl.pb[1] >= 0.f && pl.pb[2] >= 0.f))) {
+      pl.fam = FAM_TWO;
+      pl.two_pass = true;
+    }
     const bool pow_ring = pl.npow == 1 && (pl.tsrc == TSRC_MEM || pl.pb[0] >= 0.f);
     pl.f_tl = pl.eb == 2 && pl.H > 64 && (pl.fam != FAM_POW || pow_ring) &&
               (pl.tsrc == TSRC_MEM || pl.tsrc == TSRC_SEP);

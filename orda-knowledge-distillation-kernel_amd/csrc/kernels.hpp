@@ -267,10 +267,27 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
 //   skew-F: x0 += p_t (l_t - l_m), x1 += p_s p_t / m,     m = a p_t + (1-a) p_s
 //   skew-R: x0 += p_s (l_s - l_m), x1 += p_s p_s / m,     m = a p_s + (1-a) p_t
 //   TVD:    x0 += |p_t - p_s|,     x1 += p_s sign(p_s - p_t)
+// and, as second passes of the three-term power divergences over a staged or
+// in-place teacher (w = alpha, w1 = beta for AB):
+//   L2:     x0 += (p_t - p_s)^2,   x1 += p_s (p_s - p_t)
+//   AB:     x0 += q1 - a/(a+b) q2 - b/(a+b) q3,  x1 += q1 - q3,
+//           q1 = p_t^a p_s^b, q2 = p_t^(a+b), q3 = p_s^(a+b)
+// (x1: the row constant of the divergence's gradient).
 template <int DIV>
 __device__ __forceinline__ void two_term(float lps, float lpt, float w, float w1, float& s0, float& s1) {
+  if constexpr (DIV == DIV_AB) {
+    const float ab = w + w1;
+    const float q1 = fexp(w * lpt + w1 * lps), q2 = fexp(ab * lpt), q3 = fexp(ab * lps);
+    s0 += q1 - (w / ab) * q2 - (w1 / ab) * q3;
+    s1 += q1 - q3;
+    return;
+  }
   const float ps = fexp(lps), pt = fexp(lpt);
-  if constexpr (DIV == DIV_TVD) {
+  if constexpr (DIV == DIV_L2) {
+    const float d = ps - pt;
+    s0 += d * d;
+    s1 += ps * d;
+  } else if constexpr (DIV == DIV_TVD) {
     s0 += fabsf(pt - ps);
     s1 += (ps > pt) ? ps : ((ps < pt) ? -ps : 0.f);
   } else {
@@ -2878,6 +2895,8 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
         case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_SKEW_F>), grid, dim3(256), 0, s, P); break; \
         case DIV_SKEW_R: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_SKEW_R>), grid, dim3(256), 0, s, P); break; \
         case DIV_TVD: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_TVD>), grid, dim3(256), 0, s, P); break; \
+        case DIV_L2: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_L2>), grid, dim3(256), 0, s, P); break; \
+        case DIV_AB: hipLaunchKernelGGL((k_two_rows_tm<T, DIV_AB>), grid, dim3(256), 0, s, P); break; \
         default: return hipErrorInvalidValue;                                              \
       }                                                                                    \
       return hipGetLastError();                                                            \
@@ -2887,6 +2906,8 @@ inline void dlm_go(const DlmParams& P, hipStream_t s) {
       case DIV_SKEW_F: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_F>), grid, dim3(256), 0, s, P); break; \
       case DIV_SKEW_R: hipLaunchKernelGGL((k_two_rows<T, DIV_SKEW_R>), grid, dim3(256), 0, s, P); break; \
       case DIV_TVD: hipLaunchKernelGGL((k_two_rows<T, DIV_TVD>), grid, dim3(256), 0, s, P); break; \
+      case DIV_L2: hipLaunchKernelGGL((k_two_rows<T, DIV_L2>), grid, dim3(256), 0, s, P); break; \
+      case DIV_AB: hipLaunchKernelGGL((k_two_rows<T, DIV_AB>), grid, dim3(256), 0, s, P); break; \
       default: return hipErrorInvalidValue;                                                \
     }                                                                                      \
     return hipGetLastError();                                                              \

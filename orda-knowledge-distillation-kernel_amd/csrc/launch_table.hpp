@@ -32,9 +32,9 @@ enum TeacherClass {
   TC_STAGED = 1,   // written to the chunk buffer first (separate / frozen
                    // hidden teachers, precomputed logits not read in place)
   TC_INPLACE = 2,  // precomputed logits read in place (compute dtype, V % 8 == 0)
-  TC_OTHER = 3     // no teacher, fp32, power-family divergences of three
-                   // power terms (squared L2, AB) with a staged teacher
-                   // (two-stage scan)
+  TC_OTHER = 3     // no teacher, fp32, power terms with a negative student
+                   // exponent over a computed teacher's logits (two-stage
+                   // scan)
 };
 
 struct LaunchEntry {

@@ -47,10 +47,23 @@ __global__ __launch_bounds__(kMergeSlices * kMergeTok) void k_merge(MergeParams 
       case DIV_JSD: D = P.beta * x0 + (1.0 - P.beta) * x1; c1 = x1; break;
       case DIV_SKEW_F: D = x0; c1 = x1; break;
       case DIV_SKEW_R: D = x0; c0 = x0; c1 = x1; break;
+      case DIV_L2: D = x0; break;
+      case DIV_AB: D = -x0 / ((double)P.alpha * (double)P.beta); break;
       default: D = 0.5 * x0; c1 = x1; break;  // TVD
     }
-    P.rowp[4 * N + t] = (float)c0;
-    P.rowp[5 * N + t] = (float)c1;
+    if (P.div == DIV_L2 || P.div == DIV_AB) {
+      // the dlogits formulas of the power route take the gradient's row
+      // constant as exp(c_i) - exp(c_2) (L2: i = 1, sum p_s^2 - sum p_t p_s;
+      // AB: i = 0, sum q1 - sum q3): the second pass's x1, split by sign
+      const float pos = x1 > 0.0 ? (float)log(x1) : -INFINITY;
+      const float neg = x1 < 0.0 ? (float)log(-x1) : -INFINITY;
+      P.rowp[4 * N + t] = P.div == DIV_AB ? pos : 0.f;
+      P.rowp[5 * N + t] = P.div == DIV_L2 ? pos : 0.f;
+      P.rowp[6 * N + t] = neg;
+    } else {
+      P.rowp[4 * N + t] = (float)c0;
+      P.rowp[5 * N + t] = (float)c1;
+    }
     P.rowv[2 * P.ldv + t] = ignored ? 0.f : (float)(T * T * D);
     return;
   }

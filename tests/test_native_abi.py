@@ -295,14 +295,18 @@ _HELLINGER, _RENYI, _CHI2, _L2, _AB = 4, 6, 8, 9, 10
     ("c3", _RENYI, 0.5, True),
     ("c3", _RENYI, 2.0, False),     # negative student exponent over bf16-staged logits
     ("c3", _CHI2, 0.5, False),
-    ("c3", _L2, 0.5, False),        # three power terms
+    ("c3", _L2, 0.5, True),         # three power terms: two passes on the ring scan
+    ("c3", _AB, 0.5, True),
+    ("c3", _AB, -1.0, False),       # alpha + beta < 0: negative student exponent
     ("c4", _CHI2, 0.5, True),       # precomputed logits read in place: not rounded again
-    ("c4", _AB, 0.5, False),
+    ("c4", _AB, 0.5, True),
+    ("c4", _AB, -1.0, True),
 ])
 def test_power_family_scan_engine(cfg, div, alpha, ring):
     """The one-term power family runs the ring scan with a staged or in-place
-    teacher; three-term divergences, and a negative student exponent over a
-    computed teacher's logits (staged in bf16), keep the two-stage scan."""
+    teacher, and so do the three-term divergences (squared L2, AB), as
+    two-pass divergences; a negative student exponent over a computed
+    teacher's logits (staged in bf16) keeps the two-stage scan."""
     p = _cfg_problem(cfg)
     p.divergence, p.div_alpha, p.div_beta = div, alpha, 0.5
     info = _native.plan_info(p)
