@@ -317,8 +317,11 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     // gradient needs (k_two_rows); computed teachers only with non-negative
     // student exponents, for the reason above.  (At C4: 29.5-31.1 ms per
     // step on the two-stage scan, 24.9-25.5 so.)
+    // A tied teacher's logits are stored beside the student's anyway: the
+    // same route replaces the tied ring scan's three power sums, which spill.
+    const bool pb_nonneg = pl.pb[0] >= 0.f && pl.pb[1] >= 0.f && pl.pb[2] >= 0.f;
     if (pl.fam == FAM_POW && pl.npow == 3 && pl.eb == 2 && pl.H > 64 &&
-        (pl.tsrc == TSRC_MEM || (pl.tsrc == TSRC_SEP && pl.pb[0] >= 0.f && pl.pb[1] >= 0.f && pl.pb[2] >= 0.f))) {
+        (pl.tsrc == TSRC_MEM || ((pl.tsrc == TSRC_SEP || pl.tsrc == TSRC_SHARED) && pb_nonneg))) {
       pl.fam = FAM_TWO;
       pl.two_pass = true;
     }
