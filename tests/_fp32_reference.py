@@ -22,11 +22,14 @@ import math
 import torch
 import torch.nn.functional as F
 
-DIVERGENCES = ("forward_kl", "reverse_kl", "jsd")
+DIVERGENCES = ("forward_kl", "reverse_kl", "jsd", "squared_l2", "ab")
 
 
-def _divergence_rows(ls: torch.Tensor, lt: torch.Tensor, name: str, beta: float = 0.5) -> torch.Tensor:
-    """Per-row D(p_t || p_s) from log-probabilities (teacher ``lt`` detached)."""
+def _divergence_rows(ls: torch.Tensor, lt: torch.Tensor, name: str, beta: float = 0.5,
+                     alpha: float = 0.5) -> torch.Tensor:
+    """Per-row D(p_t || p_s) from log-probabilities (teacher ``lt`` detached);
+    ``beta`` is JSD's mixture weight, ``alpha``/``beta`` AB's exponents (the
+    registry's defaults, 0.5 each)."""
     if name == "forward_kl":
         return (lt.exp() * (lt - ls)).sum(1)
     if name == "reverse_kl":
@@ -34,6 +37,14 @@ def _divergence_rows(ls: torch.Tensor, lt: torch.Tensor, name: str, beta: float 
     if name == "jsd":
         lm = torch.logaddexp(math.log(beta) + lt, math.log(1.0 - beta) + ls)
         return beta * (lt.exp() * (lt - lm)).sum(1) + (1.0 - beta) * (ls.exp() * (ls - lm)).sum(1)
+    if name == "squared_l2":
+        return ((lt.exp() - ls.exp()) ** 2).sum(1)
+    if name == "ab":
+        a, b = alpha, beta
+        q1 = (a * lt + b * ls).exp()
+        q2 = ((a + b) * lt).exp()
+        q3 = ((a + b) * ls).exp()
+        return -(q1 - a / (a + b) * q2 - b / (a + b) * q3).sum(1) / (a * b)
     raise ValueError(f"divergence {name!r} is not in the float32 reference")
 
 

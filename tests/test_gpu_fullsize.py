@@ -124,13 +124,22 @@ def test_config2_tied_forward_kl_fullsize(profile):
                   profile=profile)
 
 
-@pytest.mark.parametrize("div", ["reverse_kl", "jsd"])
+@pytest.mark.parametrize("div", ["squared_l2", "ab"])
+def test_config2_tied_three_term_power_divergences_fullsize(div):
+    """Config 2's shape with squared L2 and AB (alpha = beta = 0.5), which
+    run as two-pass divergences: their second pass reads the chunk's stored
+    16-bit logits."""
+    _run_fullsize(1002, "tied", 8192, 4096, 128256, div=div, T=1.0, peak_limit=2e9)
+
+
+@pytest.mark.parametrize("div", ["reverse_kl", "jsd", "squared_l2"])
 def test_config3_separate_teacher_fullsize(div):
     """Config 3: student hidden 2048, teacher hidden 4096 (frozen), T=2."""
     _run_fullsize(1003, "separate", 8192, 2048, 128256, Ht=4096, div=div, T=2.0)
 
 
-@pytest.mark.parametrize("div, T", [("forward_kl", 1.0), ("reverse_kl", 4.0), ("jsd", 4.0)])
+@pytest.mark.parametrize("div, T", [("forward_kl", 1.0), ("reverse_kl", 4.0), ("jsd", 4.0), ("squared_l2", 1.0),
+                                    ("ab", 4.0)])
 def test_config4_precomputed_teacher_fullsize(div, T):
     """Config 4: bf16 teacher log-probs of N(0, 3) logits, [8192 x 128256]."""
     _run_fullsize(1004, "precomputed", 8192, 4096, 128256, div=div, T=T)
