@@ -255,6 +255,140 @@ def test_skew_divergences_reduce_to_kl_at_alpha_zero():
     np.testing.assert_allclose(gsr, gr, rtol=1e-10, atol=1e-14)
 
 
+# ------------------------------------------- pins off the symmetric points
+# The checks above leave five formulas where a plausible slip would not
+# show: chi-squared and squared L2 were compared with restatements of
+# themselves, AB only at alpha + beta = 1 (where swapping its a/(a+b) and
+# b/(a+b) coefficients changes nothing), JSD only at beta = 1/2 (where
+# swapping p_t and p_s changes nothing) and the skew KLs only at alpha = 0.
+# Each pin below reaches the value by another route: a library routine
+# (scipy.stats.entropy), an identity with a divergence pinned elsewhere, or a
+# limit of the published definition.  Each pin is a function of the
+# divergence evaluator, so the planted-slip tests further down can show that
+# it rejects the slip it is meant to catch.
+def _div(zt, zs, name, **kw):
+    return divergence_value_and_grad(zt, zs, name, **kw)[0]
+
+
+def _pin_chi_squared(zt, zs):
+    """Pearson chi^2 (Renyi 1961; van Erven and Harremoes 2014, eq. (7)):
+    the Renyi divergence of order 2 is log(1 + chi^2(P || Q)), and Renyi
+    orders increase, so KL = D_1 <= D_2 = log(1 + chi^2).  Renyi itself is
+    pinned at alpha = 1/2 (2 Bhattacharyya) and alpha -> 1 (KL) above."""
+    chi = _div(zt, zs, "chi_squared")
+    np.testing.assert_allclose(_div(zt, zs, "renyi", alpha=2.0), np.log1p(chi), rtol=1e-10)
+    assert np.all(_div(zt, zs, "forward_kl") <= np.log1p(chi) + 1e-12)
+
+
+def _pin_squared_l2(zt, zs):
+    """AB(1, 1) = -sum(p q - p^2/2 - q^2/2) = ||p - q||^2 / 2 (Cichocki,
+    Cruces and Amari 2011, the alpha = beta = 1 case), with ||p - q|| taken
+    from numpy's 2-norm."""
+    pt, ps = _softmax(zt), _softmax(zs)
+    l2 = _div(zt, zs, "squared_l2")
+    np.testing.assert_allclose(l2, np.linalg.norm(pt - ps, axis=-1) ** 2, rtol=1e-10)
+    np.testing.assert_allclose(_div(zt, zs, "ab", alpha=1.0, beta=1.0), 0.5 * l2, rtol=1e-10)
+
+
+def _pin_ab_off_the_line(zt, zs):
+    """AB(alpha, beta) away from alpha + beta = 1, by its limits (Cichocki
+    et al. 2011, eq. (22)-(23)): as beta -> 0 it tends to the generalised KL
+    of the powered measures, (1/alpha^2) sum(p^a log(p^a / q^a) - p^a + q^a),
+    and at alpha = 1 that is KL(p_t || p_s) (pinned by scipy above); as
+    alpha -> 0 it tends to (1/beta^2) sum(q^b log(q^b / p^b) - q^b + p^b)."""
+    lt, ls = np.log(_softmax(zt)), np.log(_softmax(zs))
+    eps = 1e-6
+    for a in (0.6, 1.0, 1.7):
+        pa, qa = np.exp(a * lt), np.exp(a * ls)
+        want = (pa * (a * lt - a * ls) - pa + qa).sum(-1) / a ** 2
+        np.testing.assert_allclose(_div(zt, zs, "ab", alpha=a, beta=eps), want, rtol=1e-4)
+    np.testing.assert_allclose(_div(zt, zs, "ab", alpha=1.0, beta=eps),
+                               [entropy(p, q) for p, q in zip(_softmax(zt), _softmax(zs))], rtol=1e-4)
+    for b in (0.3, 0.9):
+        pb, qb = np.exp(b * lt), np.exp(b * ls)
+        want = (qb * (b * ls - b * lt) - qb + pb).sum(-1) / b ** 2
+        np.testing.assert_allclose(_div(zt, zs, "ab", alpha=eps, beta=b), want, rtol=1e-4)
+
+
+def _pin_jsd(zt, zs):
+    """Generalised JSD with mixture m = beta p_t + (1 - beta) p_s:
+    beta KL(p_t || m) + (1 - beta) KL(p_s || m) = H(m) - beta H(p_t) -
+    (1 - beta) H(p_s), entropies from scipy."""
+    pt, ps = _softmax(zt), _softmax(zs)
+    for b in (0.25, 0.5, 0.75):
+        v = _div(zt, zs, "jsd", beta=b)
+        for i in range(zt.shape[0]):
+            m = b * pt[i] + (1 - b) * ps[i]
+            want = entropy(m) - b * entropy(pt[i]) - (1 - b) * entropy(ps[i])
+            np.testing.assert_allclose(v[i], want, rtol=1e-9, atol=1e-15)
+
+
+def _pin_skew(zt, zs):
+    """DistiLLM's skew KLs (Ko et al. 2024, eq. (3)-(4)) with scipy's
+    relative entropy: skew forward KL(p_t || a p_t + (1 - a) p_s), skew
+    reverse KL(p_s || a p_s + (1 - a) p_t)."""
+    pt, ps = _softmax(zt), _softmax(zs)
+    for a in (0.1, 0.3):
+        f = _div(zt, zs, "skew_forward_kl", alpha=a)
+        r = _div(zt, zs, "skew_reverse_kl", alpha=a)
+        for i in range(zt.shape[0]):
+            np.testing.assert_allclose(f[i], entropy(pt[i], a * pt[i] + (1 - a) * ps[i]), rtol=1e-10)
+            np.testing.assert_allclose(r[i], entropy(ps[i], a * ps[i] + (1 - a) * pt[i]), rtol=1e-10)
+
+
+_PINS = {"chi_squared": _pin_chi_squared, "squared_l2": _pin_squared_l2, "ab": _pin_ab_off_the_line,
+         "jsd": _pin_jsd, "skew": _pin_skew}
+
+
+@pytest.mark.parametrize("pin", sorted(_PINS))
+def test_divergence_pins_off_the_symmetric_points(pin):
+    for seed, scale in ((11, 1.5), (12, 4.0)):
+        zt, zs = _probs(seed, rows=6, V=20, scale=scale)
+        _PINS[pin](zt, zs)
+
+
+# Planted slips: each replaces one oracle formula with a plausible mistake
+# (on the CPU, in the oracle's table) and shows that its pin fails.
+def _neyman_chi2(pt, ps, lt, ls, a, b):
+    return ((pt - ps) ** 2 / pt).sum(), 2.0 * (ps - pt) / pt
+
+
+def _half_l2(pt, ps, lt, ls, a, b):
+    return 0.5 * ((pt - ps) ** 2).sum(), ps - pt
+
+
+def _ab_swapped_coefficients(pt, ps, lt, ls, a, b):
+    s = a + b
+    v = -(np.exp(a * lt + b * ls) - b / s * np.exp(s * lt) - a / s * np.exp(s * ls)).sum() / (a * b)
+    return v, np.zeros_like(ps)
+
+
+def _jsd_swapped_arguments(pt, ps, lt, ls, a, b):
+    m = (1 - b) * pt + b * ps
+    return b * entropy(pt, m) + (1 - b) * entropy(ps, m), np.zeros_like(ps)
+
+
+def _skew_forward_swapped_weights(pt, ps, lt, ls, a, b):
+    return entropy(pt, (1 - a) * pt + a * ps), np.zeros_like(ps)
+
+
+_SLIPS = [("chi_squared", "chi_squared", _neyman_chi2, None, None),
+          ("squared_l2", "squared_l2", _half_l2, None, None),
+          ("ab", "ab", _ab_swapped_coefficients, 0.5, 0.5),
+          ("jsd", "jsd", _jsd_swapped_arguments, None, 0.5),
+          ("skew", "skew_forward_kl", _skew_forward_swapped_weights, 0.1, None)]
+
+
+@pytest.mark.parametrize("pin,name,slip,da,db", _SLIPS, ids=[s[0] for s in _SLIPS])
+def test_divergence_pins_reject_planted_slips(monkeypatch, pin, name, slip, da, db):
+    import oracle.orda_oracle as orc
+
+    zt, zs = _probs(11, rows=6, V=20)
+    monkeypatch.setitem(orc.DIVERGENCE_DEFS, name, (slip, da, db))
+    with pytest.raises(AssertionError):
+        _PINS[pin](zt, zs)
+
+
 @pytest.mark.parametrize("name", DIVS)
 def test_divergence_is_zero_at_equal_distributions(name):
     zt, _ = _probs(6)
