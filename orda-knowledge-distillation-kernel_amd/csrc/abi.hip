@@ -1059,15 +1059,20 @@ int run_scale(const Plan& pl, const orda_tensors_t* t, hipStream_t s) {
   return ORDA_OK;
 }
 
+// Each gradient pointer is read only when its flag asks for that gradient, so
+// a caller that uses none of a later ABI's features may pass a struct that
+// ends before their fields (the RMSNorm pointers come last).
 int check_grads(const Plan& pl, const orda_tensors_t* t) {
-  if (pl.need_gs && !t->grad_student_hidden) return fail(ORDA_EINVAL, "grad_student_hidden is required");
-  if (pl.need_gw && !t->grad_weight) return fail(ORDA_EINVAL, "grad_weight is required");
-  if (pl.need_gt && !t->grad_teacher_hidden) return fail(ORDA_EINVAL, "grad_teacher_hidden is required");
-  if (pl.need_gwt && !t->grad_teacher_weight) return fail(ORDA_EINVAL, "grad_teacher_weight is required");
-  if (pl.need_gnw && !t->grad_student_norm_weight) return fail(ORDA_EINVAL, "grad_student_norm_weight is required");
-  for (const void* g : {t->grad_student_hidden, t->grad_weight, t->grad_teacher_hidden, t->grad_teacher_weight,
-                        t->grad_student_norm_weight})
-    if (g && !aligned16(g)) return fail(ORDA_EINVAL, "gradient buffers must be 16-byte aligned");
+  auto need = [](const void* g, const char* missing) -> int {
+    if (!g) return fail(ORDA_EINVAL, missing);
+    if (!aligned16(g)) return fail(ORDA_EINVAL, "gradient buffers must be 16-byte aligned");
+    return ORDA_OK;
+  };
+  if (pl.need_gs) ORDA_TRY(need(t->grad_student_hidden, "grad_student_hidden is required"));
+  if (pl.need_gw) ORDA_TRY(need(t->grad_weight, "grad_weight is required"));
+  if (pl.need_gt) ORDA_TRY(need(t->grad_teacher_hidden, "grad_teacher_hidden is required"));
+  if (pl.need_gwt) ORDA_TRY(need(t->grad_teacher_weight, "grad_teacher_weight is required"));
+  if (pl.need_gnw) ORDA_TRY(need(t->grad_student_norm_weight, "grad_student_norm_weight is required"));
   return ORDA_OK;
 }
 
@@ -1256,6 +1261,23 @@ int orda_backward(const orda_problem_t* p, const orda_tensors_t* t, void* worksp
     case ORDA_F16: return run_backward<f16>(pl, p, t, ws, s);
     default: return run_backward<float>(pl, p, t, ws, s);
   }
+}
+
+int orda_scale_gradient(int32_t dtype, void* grad, int64_t numel, const float* factor, void* stream) {
+  g_err.clear();
+  if (numel < 0) return fail(ORDA_EINVAL, "numel must be >= 0, got %lld", (long long)numel);
+  if (numel == 0) return ORDA_OK;
+  if (!grad || !factor) return fail(ORDA_EINVAL, "grad and factor are required");
+  if (!aligned16(grad)) return fail(ORDA_EINVAL, "grad must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+  switch (dtype) {
+    case ORDA_BF16: ORDA_CHECK_LAUNCH(launch_scale<bf16>(grad, numel, factor, s)); break;
+    case ORDA_F16: ORDA_CHECK_LAUNCH(launch_scale<f16>(grad, numel, factor, s)); break;
+    case ORDA_F32: ORDA_CHECK_LAUNCH(launch_scale<float>(grad, numel, factor, s)); break;
+    default: return fail(ORDA_EINVAL, "unknown dtype %d", dtype);
+  }
+  return ORDA_OK;
 }
 
 int orda_gemm_abt(int32_t dtype, int64_t M, int64_t N, int64_t K, const void* A, const void* B, void* C,

@@ -95,6 +95,52 @@ def test_struct_layout_matches_the_header(tmp_path):
     assert int(got["ORDA_K_COUNT"]) == len(_native.KERNEL_CLASSES)
 
 
+def _integration_structs():
+    """The ctypes structs of INTEGRATION.md's reference-side binding: the
+    class definitions of its first python block, executed alone (nothing in
+    the block is loaded or called)."""
+    import ast
+
+    text = (ROOT / "INTEGRATION.md").read_text()
+    section = text.split("### Binding a maintainer would add", 1)[1]
+    code = section.split("```python", 1)[1].split("```", 1)[0]
+    tree = ast.parse(code)
+    keep = [n for n in tree.body if isinstance(n, ast.ClassDef)]
+    ns = {"ctypes": ctypes}
+    exec(compile(ast.Module(body=keep, type_ignores=[]), "INTEGRATION.md", "exec"), ns)  # noqa: S102
+    return ns["Problem"], ns["Tensors"]
+
+
+def test_integration_binding_matches_the_header(tmp_path):
+    """Every field of the documented binding's Problem / Tensors sits at the
+    header's offset, and both structs have the header's size (so a caller
+    copying the snippet passes the whole struct the library reads)."""
+    gcc = shutil.which("gcc")
+    if not gcc:
+        pytest.skip("gcc not available")
+    P, T = _integration_structs()
+    lines = []
+    for cname, cls in (("orda_problem_t", P), ("orda_tensors_t", T)):
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{field} %zu\\n", offsetof({cname}, {field}));')
+    src = tmp_path / "probe_doc.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "orda_ce.h"\nint main(void) {\n'
+                   + "\n".join(lines) + "\nreturn 0;\n}\n")
+    exe = tmp_path / "probe_doc"
+    subprocess.run([gcc, "-std=c11", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                               check=True).stdout.splitlines())
+    assert int(got["orda_problem_t"]) == ctypes.sizeof(P)
+    assert int(got["orda_tensors_t"]) == ctypes.sizeof(T)
+    for cname, cls in (("orda_problem_t", P), ("orda_tensors_t", T)):
+        for field, _ in cls._fields_:
+            assert getattr(cls, field).offset == int(got[f"{cname}.{field}"]), f"{cname}.{field}"
+    # and the package's own binding is the same layout
+    for doc, pkg in ((P, _native.Problem), (T, _native.Tensors)):
+        assert [f for f, _ in doc._fields_] == [f for f, _ in pkg._fields_]
+
+
 def _problem(**kw):
     p = _native.Problem()
     p.abi_version = _native.ABI_VERSION
