@@ -111,7 +111,7 @@ def algorithmic_flops(cfg) -> float:
 
 
 def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=None, student_norm=False,
-            logits_gemm="default", teacher_logits_fp32=False):
+            logits_gemm="default", teacher_logits_fp32=False, compiled_backend=None):
     import torch
 
     import orda_ce_kernel as orda
@@ -144,10 +144,24 @@ def run_gpu(cfg, steps, warmup, seed, timing, row_tau=None, chunk=None, splits=N
                                       device=device)).to(hs.dtype).requires_grad_(True)
         norm = orda.StudentRMSNorm(nw)
 
+    if compiled_backend:
+        # the torch.compile-friendly entry (custom ops) in one compiled graph
+        from orda_ce_kernel import compiled
+
+        def loss_fn(a, b, c, tch):
+            return compiled.distillation_loss(a, b, c, tch, student_ce_weight=w_s, teacher_ce_weight=w_t,
+                                              kl_weight=kl_w, kl_temperature=T, divergence=div, chunk_size=chunk,
+                                              student_norm=norm, logits_gemm=logits_gemm)
+
+        compiled_fn = torch.compile(loss_fn, fullgraph=True, backend=compiled_backend)
+
     def step():
-        out = orda.distillation_loss(hs, W, y, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t,
-                                     kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div,
-                                     config=config, student_norm=norm, logits_gemm=logits_gemm)
+        if compiled_backend:
+            out = compiled_fn(hs, W, y, teacher)
+        else:
+            out = orda.distillation_loss(hs, W, y, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t,
+                                         kl_weight=kl_w, kl_temperature=T, backend="triton", divergence=div,
+                                         config=config, student_norm=norm, logits_gemm=logits_gemm)
         out.loss.backward()
         hs.grad = None
         W.grad = None
@@ -458,6 +472,9 @@ def main() -> int:
                     help="fp8: the logits GEMM on e4m3 operands (its own tolerance; not the headline number)")
     ap.add_argument("--teacher-logits-fp32", action="store_true",
                     help="precomputed configurations: hold the teacher's logits in float32 (an input-format variant)")
+    ap.add_argument("--compiled", nargs="?", const="inductor", default=None, metavar="BACKEND",
+                    help="run the step through the torch.compile-friendly entry (orda_ce_kernel.compiled) under "
+                         "torch.compile(fullgraph=True, backend=BACKEND; default inductor)")
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true")
@@ -492,7 +509,8 @@ def main() -> int:
     ms_step, peak_extra, loss_val, kern = run_gpu(cfg, args.steps, args.warmup, args.seed, not args.no_timing,
                                                  row_tau, chunk=args.chunk, splits=args.splits,
                                                  student_norm=args.student_norm, logits_gemm=args.logits_gemm,
-                                                 teacher_logits_fp32=args.teacher_logits_fp32)
+                                                 teacher_logits_fp32=args.teacher_logits_fp32,
+                                                 compiled_backend=args.compiled)
     peak = PEAK_FP32_TFLOPS if dtype_name == "float32" else PEAK_BF16_TFLOPS
     alg = algorithmic_flops(cfg)
     step_tflops = alg / (ms_step / 1e3) / 1e12
@@ -518,7 +536,9 @@ def main() -> int:
                         + (f", top-{TOPK} teacher" if mode == "topk" else "")
                         + (", student RMSNorm fused (grad x + grad norm weight)" if args.student_norm else "")
                         + (", fp8 (e4m3) logits GEMM" if args.logits_gemm == "fp8" else "")
-                        + (", teacher logits held in float32" if args.teacher_logits_fp32 else ""),
+                        + (", teacher logits held in float32" if args.teacher_logits_fp32 else "")
+                        + (f", torch.compile(fullgraph=True, backend={args.compiled}) through the custom-op entry"
+                           if args.compiled else ""),
             "tokens": N, "hidden": H, "vocab": V, "teacher": mode, "divergence": div, "temperature": T,
             "student_ce_weight": w_s, "teacher_ce_weight": w_t, "kl_weight": kl_w, "ignore_frac": ignore_frac,
         },

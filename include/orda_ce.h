@@ -289,6 +289,16 @@ int orda_forward_static(const orda_problem_t* p, const orda_tensors_t* t, void* 
 int orda_backward(const orda_problem_t* p, const orda_tensors_t* t,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* grad *= factor[0] in place (numel elements of `dtype`, 16-byte aligned;
+ * factor a device fp32 scalar, read on the device, so the host does not
+ * synchronise; factor == 1 leaves grad untouched).  Replaces the
+ * multiplication of the cached gradients by grad_output * mean_scale in
+ * TiedCEFunction.backward (ops/tied_teacher.py:538-545, which allocates new
+ * tensors) for callers that hold gradients from an ORDA_GRADS_IN_FORWARD
+ * forward without its problem description: the torch.compile-friendly
+ * custom op's backward. */
+int orda_scale_gradient(int32_t dtype, void* grad, int64_t numel, const float* factor, void* stream);
+
 /* Plain C = A * B^T with A [M x K], B [N x K] (both K-contiguous) and C
  * [M x N] in `dtype`, fp32 accumulation (the engine behind every GEMM of the
  * path).  Exposed for tests and for callers that want the MFMA engine alone;

@@ -2482,9 +2482,12 @@ __global__ __launch_bounds__(256) void k_topk_rows(TopKParams P) {
     P.rowv[2 * P.ldv + t] = ignored ? 0.f : P.temperature * P.temperature * D;
     P.rowp[3 * P.N + t] = kInf;
   }
+  // an ignored row writes exact zeros: with every id at -inf its lse_p is
+  // -inf and the products below would be NaN (0 * NaN), which the scatter
+  // would carry into the gradients
   const float sc = ignored ? 0.f : -P.mean_scale[0] * P.w_kl * P.temperature;
   float* corr = P.corr + t * P.k;
-  for (int64_t i = lane; i < P.k; i += 64) corr[i] = sc * fexp(lp[i] * invT - lse_p);
+  for (int64_t i = lane; i < P.k; i += 64) corr[i] = ignored ? 0.f : sc * fexp(lp[i] * invT - lse_p);
 }
 
 // L[id][t] += corr[t][i] for every token t of the chunk and each of its k ids

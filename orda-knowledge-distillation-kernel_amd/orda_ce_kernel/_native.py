@@ -173,6 +173,9 @@ def library() -> ctypes.CDLL:
             ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
             ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ]
+        lib.orda_scale_gradient.restype = ctypes.c_int
+        lib.orda_scale_gradient.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                            ctypes.c_void_p]
         lib.orda_timing_enable.restype = ctypes.c_int
         lib.orda_timing_enable.argtypes = [ctypes.c_int]
         lib.orda_timing_collect.restype = ctypes.c_int
@@ -246,6 +249,19 @@ def backward(problem: Problem, tensors: Tensors, workspace: torch.Tensor | None,
     size = workspace.numel() if workspace is not None else 0
     rc = library().orda_backward(ctypes.byref(problem), ctypes.byref(tensors), ptr, size, _stream(device))
     _check(rc, "orda_backward")
+
+
+def scale_gradient_(grad: torch.Tensor, factor: torch.Tensor) -> None:
+    """``grad *= factor`` in place on the library's scaling kernel (``factor``
+    a 1-element fp32 tensor on grad's device, read there: no host
+    synchronisation, and factor 1 leaves ``grad`` untouched)."""
+    if grad.dtype not in DTYPE or not grad.is_contiguous():
+        raise ValueError("grad must be a contiguous bf16, fp16 or fp32 tensor")
+    if factor.dtype != torch.float32 or factor.numel() != 1 or factor.device != grad.device:
+        raise ValueError("factor must be a 1-element float32 tensor on grad's device")
+    rc = library().orda_scale_gradient(DTYPE[grad.dtype], grad.data_ptr(), grad.numel(), factor.data_ptr(),
+                                       _stream(grad.device))
+    _check(rc, "orda_scale_gradient")
 
 
 def gemm_abt(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

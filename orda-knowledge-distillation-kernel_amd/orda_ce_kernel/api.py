@@ -93,7 +93,14 @@ class TopKTeacher:
     renormalised over its ids: ``softmax(logprobs / T)`` there, zero
     elsewhere.  Divergences: ``forward_kl`` and ``soft_target_ce``; no
     teacher CE.  Not in the reference, whose precomputed teacher is full
-    ``[BT, V]`` logits (``PrecomputedTeacher``)."""
+    ``[BT, V]`` logits (``PrecomputedTeacher``).
+
+    The HIP path checks the ids only with ``profile="debug"`` (a host
+    synchronisation); otherwise an id outside ``[0, V)`` is clamped to 0 on
+    the device and a repeated id in a row races in the dlogits scatter, so
+    both give undefined (nondeterministic) gradients.  A row whose
+    log-probabilities are all ``-inf`` has no teacher mass: fine on an
+    ignored row (it adds nothing), NaN on a counted one."""
 
     indices: torch.Tensor
     logprobs: torch.Tensor
@@ -350,7 +357,11 @@ def _torch_topk_reference(*, student_hidden, weight, labels, teacher: TopKTeache
     T = float(kl_temperature)
     log_p_s = F.log_softmax(logits_s / T, dim=-1)
     lps_k = log_p_s.gather(1, teacher.indices.long())
-    p_t = F.softmax(teacher.logprobs.detach().to(lps_k.dtype) / T, dim=-1)
+    # ignored rows add nothing; their teacher (padding tokens may carry only
+    # -inf log-probabilities) is replaced by a finite one so that no NaN
+    # reaches the gradients through the masked rows
+    lp_t = teacher.logprobs.detach().to(lps_k.dtype).masked_fill(~keep[:, None], 0.0)
+    p_t = F.softmax(lp_t / T, dim=-1)
     cross = -(p_t * lps_k).sum(-1)
     d = cross + torch.xlogy(p_t, p_t).sum(-1) if divergence.name == "forward_kl" else cross
     d_rows = (d * (T * T)).masked_fill(~keep, 0.0)

@@ -7,19 +7,30 @@ contract.  This module exposes the same loss as ``torch.library`` custom ops,
 so a compiled training step traces through it in one graph:
 
 * ``orda_ce::fused_loss`` runs ``orda_forward`` with the gradients computed
-  inside forward (the default schedule) and returns the four loss components
-  and the four gradients (empty tensors where not requested) as outputs;
-* its autograd formula multiplies those gradients by ``grad_output`` (out of
-  place, in the gradient's dtype: no tensor handed out is changed later);
+  inside forward (the default schedule) and returns the four loss components,
+  the five gradients (empty tensors where not requested) and a one-element
+  record of the factor already applied to them (1);
+* its autograd formula multiplies those gradients by ``grad_output`` in
+  place (``orda_ce::scale_grads_``, the library's scaling kernel, which
+  leaves them untouched when the factor is 1) and returns them, so no second
+  gradient-sized buffer is allocated (grad W is 1.05 GB at the headline
+  shape).  Under ``torch.compile`` a second backward through a retained
+  graph multiplies by the new ``grad_output`` over the recorded one, and
+  autograd copies a gradient it cannot take over (the retained graph still
+  holds it), so tensors already handed out never change; called eagerly,
+  the first backward hands the buffers over and a second one recomputes
+  them, as the drop-in does;
 * a fake (meta) implementation gives the output shapes, so Dynamo/AOT
   tracing never runs the kernels.
 
-Differences from the drop-in entry: no OOM retry with more chunks (the chunk
-is the reference's auto chunk, or ``chunk_size``), and the compute dtype comes
-from the inputs, not from an enclosing autocast region.  The drop-in's
-extensions come along: ``TopKTeacher``, ``student_norm=StudentRMSNorm(w,
-eps)`` (the norm weight is an op input with its own gradient) and
-``logits_gemm="fp8"``.
+As in the drop-in entry, the compute dtype follows an enclosing autocast
+region (``_runtime.default_compute_dtype``, reference ``_runtime.py:41-80``),
+and a device out-of-memory error inside the op halves the token chunk and
+retries, up to the dispatcher's limit of ``2 * max(1, BT // 512)`` chunks
+(reference ``utils/dispatcher.py:218-293``; the op cannot raise back to a
+caller-side loop, so the retry lives in it).  The drop-in's extensions come
+along: ``TopKTeacher``, ``student_norm=StudentRMSNorm(w, eps)`` (the norm
+weight is an op input with its own gradient) and ``logits_gemm="fp8"``.
 """
 from __future__ import annotations
 
@@ -28,6 +39,7 @@ from typing import Optional
 
 import torch
 
+from ._runtime import _autocast_dtype
 from .api import (DistillationLossOutput, StudentRMSNorm, TopKTeacher, _resolve_teacher_ce_weight,
                   _teacher_mode_and_tensors, _validate_teacher)
 from .divergences import Divergence, resolve_divergence
@@ -44,9 +56,16 @@ def _mode_name(mode: str, teacher_logits) -> str:
     return mode
 
 
-def _compute_dtype(student_hidden, weight, teacher_hidden, teacher_weight, teacher_logits, use_teacher: bool):
-    """The inputs' compute dtype by the reference's rule without autocast
-    (``_runtime.py:61-80``): bf16 if any input is bf16, then fp16, then fp32."""
+_DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+
+
+def _compute_dtype(student_hidden, weight, teacher_hidden, teacher_weight, teacher_logits, use_teacher: bool,
+                   autocast: str = ""):
+    """The compute dtype by the reference's rule (``_runtime.py:61-80``): the
+    autocast dtype when one was active at the call (``autocast``: its name,
+    "" for none), else bf16 if any input is bf16, then fp16, then fp32."""
+    if autocast:
+        return _DTYPES[autocast]
     ts = [t for t in (weight, student_hidden, teacher_hidden, teacher_weight) if t is not None]
     if teacher_logits is not None and use_teacher:
         ts.append(teacher_logits)
@@ -82,19 +101,25 @@ def fused_loss(
     chunk_size: int,
     norm_eps: float,
     fp8_logits: bool,
+    autocast: str,
 ) -> list[torch.Tensor]:
-    """Loss components and gradients of one fused evaluation (see module doc).
-    ``div_alpha`` / ``div_beta`` NaN = the divergence's default;
-    ``chunk_size`` 0 = the reference's auto chunk; ``need_grads``: student
-    hidden, weight, teacher hidden, teacher weight, norm weight."""
+    """Loss components, gradients and the applied-factor record of one fused
+    evaluation (see module doc).  ``div_alpha`` / ``div_beta`` NaN = the
+    divergence's default; ``chunk_size`` 0 = the reference's auto chunk;
+    ``need_grads``: student hidden, weight, teacher hidden, teacher weight,
+    norm weight; ``autocast``: the autocast dtype's name at the call ("" for
+    none)."""
     from .ops._engine import FusedCall, run_fused_call, token_chunk_for
+    from .utils._autotune import _is_oom_error
     from .utils.resolver import resolve_chunk_size
 
     use_teacher = kl_weight != 0.0 or teacher_ce_weight != 0.0
-    dtype = _compute_dtype(student_hidden, weight, teacher_hidden, teacher_weight, teacher_logits, use_teacher)
+    dtype = _compute_dtype(student_hidden, weight, teacher_hidden, teacher_weight, teacher_logits, use_teacher,
+                           autocast)
     BT, H = student_hidden.shape
     V = weight.shape[0]
-    cs = chunk_size if chunk_size > 0 else resolve_chunk_size(BT, None, V=V)[0]
+    limit = 2 * max(1, BT // 512)
+    cs, n_chunks = (chunk_size, None) if chunk_size > 0 else resolve_chunk_size(BT, None, V=V, max_chunks=limit)
     nan_none = lambda x: None if math.isnan(x) else float(x)  # noqa: E731
     div = resolve_divergence(Divergence(divergence, nan_none(div_alpha), nan_none(div_beta)))
     need = _need(mode, teacher_ce_weight, need_grads, norm_weight)
@@ -115,37 +140,53 @@ def fused_loss(
         reduction=reduction, vocab_chunk=0, divergence=div, compute_teacher_ce=teacher_ce_weight != 0.0,
         need_grad_student_hidden=need[0], need_grad_weight=need[1], need_grad_teacher_hidden=need[2],
         need_grad_teacher_weight=need[3],
-        # gradients inside forward; given logits of another dtype take the
-        # two-phase schedule, which computes no gradients here (the
-        # extensions always run the gradients-in-forward schedule)
-        grads_in_forward=extended or (any(need) and (lt is None or lt.dtype == dtype)),
+        # gradients inside forward (precomputed logits of another dtype are
+        # cast to the compute dtype on their way into the chunk's buffer);
+        # the extensions always run this schedule
+        grads_in_forward=extended or any(need),
         token_chunk=token_chunk_for(cs),
         topk_indices=None if topk_indices is None else topk_indices.contiguous().to(torch.int64),
         topk_logprobs=None if topk_logprobs is None else topk_logprobs.detach().contiguous().to(torch.float32),
         student_norm_weight=cast(norm_weight), norm_eps=float(norm_eps), need_grad_student_norm_weight=need[4],
         fp8_logits=bool(fp8_logits),
     )
-    if any(need) and not call.grads_in_forward:
-        raise ValueError("orda_ce::fused_loss: precomputed teacher logits must be in the compute dtype "
-                         f"({dtype}) when gradients are requested; got {lt.dtype}")
-    outs, grads, _ = run_fused_call(call)
+    while True:
+        try:
+            outs, grads, _ = run_fused_call(call)
+            break
+        except Exception as exc:  # the dispatcher's OOM retry (reference utils/dispatcher.py:244-293)
+            if chunk_size > 0 or not _is_oom_error(exc) or n_chunks >= min(BT, limit):
+                raise
+            torch.cuda.empty_cache()
+            n_chunks = min(2 * n_chunks, BT, limit)
+            call.token_chunk = token_chunk_for(-(-BT // n_chunks))
     widths = (H, H, H if mode == "tied" else (teacher_hidden.shape[1] if teacher_hidden is not None else 0),
               teacher_hidden.shape[1] if teacher_hidden is not None else 0)
     res = list(outs)
+    # padded columns (H not a multiple of the kernels' 16 bytes) are cut off
+    # into a dense tensor: the fake gives dense (N, width) outputs, and the
+    # backward scales these tensors in place
     for g, width in zip(grads[:4], widths):
         if g is None:
             res.append(student_hidden.new_empty((0,), dtype=dtype))
         else:
-            res.append(g[:, :width] if g.shape[1] != width else g)
+            res.append(g[:, :width].contiguous() if g.shape[1] != width else g)
     g_nw = grads[4]
-    res.append(student_hidden.new_empty((0,), dtype=dtype) if g_nw is None else g_nw[:H])
+    res.append(student_hidden.new_empty((0,), dtype=dtype) if g_nw is None else g_nw[:H].contiguous())
+    res.append(torch.ones(1, dtype=torch.float32, device=student_hidden.device))
     return res
 
 
 def _need(mode, teacher_ce_weight, need_grads, norm_weight):
-    grads_teacher = mode in ("tied", "separate") and teacher_ce_weight != 0.0
-    return [bool(need_grads[0]), bool(need_grads[1]), bool(need_grads[2]) and grads_teacher,
-            bool(need_grads[3]) and grads_teacher and mode == "separate",
+    """Which gradients the op computes.  A tied teacher that requires grad
+    gets one even with its CE off (zeros, as the reference returns,
+    ``ops/tied_teacher.py:349,478-479``); a separate teacher's come only
+    with its CE (the student-only Function returns none,
+    ``ops/separate_teacher.py:713``)."""
+    t_ce = teacher_ce_weight != 0.0
+    return [bool(need_grads[0]), bool(need_grads[1]),
+            bool(need_grads[2]) and (mode == "tied" or (mode == "separate" and t_ce)),
+            bool(need_grads[3]) and mode == "separate" and t_ce,
             bool(need_grads[4]) and norm_weight is not None]
 
 
@@ -153,40 +194,95 @@ def _need(mode, teacher_ce_weight, need_grads, norm_weight):
 def _fused_loss_fake(student_hidden, weight, labels, teacher_hidden, teacher_weight, teacher_logits, topk_indices,
                      topk_logprobs, norm_weight, mode, student_ce_weight, teacher_ce_weight, kl_weight,
                      kl_temperature, ignore_index, reduction, divergence, div_alpha, div_beta, need_grads,
-                     chunk_size, norm_eps, fp8_logits):
+                     chunk_size, norm_eps, fp8_logits, autocast):
     use_teacher = kl_weight != 0.0 or teacher_ce_weight != 0.0
-    dtype = _compute_dtype(student_hidden, weight, teacher_hidden, teacher_weight, teacher_logits, use_teacher)
+    dtype = _compute_dtype(student_hidden, weight, teacher_hidden, teacher_weight, teacher_logits, use_teacher,
+                           autocast)
     need = _need(mode, teacher_ce_weight, need_grads, norm_weight)
     res = [student_hidden.new_empty((), dtype=torch.float32) for _ in range(4)]
     for flag, ref in zip(need, (student_hidden, weight, teacher_hidden, teacher_weight, norm_weight)):
         res.append(ref.new_empty(ref.shape, dtype=dtype) if (flag and ref is not None)
                    else student_hidden.new_empty((0,), dtype=dtype))
+    res.append(student_hidden.new_empty((1,), dtype=torch.float32))
     return res
 
 
+@torch.library.custom_op("orda_ce::scale_grads_", mutates_args=("grads", "applied"))
+def scale_grads_(grads: list[torch.Tensor], applied: torch.Tensor, grad_output: torch.Tensor) -> None:
+    """``grads *= grad_output / applied`` in place, then ``applied =
+    grad_output``: the gradients ``fused_loss`` returned, scaled for this
+    backward (``applied`` records the factor already in them; 1 after the
+    forward, so the first backward multiplies by ``grad_output`` exactly, on
+    the library's kernel, which skips a factor of 1)."""
+    from . import _native
+
+    go = grad_output.detach().to(device=applied.device, dtype=torch.float32).reshape(1)
+    factor = go / applied
+    for g in grads:
+        if g.numel():
+            _native.scale_gradient_(g, factor)
+    applied.copy_(go)
+
+
+@scale_grads_.register_fake
+def _scale_grads_fake(grads, applied, grad_output):
+    return None
+
+
 def _setup_context(ctx, inputs, output):
-    ctx.save_for_backward(*output[4:4 + _GRAD_SLOTS])
+    # The gradients and the factor record are held on ctx as plain
+    # references (marked non-differentiable): they are mutated by the
+    # backward, which the version check of saved tensors would reject.
+    held = output[4:4 + _GRAD_SLOTS + 1]
+    ctx.mark_non_differentiable(*held)
+    ctx.held = tuple(held)
+    ctx.op_args = tuple(inputs)
     ctx.input_dtypes = tuple(None if inputs[i] is None else inputs[i].dtype for i in (0, 1, 3, 4, 8))
+
+
+def _traced(t: torch.Tensor) -> bool:
+    """True while AOT autograd traces the backward (functional or fake
+    tensors), False for an eager call."""
+    from torch._subclasses.fake_tensor import FakeTensor
+    from torch._subclasses.functional_tensor import FunctionalTensor
+
+    return isinstance(t, (FakeTensor, FunctionalTensor))
 
 
 def _backward(ctx, grads):
     g_loss = grads[0]
-    saved = ctx.saved_tensors
+    held = ctx.held
+    if held is None:
+        # eager, a second backward through a retained graph: the first one
+        # handed its buffers over, so recompute (as the drop-in does)
+        held = tuple(fused_loss(*ctx.op_args)[4:4 + _GRAD_SLOTS + 1])
+    *gs, applied = held
+    live = [g for g, dt in zip(gs, ctx.input_dtypes) if g.numel() and dt is not None]
+    if g_loss is None or not live:
+        return (None,) * (_TENSOR_INPUTS + 15)
+    torch.ops.orda_ce.scale_grads_(live, applied, g_loss)
+    if not _traced(applied):
+        ctx.held = None  # eager: drop our references so autograd takes the buffers without a copy
     res = []
-    for g, dt in zip(saved, ctx.input_dtypes):
+    for g, dt in zip(gs, ctx.input_dtypes):
         if g.numel() == 0 or dt is None:
             res.append(None)
         else:
-            # (grad_output is applied in the gradient's dtype: no fp32 copy of
-            # a [V x H] gradient)
-            res.append((g * g_loss).to(dt))
+            res.append(g if g.dtype == dt else g.to(dt))
     d_hs, d_w, d_ht, d_wt, d_nw = res
     # one gradient per op input (None for labels, logits, top-k pairs and the
     # scalars)
-    return (d_hs, d_w, None, d_ht, d_wt, None, None, None, d_nw) + (None,) * 14
+    return (d_hs, d_w, None, d_ht, d_wt, None, None, None, d_nw) + (None,) * 15
 
 
 fused_loss.register_autograd(_backward, setup_context=_setup_context)
+
+
+def _autocast_name(device: torch.device) -> str:
+    if device.type != "cuda":  # the op runs on HIP tensors; meta tensors trace without autocast
+        return ""
+    dt = _autocast_dtype(device)
+    return "" if dt is None else str(dt).replace("torch.", "")
 
 
 def distillation_loss(
@@ -258,6 +354,6 @@ def distillation_loss(
         float(student_ce_weight), float(w_t), float(kl_weight), float(kl_temperature), int(ignore_index),
         reduction, div.name, float("nan") if div.alpha is None else float(div.alpha),
         float("nan") if div.beta is None else float(div.beta), need, int(chunk_size or 0), eps,
-        logits_gemm == "fp8",
+        logits_gemm == "fp8", _autocast_name(student_hidden.device),
     )
     return DistillationLossOutput(outs[0], outs[1].detach(), outs[2].detach(), outs[3].detach())

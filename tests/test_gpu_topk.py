@@ -144,3 +144,34 @@ def test_topk_int32_ids_and_shuffled_order():
         outs.append((float(out.kl), _np(hs_d.grad)))
     assert outs[0][0] == pytest.approx(outs[1][0], rel=1e-5)
     np.testing.assert_allclose(outs[0][1], outs[1][1], rtol=0, atol=1e-2 * np.abs(outs[0][1]).max())
+
+
+def test_topk_ignored_rows_with_no_teacher_mass_give_finite_gradients():
+    """Padding tokens (label -100) whose top-k log-probabilities are all
+    -inf: they add nothing (exact zeros in their dlogits, no NaN carried
+    into grad W by the scatter), so the result equals the oracle's with any
+    finite teacher on those rows."""
+    o = _orda()
+    hs, W, _, hts, Wt, y = D.make_inputs(61, torch.bfloat16)
+    idx, lp = _teacher(61, hts, Wt, 16)
+    ign = torch.nonzero(y == -100).flatten()
+    assert ign.numel() > 0
+    lp_pad = lp.clone()
+    lp_pad[ign] = -float("inf")
+    hs_d, W_d = hs.cuda().requires_grad_(True), W.cuda().requires_grad_(True)
+    out = o.distillation_loss(hs_d, W_d, y.cuda(), o.TopKTeacher(idx.cuda(), lp_pad.cuda()), kl_weight=1.0,
+                              kl_temperature=2.0, backend="triton", config=o.KernelConfig(chunk_size=48))
+    out.loss.backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(hs_d.grad).all() and torch.isfinite(W_d.grad).all()
+    assert not torch.any(hs_d.grad[ign.cuda()])
+    ref = distillation_loss_oracle("precomputed", _np(hs), _np(W), y.numpy(),
+                                   teacher_logits=topk_dense_logits(idx.numpy(), lp.double().numpy(), D.V),
+                                   teacher_ce_weight=0.0, kl_weight=1.0, kl_temperature=2.0,
+                                   grad_logits_dtype="bfloat16")
+    for key in ("loss", "student_ce", "kl"):
+        got = float(getattr(out, key).detach())
+        assert abs(got - ref[key]) <= 1e-3 * abs(ref[key]) + 1e-5, (key, got, ref[key])
+    for got, key in ((hs_d.grad, "grad_student_hidden"), (W_d.grad, "grad_weight")):
+        ok, msg = D.grad_ok(_np(got), ref[key], torch.bfloat16)
+        assert ok, f"{key}: {msg}"

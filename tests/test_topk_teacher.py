@@ -187,3 +187,25 @@ def test_topk_module_wrapper_and_kl_off():
     out = mod(hs, W, y, o.TopKTeacher(idx, vals))
     ce = torch.nn.functional.cross_entropy(hs @ W.t(), y, ignore_index=-100)
     assert float(out.loss.detach()) == pytest.approx(float(ce), rel=1e-12)
+
+
+def test_ignored_rows_with_no_teacher_mass_stay_finite_on_the_torch_path():
+    """Padding tokens whose top-k log-probabilities are all -inf (label
+    -100): the torch formulation gives the oracle's result for the same
+    rows with any finite teacher (ignored rows add nothing), with finite
+    gradients; the HIP kernels' counterpart is in tests/test_gpu_topk.py."""
+    hs, W, y, _, _, idx, vals = _problem(17, n=12, h=8, v=40, k=7)
+    ign = np.flatnonzero(y == -100)
+    assert ign.size > 0
+    pad = vals.copy()
+    pad[ign] = -np.inf
+    hs_t = torch.tensor(hs, requires_grad=True)
+    W_t = torch.tensor(W, requires_grad=True)
+    out = o.distillation_loss(hs_t, W_t, torch.tensor(y), o.TopKTeacher(torch.tensor(idx), torch.tensor(pad)),
+                              kl_weight=0.9, kl_temperature=2.0)
+    out.loss.backward()
+    ref = _oracle(hs, W, y, idx, vals, kl_weight=0.9, kl_temperature=2.0)
+    assert float(out.loss.detach()) == pytest.approx(ref["loss"], rel=1e-10)
+    assert np.isfinite(hs_t.grad.numpy()).all() and np.isfinite(W_t.grad.numpy()).all()
+    np.testing.assert_allclose(hs_t.grad.numpy(), ref["grad_student_hidden"], rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(W_t.grad.numpy(), ref["grad_weight"], rtol=1e-9, atol=1e-12)
