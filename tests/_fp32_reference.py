@@ -6,10 +6,10 @@ It restates the reference's unfused torch path (``api.py:274-335`` of
 distillation term times ``T^2`` masked on ignored rows, masked mean with
 ``clamp(count, 1)``) with autograd over each chunk's logits for the dlogits,
 then the gradient GEMMs in float32.  The distillation term never sends a
-gradient to the teacher (``ops/tied_teacher.py:153-186``).  Only the
-divergences the benchmark configurations name are written here; a label
-outside ``[0, V)`` counts as class 0, as in the Triton kernels
-(``ops/tied_teacher.py:42-44``).
+gradient to the teacher (``ops/tied_teacher.py:153-186``).  Every divergence
+of the package is written here from its published definition (the reference
+has forward KL only); a label outside ``[0, V)`` counts as class 0, as in the
+Triton kernels (``ops/tied_teacher.py:42-44``).
 
 ``tests/test_fp32_reference.py`` pins this restatement against the float64
 oracle on small shapes (CPU), so the full-size GPU tests compare the HIP path
@@ -22,29 +22,59 @@ import math
 import torch
 import torch.nn.functional as F
 
-DIVERGENCES = ("forward_kl", "reverse_kl", "jsd", "squared_l2", "ab")
+# every divergence of the package, with the registry's default parameters
+# (renyi / amari alpha 0.5, ab alpha = beta = 0.5, jsd beta 0.5, skew alpha
+# 0.1), written from the published definitions
+DEFAULT_PARAMS = {"renyi": (0.5, None), "amari_alpha": (0.5, None), "ab": (0.5, 0.5), "jsd": (None, 0.5),
+                  "skew_forward_kl": (0.1, None), "skew_reverse_kl": (0.1, None)}
+DIVERGENCES = ("forward_kl", "reverse_kl", "symmetric_kl", "soft_target_ce", "hellinger", "bhattacharyya", "renyi",
+               "amari_alpha", "chi_squared", "squared_l2", "ab", "jsd", "skew_forward_kl", "skew_reverse_kl", "tvd")
 
 
-def _divergence_rows(ls: torch.Tensor, lt: torch.Tensor, name: str, beta: float = 0.5,
-                     alpha: float = 0.5) -> torch.Tensor:
+def _divergence_rows(ls: torch.Tensor, lt: torch.Tensor, name: str, alpha: float | None = None,
+                     beta: float | None = None) -> torch.Tensor:
     """Per-row D(p_t || p_s) from log-probabilities (teacher ``lt`` detached);
-    ``beta`` is JSD's mixture weight, ``alpha``/``beta`` AB's exponents (the
-    registry's defaults, 0.5 each)."""
+    ``alpha`` / ``beta`` default to the registry's (``DEFAULT_PARAMS``)."""
+    da, db = DEFAULT_PARAMS.get(name, (None, None))
+    a = da if alpha is None else float(alpha)
+    b = db if beta is None else float(beta)
+    pt, ps = lt.exp(), ls.exp()
     if name == "forward_kl":
-        return (lt.exp() * (lt - ls)).sum(1)
+        return (pt * (lt - ls)).sum(1)
     if name == "reverse_kl":
-        return (ls.exp() * (ls - lt)).sum(1)
-    if name == "jsd":
-        lm = torch.logaddexp(math.log(beta) + lt, math.log(1.0 - beta) + ls)
-        return beta * (lt.exp() * (lt - lm)).sum(1) + (1.0 - beta) * (ls.exp() * (ls - lm)).sum(1)
+        return (ps * (ls - lt)).sum(1)
+    if name == "symmetric_kl":
+        return (pt * (lt - ls)).sum(1) + (ps * (ls - lt)).sum(1)
+    if name == "soft_target_ce":
+        return -(pt * ls).sum(1)
+    if name == "hellinger":
+        return 1.0 - (0.5 * (lt + ls)).exp().sum(1)
+    if name == "bhattacharyya":
+        return -torch.logsumexp(0.5 * (lt + ls), 1)
+    if name == "renyi":
+        return torch.logsumexp(a * lt + (1.0 - a) * ls, 1) / (a - 1.0)
+    if name == "amari_alpha":
+        return (1.0 - (a * lt + (1.0 - a) * ls).exp().sum(1)) / (a * (1.0 - a))
+    if name == "chi_squared":
+        return ((pt - ps) ** 2 * (-ls).exp()).sum(1)
     if name == "squared_l2":
-        return ((lt.exp() - ls.exp()) ** 2).sum(1)
+        return ((pt - ps) ** 2).sum(1)
     if name == "ab":
-        a, b = alpha, beta
         q1 = (a * lt + b * ls).exp()
         q2 = ((a + b) * lt).exp()
         q3 = ((a + b) * ls).exp()
         return -(q1 - a / (a + b) * q2 - b / (a + b) * q3).sum(1) / (a * b)
+    if name == "jsd":
+        lm = torch.logaddexp(math.log(b) + lt, math.log(1.0 - b) + ls)
+        return b * (pt * (lt - lm)).sum(1) + (1.0 - b) * (ps * (ls - lm)).sum(1)
+    if name == "skew_forward_kl":
+        lm = torch.logaddexp(math.log(a) + lt, math.log(1.0 - a) + ls)
+        return (pt * (lt - lm)).sum(1)
+    if name == "skew_reverse_kl":
+        lm = torch.logaddexp(math.log(a) + ls, math.log(1.0 - a) + lt)
+        return (ps * (ls - lm)).sum(1)
+    if name == "tvd":
+        return 0.5 * (pt - ps).abs().sum(1)
     raise ValueError(f"divergence {name!r} is not in the float32 reference")
 
 

@@ -22,7 +22,7 @@ import math
 import pytest
 import torch
 
-from tests._fp32_reference import fp32_reference
+from tests._fp32_reference import DIVERGENCES, fp32_reference
 
 pytestmark = pytest.mark.gpu
 
@@ -67,7 +67,7 @@ def _teacher(o, mode, ht, Wt, lt):
     return o.PrecomputedTeacher(logits=lt)
 
 
-def _grad_close(name, got, ref, max_frac=2e-2):
+def _grad_close(name, got, ref, max_frac=2e-2, frob_frac=2e-2):
     got = got.float()
     err = (got - ref).abs()
     ref_max = float(ref.abs().max())
@@ -78,11 +78,12 @@ def _grad_close(name, got, ref, max_frac=2e-2):
     assert torch.isfinite(got).all(), f"{name} has non-finite values"
     assert ns_excess <= 0, f"{name}: outside atol/rtol 1e-2"
     assert worst <= max_frac * ref_max, f"{name}: max |err| {worst:.3e} > {max_frac:g} x max|ref| {ref_max:.3e}"
-    assert frob <= 2e-2, f"{name}: relative Frobenius error {frob:.3e}"
+    assert frob <= frob_frac, f"{name}: relative Frobenius error {frob:.3e}"
 
 
 def _run_fullsize(seed, mode, N, H, V, *, Ht=None, div="forward_kl", T=1.0, w_s=1.0, w_t=None, kl_w=1.0,
-                  ignore_frac=0.05, teacher_row_scale=None, profile="balanced", peak_limit=None, max_frac=2e-2):
+                  ignore_frac=0.05, teacher_row_scale=None, profile="balanced", peak_limit=None, max_frac=2e-2,
+                  frob_frac=2e-2):
     o = _orda()
     print(f"case: {mode} N={N} H={H} Ht={Ht} V={V} div={div} T={T} profile={profile}", flush=True)
     hs, W, y, ht, Wt, lt = _inputs(seed, mode, N, H, V, Ht=Ht, ignore_frac=ignore_frac,
@@ -110,8 +111,8 @@ def _run_fullsize(seed, mode, N, H, V, *, Ht=None, div="forward_kl", T=1.0, w_s=
         print(f"{k}: hip {got[k]:.7g} fp32-ref {ref[k]:.7g}", flush=True)
         assert math.isfinite(got[k]), k
         assert abs(got[k] - ref[k]) <= 1e-3 * abs(ref[k]) + 1e-5, (k, got[k], ref[k])
-    _grad_close("grad_student_hidden", hs_d.grad, ref["grad_student_hidden"], max_frac)
-    _grad_close("grad_weight", W_d.grad, ref["grad_weight"], max_frac)
+    _grad_close("grad_student_hidden", hs_d.grad, ref["grad_student_hidden"], max_frac, frob_frac)
+    _grad_close("grad_weight", W_d.grad, ref["grad_weight"], max_frac, frob_frac)
     return ref
 
 
@@ -138,11 +139,20 @@ def test_config3_separate_teacher_fullsize(div):
     _run_fullsize(1003, "separate", 8192, 2048, 128256, Ht=4096, div=div, T=2.0)
 
 
-@pytest.mark.parametrize("div, T", [("forward_kl", 1.0), ("reverse_kl", 4.0), ("jsd", 4.0), ("squared_l2", 1.0),
-                                    ("ab", 4.0)])
+@pytest.mark.parametrize("T", [1.0, 4.0])
+@pytest.mark.parametrize("div", DIVERGENCES)
 def test_config4_precomputed_teacher_fullsize(div, T):
-    """Config 4: bf16 teacher log-probs of N(0, 3) logits, [8192 x 128256]."""
-    _run_fullsize(1004, "precomputed", 8192, 4096, 128256, div=div, T=T)
+    """Config 4's sweep: bf16 teacher log-probs of N(0, 3) logits,
+    [8192 x 128256], every divergence at T = 1 and 4 (default parameters:
+    skew alpha 0.1, JSD beta 0.5).  TVD's gradient is a sign function of
+    p_s - p_t, so where the two are within rounding of each other the kernels
+    and the reference may take opposite sides: its gradients are held to
+    the scale-relative bounds the small-shape TVD tests use (worst element
+    0.5 and Frobenius 0.1 of the reference's scale; atol/rtol 1e-2 still
+    apply)."""
+    tvd = div == "tvd"
+    _run_fullsize(1004, "precomputed", 8192, 4096, 128256, div=div, T=T, max_frac=0.5 if tvd else 2e-2,
+                  frob_frac=0.1 if tvd else 2e-2)
 
 
 def test_config5_long_sequence_stress_fullsize():
