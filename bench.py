@@ -49,11 +49,20 @@ CONFIGS = {
     "c5": ("tied", 32768, 5120, 5120, 152064, "bfloat16", "forward_kl", 1.0, 0.7, None, 0.3, 0.20),
     # config 4's teacher as its top-64 (id, log-prob) pairs per token (TopKTeacher)
     "c4topk": ("topk", 8192, 4096, 4096, 128256, "bfloat16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
+    # launch-table shapes beyond the benchmark configurations: configs 2-5 in fp16, and two
+    # other (hidden, vocabulary) pairs of the tied headline workload (8192 tokens)
+    "c2f16": ("tied", 8192, 4096, 4096, 128256, "float16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
+    "c3f16": ("separate", 8192, 2048, 4096, 128256, "float16", "reverse_kl", 2.0, 1.0, None, 1.0, 0.05),
+    "c4f16": ("precomputed", 8192, 4096, 4096, 128256, "float16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
+    "c5f16": ("tied", 32768, 5120, 5120, 152064, "float16", "forward_kl", 1.0, 0.7, None, 0.3, 0.20),
+    "h8192": ("tied", 8192, 8192, 8192, 128256, "bfloat16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
+    "h3584": ("tied", 8192, 3584, 3584, 152064, "bfloat16", "forward_kl", 1.0, 1.0, None, 1.0, 0.05),
 }
 TOPK = 64
 # config 5: teacher rows scaled by c / tau_n, tau_n ~ U[0.5, 4]; c puts the teacher logit spread at
 # ~6.4 standard deviations for tau = 0.5 (entropy of a few nats) and ~0.8 for tau = 4 (near uniform)
-ROW_TEMPERATURE = {"c5": (0.5, 4.0, 6.4 * 0.5 / (0.02 * 5120 ** 0.5))}
+ROW_TEMPERATURE = {"c5": (0.5, 4.0, 6.4 * 0.5 / (0.02 * 5120 ** 0.5)),
+                   "c5f16": (0.5, 4.0, 6.4 * 0.5 / (0.02 * 5120 ** 0.5))}
 
 
 def _log(msg: str) -> None:
@@ -415,12 +424,20 @@ def sweep(cfg, args, row_tau) -> int:
 
 # Launch-table sweep: (requested chunk, grad-hidden split count) per config;
 # the chunk is the dispatcher's chunk_size, which the library scales by the
-# table's chunk_scale (so 512 -> 1024 tokens at scale 2).
+# table's chunk_scale (so 512 -> 1024 tokens at scale 2).  A split count of
+# None is the library's own choice (the table entry, or the rule for shapes
+# the table does not list).
 TABLE_SWEEP = {
     "c2": [(c, s) for c in (256, 512) for s in (4, 8, 12, 16)],
     "c3": [(c, s) for c in (512, 1024) for s in (4, 8, 16)],
     "c4": [(c, s) for c in (256, 512) for s in (2, 4, 8)],
     "c5": [(256, 16), (512, 4), (512, 8), (512, 16), (1024, 8)],
+    "c2f16": [(c, s) for c in (256, 512) for s in (None, 4, 8, 16)],
+    "c3f16": [(c, s) for c in (512, 1024) for s in (None, 4, 8)],
+    "c4f16": [(c, s) for c in (256, 512) for s in (None, 2, 4, 8)],
+    "c5f16": [(256, None), (512, None), (512, 4), (512, 8), (512, 16)],
+    "h8192": [(c, s) for c in (256, 512, 1024) for s in (None, 2, 4, 8)],
+    "h3584": [(c, s) for c in (256, 512, 1024) for s in (None, 4, 8, 16)],
 }
 
 
@@ -429,7 +446,10 @@ def table_sweep(args) -> int:
     (one json line each); the rows behind csrc/launch_table.hpp."""
     import torch
 
+    only = set(args.sweep_configs.split(",")) if args.sweep_configs else None
     for name, cases in TABLE_SWEEP.items():
+        if only is not None and name not in only:
+            continue
         cfg = CONFIGS[name]
         row_tau = ROW_TEMPERATURE.get(name)
         for chunk, splits in cases:
@@ -439,6 +459,7 @@ def table_sweep(args) -> int:
             plan = launch_plan_of(cfg, chunk, splits)
             print(json.dumps({
                 "config": name, "chunk": chunk, "splits": splits, "token_chunk": plan["token_chunk"],
+                "used_splits": plan["grad_hidden_splits"], "table_entry": plan["table_entry"],
                 "ms_per_step": round(ms, 3), "peak_extra_hbm_gb": round(peak_extra / 1e9, 3),
                 "ms_per_step_by_class": {k: round(r["ms_per_step"], 3) for k, r in rows.items()},
             }), flush=True)
@@ -466,6 +487,8 @@ def main() -> int:
     ap.add_argument("--table-sweep", action="store_true",
                     help="instead of the one-line benchmark, time the launch-table candidates (requested chunk x "
                          "grad-hidden splits) of configs 2-5, one json line each")
+    ap.add_argument("--sweep-configs", default=None, metavar="NAMES",
+                    help="with --table-sweep: only these configurations (comma-separated)")
     ap.add_argument("--student-norm", action="store_true",
                     help="fuse the student's final RMSNorm in front of the loss (StudentRMSNorm)")
     ap.add_argument("--logits-gemm", default="default", choices=("default", "fp8"),

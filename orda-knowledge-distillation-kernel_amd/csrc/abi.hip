@@ -117,6 +117,38 @@ constexpr int kScalFloats = 64;  // scalars at the head of the saved buffer
     if (rc_ != ORDA_OK) return rc_; \
   } while (0)
 
+// Budget of the step's extra device memory that the chunk rule keeps to
+// (the headline configuration's ceiling: gradients, chunk logits and
+// scratch together under 2 GB).
+constexpr double kExtraMemoryBudget = 2e9;
+
+// Chunk scale of the rule for shapes the launch table does not list: 4 when
+// the chunk buffer holds only the student's 16-bit logits (teacher logits
+// read in place, or none), else 2.  A large problem (a scale-2 chunk holding
+// at least 256 MiB of logits) is raised from 2 to 4 when the step's extra
+// memory at 4 -- the requested gradients, the chunk's logits, 4 split-K
+// partials and the transposed hidden rows -- stays within
+// kExtraMemoryBudget, or when the gradients alone exceed it (no chunk keeps
+// the budget then) and the scale-4 chunk by itself stays within it: a deeper
+// chunk halves grad W's read-modify-write passes over the weight.  Measured (the launch-table sweep, 8192 tokens): a
+// separate teacher with student hidden 2048 in fp16, 19.97 ms per step at 4
+// (1.69 GB) against 22.44-22.57 at 2; tied hidden 8192, 72.1 against 75.0
+// (gradients 2.2 GB); tied hidden 3584, vocabulary 152064, kept at 2 (2.4 GB
+// at 4).  Smaller problems keep the plain rule (not swept).
+inline int rule_chunk_scale(const Plan& pl, const orda_problem_t* p, int64_t ncol, int64_t Nr) {
+  if (pl.f_tmem || (pl.tsrc == TSRC_NONE && pl.eb == 2)) return 4;
+  if (p->token_chunk <= 0) return 2;
+  const double eb = (double)pl.eb, V = (double)pl.V, H = (double)pl.H, Ht = (double)pl.Ht, N = (double)pl.N;
+  const double n2 = (double)std::min<int64_t>(round_up(p->token_chunk * 2, 8), Nr);
+  if (V * (double)ncol * n2 * eb < (double)(kFusedLogitsBytes / 2)) return 2;
+  const double n4 = (double)std::min<int64_t>(round_up(p->token_chunk * 4, 8), Nr);
+  const double grads = (pl.need_gw ? V * H * eb : 0.0) + (pl.need_gs ? N * H * eb : 0.0) +
+                       (pl.need_gt ? N * Ht * eb : 0.0) + (pl.need_gwt ? V * Ht * eb : 0.0);
+  const double chunk4 = V * (double)ncol * n4 * eb + 4.0 * n4 * H * 4.0 + 2.0 * n4 * H * eb;
+  if (grads + chunk4 <= kExtraMemoryBudget) return 4;
+  return (grads >= kExtraMemoryBudget && chunk4 <= kExtraMemoryBudget) ? 4 : 2;
+}
+
 int make_plan(const orda_problem_t* p, Plan& pl) {
   pl = Plan{};
   if (!p) return fail(ORDA_EINVAL, "problem is NULL");
@@ -351,8 +383,10 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     const LaunchEntry* te = pl.table_entry >= 0 ? &kLaunchTable[pl.table_entry] : nullptr;
     // (the rule: 4 when the chunk buffer holds only the student's 16-bit
     // logits -- teacher logits read in place, or no teacher logits at all --
-    // else 2)
-    pl.chunk_scale = te ? te->chunk_scale : (pl.f_tmem || (pl.tsrc == TSRC_NONE && pl.eb == 2) ? 4 : 2);
+    // else 2, raised to 4 for large problems when the step's extra memory at
+    // 4 stays under the 2 GB budget, or when the gradients alone exceed it;
+    // see rule_chunk_scale)
+    pl.chunk_scale = te ? te->chunk_scale : rule_chunk_scale(pl, p, ncol, Nr);
     pl.scan_groups = te ? te->scan_groups : (int)kPersistentGroups;
     int64_t n = p->token_chunk;
     if (n > 0) {

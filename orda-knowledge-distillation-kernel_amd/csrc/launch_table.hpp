@@ -19,7 +19,10 @@
 // Entries are keyed by (teacher class, dtype, vocabulary, student hidden) and
 // were chosen by sweeping on an MI355X (the sweep and its timings are in the
 // repository's profiles, launch_table_sweep.md); every other shape takes the
-// rule in choose_launch().
+// rule of make_plan in abi.hip (rule_chunk_scale for the chunk scale, the
+// round-filling split count), which lands within 1% of the swept best on
+// every swept shape that the table lists and keeps the 2 GB budget where one
+// can be kept.
 #pragma once
 
 #include <stdint.h>
@@ -47,7 +50,7 @@ struct LaunchEntry {
   const char* evidence;  // the sweep row the entry comes from
 };
 
-// dtype 0 = bf16 (orda_dtype).
+// dtype: 0 = bf16, 1 = f16 (orda_dtype).
 constexpr LaunchEntry kLaunchTable[] = {
     // config 2: tied, N = 8192, H = 4096, V = 128256.  1024-token chunks
     // (2048 would pass the 2 GB memory ceiling); 4 splits: 38.7 ms/step vs
@@ -67,6 +70,29 @@ constexpr LaunchEntry kLaunchTable[] = {
     // full rounds of 256): 216.4 ms/step, peak extra 3.52 GB, vs 229.4 with
     // 1024-token chunks and 16 splits (2.88 GB); 4 splits 224.5, 16 218.2
     {TC_TIED, 0, 152064, 5120, 4, 8, 256, "c5: chunk 512 x 4, split 8"},
+    // configs 2-5 in fp16 (their fp16 dlogits underflow more: the gradient
+    // GEMMs run faster than in bf16 at the same plan).  c2f16: 1024-token
+    // chunks, 4 splits: 35.9 ms/step at 1.73 GB (8 splits 36.1, 16 36.5;
+    // 512-token chunks 40.1-44.2)
+    {TC_TIED, 1, 128256, 4096, 2, 4, 256, "c2f16: chunk 512 x 2, split 4"},
+    // c3f16: 2048-token chunks, 4 splits: 20.0 ms/step at 1.69 GB (1024-token
+    // chunks 22.4-24.6)
+    {TC_STAGED, 1, 128256, 2048, 4, 4, 256, "c3f16: chunk 512 x 4, split 4"},
+    // c4f16: 2048-token chunks, 4 splits: 21.8 ms/step (2 and 8 within 0.6%;
+    // 1024-token chunks 23.7-28.4)
+    {TC_INPLACE, 1, 128256, 4096, 4, 4, 256, "c4f16: chunk 512 x 4, split 4"},
+    // c5f16: 1024-token chunks, 16 splits: 207.2 ms/step at 2.88 GB (8
+    // splits 211.1, 4 224.1; 512-token chunks 232.6)
+    {TC_TIED, 1, 152064, 5120, 2, 16, 256, "c5f16: chunk 512 x 2, split 16"},
+    // two shapes beyond the benchmark configurations, tied, 8192 tokens.
+    // Hidden 8192: the gradients alone take 2.2 GB, so no chunk keeps the
+    // 2 GB budget; 2048-token chunks, 2 splits: 72.1 ms/step at 3.49 GB
+    // (1024-token chunks 75.0-75.6, 512-token 82.0-92.2)
+    {TC_TIED, 0, 128256, 8192, 4, 2, 256, "h8192: chunk 512 x 4, split 2"},
+    // Hidden 3584, vocabulary 152064: 1024-token chunks, 9 splits: 42.5
+    // ms/step at 1.92 GB (2048-token chunks 40.1-40.5 at 2.5-2.9 GB, past
+    // the 2 GB budget; 512-token chunks 45.9-50.3)
+    {TC_TIED, 0, 152064, 3584, 2, 9, 256, "h3584: chunk 512 x 2, split 9"},
 };
 constexpr int kLaunchTableSize = (int)(sizeof(kLaunchTable) / sizeof(kLaunchTable[0]));
 

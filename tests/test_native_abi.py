@@ -312,11 +312,21 @@ def _cfg_problem(cfg):
     if cfg == "c5":
         return _problem(n_rows=32768, hidden=5120, teacher_hidden=5120, vocab=152064, flags=0x33 | GIF,
                         token_chunk=512)
+    if cfg.endswith("f16"):  # the configuration in fp16
+        q = _cfg_problem(cfg[:-3])
+        q.dtype = q.logits_dtype = 1
+        return q
+    if cfg == "h8192":
+        return _problem(hidden=8192, teacher_hidden=8192, flags=0x33 | GIF, token_chunk=512)
+    if cfg == "h3584":
+        return _problem(hidden=3584, teacher_hidden=3584, vocab=152064, flags=0x33 | GIF, token_chunk=512)
     raise ValueError(cfg)
 
 
 @pytest.mark.parametrize("cfg, entry, chunk, splits, tclass", [
-    ("c2", 0, 1024, 4, 0), ("c3", 1, 2048, 4, 1), ("c4", 2, 2048, 2, 2), ("c5", 3, 2048, 8, 0)])
+    ("c2", 0, 1024, 4, 0), ("c3", 1, 2048, 4, 1), ("c4", 2, 2048, 2, 2), ("c5", 3, 2048, 8, 0),
+    ("c2f16", 4, 1024, 4, 0), ("c3f16", 5, 2048, 4, 1), ("c4f16", 6, 2048, 4, 2), ("c5f16", 7, 1024, 16, 0),
+    ("h8192", 8, 2048, 2, 0), ("h3584", 9, 1024, 9, 0)])
 def test_launch_table_drives_the_benchmark_configurations(cfg, entry, chunk, splits, tclass):
     """Each benchmark configuration finds its row of the gfx950 launch table
     (csrc/launch_table.hpp) and takes its chunk scale and split count."""
@@ -374,6 +384,32 @@ def test_launch_overrides_and_rule_for_unlisted_shapes():
     # the two-phase schedule has no token chunks
     r = _problem(flags=0x33)
     assert _native.plan_info(r)["grads_in_forward"] == 0
+
+
+@pytest.mark.parametrize("name, kw, scale", [
+    # (the launch table's swept shapes with the vocabulary moved off its rows,
+    # so the rule decides; the table's measured choice in parentheses)
+    ("tied, hidden 4096", dict(flags=0x33 | GIF), 2),                                   # (c2: 2)
+    ("separate, hidden 2048", dict(mode=1, hidden=2048, teacher_hidden=4096, flags=0x23 | GIF,
+                                   teacher_ce_weight=0.0, divergence=1, temperature=2.0), 4),  # (c3: 4)
+    ("separate, hidden 2048, fp16", dict(mode=1, dtype=1, hidden=2048, teacher_hidden=4096, flags=0x23 | GIF,
+                                         teacher_ce_weight=0.0, divergence=1, temperature=2.0), 4),  # (c3f16: 4)
+    ("tied, hidden 8192", dict(hidden=8192, teacher_hidden=8192, flags=0x33 | GIF), 4),  # (h8192: 4)
+    ("tied, hidden 3584", dict(hidden=3584, teacher_hidden=3584, flags=0x33 | GIF), 2),  # (h3584: 2)
+    ("tied, hidden 5120, 32768 tokens", dict(n_rows=32768, hidden=5120, teacher_hidden=5120, flags=0x33 | GIF), 2),
+])
+def test_chunk_rule_keeps_the_memory_budget(name, kw, scale):
+    """Shapes the table does not list (vocabulary 128000) take the rule: the
+    chunk scale rises from 2 to 4 when the step's extra memory at 4 stays
+    under 2 GB (a separate teacher with a small student hidden) or when the
+    gradients alone exceed 2 GB (hidden 8192), and stays at 2 otherwise."""
+    p = _problem(vocab=128000, token_chunk=512, **kw)
+    info = _native.plan_info(p)
+    assert info["table_entry"] == -1, name
+    assert info["chunk_scale"] == scale, name
+    # a small problem keeps the plain rule
+    small = _problem(n_rows=96, hidden=64, teacher_hidden=64, vocab=1000, flags=0x33 | GIF, token_chunk=20)
+    assert _native.plan_info(small)["token_chunk"] == 40
 
 
 def test_grad_hidden_splits_keep_each_split_inside_a_buffer_resource():
