@@ -11,7 +11,7 @@ import torch
 
 from orda_ce_kernel.ops._engine import vocab_chunk_for
 from orda_ce_kernel.utils import dispatcher
-from orda_ce_kernel.utils._autotune import ENGINE_TILES, _is_oom_error, engine_tile
+from orda_ce_kernel.utils._autotune import _is_oom_error
 from orda_ce_kernel.utils.resolver import resolve_chunk_size
 
 
@@ -161,19 +161,6 @@ def test_non_oom_errors_propagate(monkeypatch):
     with pytest.raises(ValueError, match="not an OOM"):
         dispatcher.dynamic_chunk(torch.randn(4, 2), torch.randn(4, 2), torch.randn(4, 2),
                                  torch.randint(0, 4, (4,)))
-
-
-def test_engine_tiles_cover_compute_dtypes():
-    """16-bit kernels run the 4-wave ring engine (wave tile 128 x 128), fp32
-    the 8-wave two-stage engine (128 x 64); both use 256 x 256 tiles."""
-    for dt in (torch.bfloat16, torch.float16):
-        cfg = engine_tile(dt)
-        assert cfg.engine == "ring" and cfg.waves == 4 and cfg.wave_tile == (128, 128)
-    f32 = engine_tile(torch.float32)
-    assert f32.engine == "two-stage" and f32.waves == 8 and f32.wave_tile == (128, 64)
-    assert all(t.tile_m == t.tile_n == 256 for t in ENGINE_TILES.values())
-    with pytest.raises(ValueError):
-        engine_tile(torch.float64)
 
 
 PKG = Path(__file__).resolve().parents[1] / "orda-knowledge-distillation-kernel_amd" / "orda_ce_kernel"
