@@ -100,3 +100,51 @@ def test_compiled_entry_traces_the_extensions(ext):
         assert nw.grad.shape == (H,)
     else:
         assert nw.grad is None
+
+
+def test_compiled_op_retries_a_device_oom_with_halved_chunks(monkeypatch):
+    """The op's OOM retry (the dispatcher's, reference
+    ``utils/dispatcher.py:244-293``): a device out-of-memory error doubles
+    the chunk count (halves the token chunk) and calls again, up to
+    ``2 * max(1, BT // 512)`` chunks, then re-raises; any other error, or an
+    explicit chunk size, is raised at once.  The library call is replaced on
+    the host (no kernel runs)."""
+    from orda_ce_kernel.ops import _engine
+
+    BT, H, V = 2048, 16, 64
+    hs, W = torch.randn(BT, H, dtype=torch.bfloat16), torch.randn(V, H, dtype=torch.bfloat16)
+    y = torch.randint(0, V, (BT,))
+    chunks = []
+
+    def fake_run(fail_times, exc):
+        def run(call):
+            chunks.append(call.token_chunk)
+            if len(chunks) <= fail_times:
+                raise exc
+            outs = tuple(torch.zeros((), dtype=torch.float32) for _ in range(4))
+            return outs, (torch.zeros(BT, H, dtype=torch.bfloat16), None, None, None, None), None
+        return run
+
+    def op(chunk_size=0):
+        return compiled.fused_loss(hs, W, y, None, None, None, None, None, None, "tied", 1.0, 0.0, 0.0, 1.0,
+                                   -100, "mean", "forward_kl", float("nan"), float("nan"),
+                                   [True, False, False, False, False], chunk_size, 1e-6, False, "")
+
+    oom = torch.cuda.OutOfMemoryError("HIP out of memory. Tried to allocate 2.00 GiB")
+    monkeypatch.setattr(_engine, "run_fused_call", fake_run(2, oom))
+    res = op()
+    assert len(res) == 10 and res[4].shape == (BT, H)
+    assert len(chunks) == 3 and chunks[1] * 2 == chunks[0] and chunks[2] * 2 == chunks[1]
+    # the limit: 2 * (2048 // 512) = 8 chunks, then the error goes to the caller
+    chunks.clear()
+    monkeypatch.setattr(_engine, "run_fused_call", fake_run(100, oom))
+    with pytest.raises(torch.cuda.OutOfMemoryError):
+        op()
+    assert chunks[-1] * 8 >= BT and len(chunks) <= 4
+    # not an OOM, or an explicit chunk size: no retry
+    for exc, cs in ((RuntimeError("invalid argument"), 0), (oom, 256)):
+        chunks.clear()
+        monkeypatch.setattr(_engine, "run_fused_call", fake_run(1, exc))
+        with pytest.raises(type(exc)):
+            op(cs)
+        assert len(chunks) == 1
