@@ -148,3 +148,35 @@ def test_compiled_op_retries_a_device_oom_with_halved_chunks(monkeypatch):
         with pytest.raises(type(exc)):
             op(cs)
         assert len(chunks) == 1
+
+
+def test_compiled_op_returns_dense_gradients_like_its_fake(monkeypatch):
+    """H = 100 (not a multiple of the kernels' 16 bytes): the library hands
+    back gradients with padded rows (pitch 104); the op cuts them to dense
+    (N, 100) tensors, whose shape and strides equal the fake's, so compiled
+    code that relies on the fake's layout reads them correctly.  The library
+    call is replaced on the host (no kernel runs)."""
+    from orda_ce_kernel.ops import _engine
+
+    BT, H, Hp, V = 64, 100, 104, 50
+
+    def run(call):
+        outs = tuple(torch.zeros((), dtype=torch.float32) for _ in range(4))
+        g = torch.arange(BT * Hp, dtype=torch.float32).reshape(BT, Hp).to(torch.bfloat16)
+        gw = torch.ones(V, Hp, dtype=torch.bfloat16)
+        return outs, (g, gw, None, None, None), None
+
+    monkeypatch.setattr(_engine, "run_fused_call", run)
+    args = lambda dev: (torch.randn(BT, H, dtype=torch.bfloat16, device=dev),  # noqa: E731
+                        torch.randn(V, H, dtype=torch.bfloat16, device=dev),
+                        torch.randint(0, V, (BT,), device=dev), None, None, None, None, None, None, "tied", 1.0, 0.0,
+                        0.0, 1.0, -100, "mean", "forward_kl", float("nan"), float("nan"),
+                        [True, True, False, False, False], 0, 1e-6, False, "")
+    real = compiled.fused_loss(*args("cpu"))
+    fake = compiled.fused_loss(*args("meta"))
+    for i in (4, 5):
+        assert real[i].shape == fake[i].shape and real[i].stride() == fake[i].stride(), i
+        assert real[i].is_contiguous()
+    assert real[4].shape == (BT, H) and real[5].shape == (V, H)
+    assert torch.equal(real[4].float(), torch.arange(BT * Hp, dtype=torch.float32).reshape(BT, Hp)[:, :H]
+                       .to(torch.bfloat16).float())
