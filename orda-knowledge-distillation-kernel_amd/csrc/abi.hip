@@ -93,6 +93,8 @@ struct Plan {
   size_t off_hT, off_htT, off_dLT, off_dLNs, off_dLNt, off_WT, off_WtT, off_g32s, off_g32t, bwd_bytes;
   // gradients inside forward (materialised token chunks)
   bool fused, store_t, f_tl, f_tmem, f_sring, topk;
+  // fp16: dlogits without the mean scale, gradients scaled once at the end
+  bool late_scale;
   int tclass, table_entry, chunk_scale, scan_groups;
   int64_t fn, fnP, fldL, fnchunks;
   int f_nvr, f_tpr, splits_s, splits_t;
@@ -176,6 +178,13 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
   pl.mode = p->mode;
   pl.dtype = p->dtype;
   pl.eb = p->dtype == ORDA_F32 ? 4 : 2;
+  // In fp16 the dlogits times 1 / count (probabilities of ~1e-6 over ~1e4
+  // counted tokens) fall below fp16's subnormals and flush to zero, which
+  // drops most of grad hidden's softmax term.  The reference's fp16 path
+  // stores them unscaled and applies the mean scale to the gradients
+  // (ops/tied_teacher.py:532-545); so does this one.  bf16 and fp32 have
+  // the range to fold the scale into the dlogits.
+  pl.late_scale = p->dtype == ORDA_F16;
   pl.kelems = 16 / pl.eb;
   pl.N = p->n_rows;
   pl.V = p->vocab;
@@ -649,6 +658,24 @@ int gemm(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, float*
     if (rc_ != ORDA_OK) return rc_; \
   } while (0)
 
+// Every requested gradient *= factor[0] (a device scalar; the scaling kernel
+// returns at once when it is 1).
+template <class T>
+int scale_grads(const Plan& pl, const orda_tensors_t* t, const float* factor, hipStream_t s) {
+  auto sc = [&](void* g, int64_t n) -> int {
+    if (!g) return ORDA_OK;
+    Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
+    ORDA_CHECK_LAUNCH(launch_scale<T>(g, n, factor, s));
+    return ORDA_OK;
+  };
+  if (pl.need_gs) ORDA_TRY(sc(t->grad_student_hidden, pl.N * pl.H));
+  if (pl.need_gw) ORDA_TRY(sc(t->grad_weight, pl.V * pl.H));
+  if (pl.need_gt) ORDA_TRY(sc(t->grad_teacher_hidden, pl.N * pl.Ht));
+  if (pl.need_gwt) ORDA_TRY(sc(t->grad_teacher_weight, pl.V * pl.Ht));
+  if (pl.need_gnw) ORDA_TRY(sc(t->grad_student_norm_weight, pl.H));
+  return ORDA_OK;
+}
+
 template <class T>
 int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, char* ws, hipStream_t s) {
   const bool tied = pl.mode == ORDA_MODE_TIED, sep = pl.mode == ORDA_MODE_SEPARATE;
@@ -703,7 +730,10 @@ int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* 
   set_mix(F.mix_w, F.mix_w1, p);
   F.n_ttiles = pl.n_ttiles; F.rowp = rowp;
   F.w_s = p->student_ce_weight; F.w_t = p->teacher_ce_weight; F.w_kl = pl.div_on ? p->kl_weight : 0.f;
-  F.grad_output = t->grad_output; F.mean_scale = scal;
+  // fp16: unscaled dlogits (scal[2] = 1); the gradients get grad_output x
+  // mean_scale at the end
+  F.grad_output = pl.late_scale ? scal + 2 : t->grad_output;
+  F.mean_scale = pl.late_scale ? scal + 2 : scal;
   F.dLT = dLT; F.ldT = pl.ldT; F.tcol = NP; F.dLNs = dLNs; F.dLNt = dLNt; F.ldN = pl.Vc;
   F.w_dlt_s = pl.w_dlt_s; F.w_dlt_t = pl.w_dlt_t; F.w_dln_s = pl.w_dln_s; F.w_dln_t = pl.w_dln_t;
 
@@ -760,6 +790,10 @@ int run_backward(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* 
     { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_weight, Ht, pl.V, 0, Ht, eb, s)); }
   if (sep && pl.need_gt && !pl.w_dln_t)
     { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, Ht, N, 0, Ht, eb, s)); }
+  if (pl.late_scale) {
+    { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_mul_scalars(t->grad_output, scal, scal + 3, s)); }
+    ORDA_TRY(scale_grads<T>(pl, t, scal + 3, s));
+  }
   return ORDA_OK;
 }
 
@@ -954,7 +988,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     if (pl.topk && pl.div_on) {
       // the teacher's k ids: divergence rows and the ids' dlogits share
       K.hs = hsc; K.W = W; K.idx = t->teacher_topk_indices + r0 * p->topk;
-      K.lp = t->teacher_topk_logprobs + r0 * p->topk; K.labels = t->labels + r0; K.mean_scale = scal;
+      K.lp = t->teacher_topk_logprobs + r0 * p->topk; K.labels = t->labels + r0; K.mean_scale = pl.late_scale ? scal + 2 : scal;
       K.lse_sT = reinterpret_cast<const float*>(ws + pl.off_lse); K.rowp = rowp; K.rowv = rowv + r0; K.ldv = N; K.corr = reinterpret_cast<float*>(ws + pl.off_corr);
       K.L = L; K.ldL = ldL; K.N = nc; K.V = V; K.H = H; K.k = p->topk; K.ignore_index = p->ignore_index;
       K.div = pl.div_on ? pl.div : DIV_FKL; K.invT = F.invT; K.temperature = p->temperature;
@@ -983,7 +1017,7 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     if (!any_grad) continue;
 
     DlmParams D{};
-    D.L = L; D.ldL = ldL; D.tcol = nP; D.labels = t->labels + r0; D.rowp = rowp; D.mean_scale = scal;
+    D.L = L; D.ldL = ldL; D.tcol = nP; D.labels = t->labels + r0; D.rowp = rowp; D.mean_scale = pl.late_scale ? scal + 2 : scal;
     D.N = nc; D.V = V; D.ignore_index = p->ignore_index;
     D.div = pl.div; D.t_is_one = pl.t1; D.tgrad = tgrad;
     D.rows_per_block = (int)round_up(std::max<int64_t>(64, cdiv(V, 65535)), 8);  // grid.y stays <= 65535
@@ -1073,24 +1107,16 @@ int run_fused(const Plan& pl, const orda_problem_t* p, const orda_tensors_t* t, 
     { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_hidden, Ht, N, 0, Ht, eb, s)); }
   if (sep && pl.need_gwt && !pl.w_dlt_t)
     { Timed tm_(ORDA_K_AUX, s, 0.0, 0.0); ORDA_CHECK_LAUNCH(launch_zero2d(t->grad_teacher_weight, Ht, V, 0, Ht, eb, s)); }
+  // fp16: the chunks' dlogits were unscaled; the mean scale once here (the
+  // backward applies grad_output)
+  if (pl.late_scale && any_grad) ORDA_TRY(scale_grads<T>(pl, t, scal, s));
   return ORDA_OK;
 }
 
 // Backward of the ORDA_GRADS_IN_FORWARD mode: gradients *= grad_output.
 template <class T>
 int run_scale(const Plan& pl, const orda_tensors_t* t, hipStream_t s) {
-  auto sc = [&](void* g, int64_t n) -> int {
-    if (!g) return ORDA_OK;
-    Timed tm_(ORDA_K_AUX, s, 0.0, 0.0);
-    ORDA_CHECK_LAUNCH(launch_scale<T>(g, n, t->grad_output, s));
-    return ORDA_OK;
-  };
-  if (pl.need_gs) ORDA_TRY(sc(t->grad_student_hidden, pl.N * pl.H));
-  if (pl.need_gw) ORDA_TRY(sc(t->grad_weight, pl.V * pl.H));
-  if (pl.need_gt) ORDA_TRY(sc(t->grad_teacher_hidden, pl.N * pl.Ht));
-  if (pl.need_gwt) ORDA_TRY(sc(t->grad_teacher_weight, pl.V * pl.Ht));
-  if (pl.need_gnw) ORDA_TRY(sc(t->grad_student_norm_weight, pl.H));
-  return ORDA_OK;
+  return scale_grads<T>(pl, t, t->grad_output, s);
 }
 
 // Each gradient pointer is read only when its flag asks for that gradient, so

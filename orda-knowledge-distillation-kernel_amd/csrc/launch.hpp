@@ -263,15 +263,18 @@ struct FinalizeParams {
   float* out_ce_s;
   float* out_ce_t;
   float* out_kl;
-  float* scal;  // [0] = mean_scale, [1] = count of non-ignored rows
+  float* scal;  // [0] = mean_scale, [1] = count of non-ignored rows, [2] = 1
 };
 hipError_t launch_finalize(const FinalizeParams& P, hipStream_t s);
 
 // scal[0] = mean scale (1 / max(count, 1), or 1 for sum), scal[1] = count of
-// non-ignored labels: the same values k_finalize writes, available before
-// the loss rows exist.
+// non-ignored labels, scal[2] = 1: the same values k_finalize writes,
+// available before the loss rows exist.
 hipError_t launch_count(const int64_t* labels, int64_t N, int64_t ignore_index, int reduction_sum, float* scal,
                         hipStream_t s);
+
+// *out = a[0] * b[0] (device scalars; one thread)
+hipError_t launch_mul_scalars(const float* a, const float* b, float* out, hipStream_t s);
 
 // out[r * ld + c] = 0 for r < R, c0 <= c < c1 (element size esize bytes)
 hipError_t launch_zero2d(void* out, int64_t ld, int64_t R, int64_t c0, int64_t c1, int esize, hipStream_t s);

@@ -215,6 +215,7 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeParams P) {
     *P.out_kl = (float)kl;
     P.scal[0] = mean_scale;
     P.scal[1] = (float)count;
+    P.scal[2] = 1.0f;
   }
 }
 
@@ -236,8 +237,11 @@ __global__ __launch_bounds__(1024) void k_count(const int64_t* labels, int64_t N
     const double denom = count < 1.0 ? 1.0 : count;
     scal[0] = reduction_sum ? 1.0f : 1.0f / (float)denom;
     scal[1] = (float)count;
+    scal[2] = 1.0f;
   }
 }
+
+__global__ void k_mul_scalars(const float* a, const float* b, float* out) { *out = a[0] * b[0]; }
 
 __global__ void k_zero2d(char* out, int64_t ld_bytes, int64_t R, int64_t c0_bytes, int64_t w_bytes) {
   const int64_t total = R * w_bytes;
@@ -262,6 +266,10 @@ hipError_t launch_finalize(const FinalizeParams& P, hipStream_t s) {
 hipError_t launch_count(const int64_t* labels, int64_t N, int64_t ignore_index, int reduction_sum, float* scal,
                         hipStream_t s) {
   hipLaunchKernelGGL(k_count, dim3(1), dim3(1024), 0, s, labels, N, ignore_index, reduction_sum, scal);
+  return hipGetLastError();
+}
+hipError_t launch_mul_scalars(const float* a, const float* b, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(k_mul_scalars, dim3(1), dim3(1), 0, s, a, b, out);
   return hipGetLastError();
 }
 hipError_t launch_zero2d(void* out, int64_t ld, int64_t R, int64_t c0, int64_t c1, int esize, hipStream_t s) {
