@@ -435,7 +435,7 @@ TABLE_SWEEP = {
     "c2f16": [(c, s) for c in (256, 512) for s in (None, 4, 8, 16)],
     "c3f16": [(c, s) for c in (512, 1024) for s in (None, 4, 8)],
     "c4f16": [(c, s) for c in (256, 512) for s in (None, 2, 4, 8)],
-    "c5f16": [(256, None), (512, None), (512, 4), (512, 8), (512, 16)],
+    "c5f16": [(256, None), (512, None), (512, 4), (512, 8), (512, 16), (1024, 8), (1024, 16)],
     "h8192": [(c, s) for c in (256, 512, 1024) for s in (None, 2, 4, 8)],
     "h3584": [(c, s) for c in (256, 512, 1024) for s in (None, 4, 8, 16)],
 }

@@ -130,13 +130,16 @@ constexpr double kExtraMemoryBudget = 2e9;
 // at least 256 MiB of logits) is raised from 2 to 4 when the step's extra
 // memory at 4 -- the requested gradients, the chunk's logits, 4 split-K
 // partials and the transposed hidden rows -- stays within
-// kExtraMemoryBudget, or when the gradients alone exceed it (no chunk keeps
-// the budget then) and the scale-4 chunk by itself stays within it: a deeper
-// chunk halves grad W's read-modify-write passes over the weight.  Measured (the launch-table sweep, 8192 tokens): a
-// separate teacher with student hidden 2048 in fp16, 19.97 ms per step at 4
-// (1.69 GB) against 22.44-22.57 at 2; tied hidden 8192, 72.1 against 75.0
-// (gradients 2.2 GB); tied hidden 3584, vocabulary 152064, kept at 2 (2.4 GB
-// at 4).  Smaller problems keep the plain rule (not swept).
+// kExtraMemoryBudget, or when no chunk keeps the budget (the gradients and a
+// scale-2 chunk already exceed it) and the scale-4 chunk by itself stays
+// within it: a deeper chunk halves grad W's read-modify-write passes over the
+// weight.  Measured (the launch-table sweep): a separate teacher with student
+// hidden 2048, 2048-token chunks at 1.69 GB against 1024 (20.9 against 22.4
+// ms per step in bf16); tied hidden 8192 (gradients 2.2 GB), 72.1 against
+// 75.0; tied hidden 5120, vocabulary 152064, 32768 tokens (gradients 1.89
+// GB), 216-220 against 229-232; tied hidden 3584, vocabulary 152064, kept at
+// 2 (1.92 GB; 2.5 GB at 4).  Smaller problems keep the plain rule (not
+// swept).
 inline int rule_chunk_scale(const Plan& pl, const orda_problem_t* p, int64_t ncol, int64_t Nr) {
   if (pl.f_tmem || (pl.tsrc == TSRC_NONE && pl.eb == 2)) return 4;
   if (p->token_chunk <= 0) return 2;
@@ -146,9 +149,11 @@ inline int rule_chunk_scale(const Plan& pl, const orda_problem_t* p, int64_t nco
   const double n4 = (double)std::min<int64_t>(round_up(p->token_chunk * 4, 8), Nr);
   const double grads = (pl.need_gw ? V * H * eb : 0.0) + (pl.need_gs ? N * H * eb : 0.0) +
                        (pl.need_gt ? N * Ht * eb : 0.0) + (pl.need_gwt ? V * Ht * eb : 0.0);
-  const double chunk4 = V * (double)ncol * n4 * eb + 4.0 * n4 * H * 4.0 + 2.0 * n4 * H * eb;
+  auto chunk_bytes = [&](double n) { return V * (double)ncol * n * eb + 4.0 * n * H * 4.0 + 2.0 * n * H * eb; };
+  const double chunk4 = chunk_bytes(n4);
   if (grads + chunk4 <= kExtraMemoryBudget) return 4;
-  return (grads >= kExtraMemoryBudget && chunk4 <= kExtraMemoryBudget) ? 4 : 2;
+  const bool out_of_reach = grads + chunk_bytes(n2) > kExtraMemoryBudget;
+  return (out_of_reach && chunk4 <= kExtraMemoryBudget) ? 4 : 2;
 }
 
 int make_plan(const orda_problem_t* p, Plan& pl) {

@@ -70,20 +70,19 @@ constexpr LaunchEntry kLaunchTable[] = {
     // full rounds of 256): 216.4 ms/step, peak extra 3.52 GB, vs 229.4 with
     // 1024-token chunks and 16 splits (2.88 GB); 4 splits 224.5, 16 218.2
     {TC_TIED, 0, 152064, 5120, 4, 8, 256, "c5: chunk 512 x 4, split 8"},
-    // configs 2-5 in fp16 (their fp16 dlogits underflow more: the gradient
-    // GEMMs run faster than in bf16 at the same plan).  c2f16: 1024-token
-    // chunks, 4 splits: 35.9 ms/step at 1.73 GB (8 splits 36.1, 16 36.5;
-    // 512-token chunks 40.1-44.2)
+    // configs 2-5 in fp16 (dlogits unscaled, gradients scaled once at the
+    // end).  c2f16: 1024-token chunks, 4 splits: 39.9 ms/step at 1.73 GB
+    // (8 splits 40.2, 16 40.5; 512-token chunks 43.7-47.6)
     {TC_TIED, 1, 128256, 4096, 2, 4, 256, "c2f16: chunk 512 x 2, split 4"},
-    // c3f16: 2048-token chunks, 4 splits: 20.0 ms/step at 1.69 GB (1024-token
-    // chunks 22.4-24.6)
+    // c3f16: 2048-token chunks, 4 splits: 21.4 ms/step at 1.69 GB (8 splits
+    // 21.5; 4096-token chunks 21.1 at 2.82 GB, past the 2 GB budget)
     {TC_STAGED, 1, 128256, 2048, 4, 4, 256, "c3f16: chunk 512 x 4, split 4"},
-    // c4f16: 2048-token chunks, 4 splits: 21.8 ms/step (2 and 8 within 0.6%;
-    // 1024-token chunks 23.7-28.4)
-    {TC_INPLACE, 1, 128256, 4096, 4, 4, 256, "c4f16: chunk 512 x 4, split 4"},
-    // c5f16: 1024-token chunks, 16 splits: 207.2 ms/step at 2.88 GB (8
-    // splits 211.1, 4 224.1; 512-token chunks 232.6)
-    {TC_TIED, 1, 152064, 5120, 2, 16, 256, "c5f16: chunk 512 x 2, split 16"},
+    // c4f16: 2048-token chunks, 2 splits: 24.9 ms/step at 1.73 GB (4 splits
+    // equal at 1.80 GB, 8 25.2; 1024-token chunks 26.6-31.7)
+    {TC_INPLACE, 1, 128256, 4096, 4, 2, 256, "c4f16: chunk 512 x 4, split 2"},
+    // c5f16: 2048-token chunks, 8 splits: 220.0 ms/step at 3.52 GB (16
+    // splits 221.7; 1024-token chunks 231.9-259.2 at 2.6-2.9 GB)
+    {TC_TIED, 1, 152064, 5120, 4, 8, 256, "c5f16: chunk 512 x 4, split 8"},
     // two shapes beyond the benchmark configurations, tied, 8192 tokens.
     // Hidden 8192: the gradients alone take 2.2 GB, so no chunk keeps the
     // 2 GB budget; 2048-token chunks, 2 splits: 72.1 ms/step at 3.49 GB
