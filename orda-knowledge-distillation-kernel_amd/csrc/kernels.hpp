@@ -6,6 +6,7 @@
 #include "orda_core.hpp"
 #include "ring4.hpp"
 #include "ring4_f8.hpp"
+#include "ring16.hpp"
 
 namespace orda {
 
@@ -1274,22 +1275,39 @@ __global__ __launch_bounds__(kThreads) void k_gemm2(GemmParams P) {
   pipeline_tiles<T, LA, LB, true, true, 8>(acc, lds, ntiles, nk, issue, epilogue);
 }
 
+// Lanes l (l / 16 even) and l + 16 trade halves of two adjacent blocks P
+// (columns c0 + 4 (l / 16) ..) and Q (c0 + 16 + 4 (l / 16) ..): afterwards
+// each lane holds 8 consecutive columns starting at c0 + g8(l), values
+// x[0..3] then y[0..3].
+__device__ __forceinline__ int g8(int lane) { return 16 * ((lane >> 4) & 1) + 8 * (lane >> 5); }
+__device__ __forceinline__ void trade16(const f32x4& P, const f32x4& Q, float (&x)[4], float (&y)[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc16_get(P, e)), __float_as_uint(acc16_get(Q, e)),
+                                                    false, false);
+    x[e] = __uint_as_float(r[0]);
+    y[e] = __uint_as_float(r[1]);
+  }
+}
+
 // C[M x N] (mode) A B^T for 16-bit operands on the four-wave ring engine
-// (pipeline4): A K-major and B K-major or MN-major (one segment; MODE
-// GEMM_STORE: C = in T, GEMM_ACC_T: C += in T, the fp32 sum rounded once; one
-// split), or both MN-major (GEMM_STORE, or GEMM_SPLIT: split s covers K rows
-// [s * k_per_split, ...) and writes its fp32 partial).  Persistent: workgroup b (in XCD order) owns work items b,
-// b + grid, ... (split-major, tiles in band order, 8 row tiles wide).  The
-// MFMAs run swapped (B x A^T), so each lane holds four consecutive columns of
-// one C row and stores them with one 8-byte (16-byte for fp32) store.
+// with 16x16x32 MFMAs (pipeline16): A K-major and B K-major or MN-major (one
+// segment; MODE GEMM_STORE: C = in T, GEMM_ACC_T: C += in T, the fp32 sum
+// rounded once; one split), or both MN-major (GEMM_STORE, or GEMM_SPLIT:
+// split s covers K rows [s * k_per_split, ...) and writes its fp32 partial).
+// Persistent: workgroup b (in XCD order) owns work items b, b + grid, ...
+// (split-major, tiles in band order, 8 row tiles wide).  The MFMAs run
+// swapped (B x A^T), so each lane holds four consecutive columns of one C row
+// per block; lanes l and l + 16 trade halves of two adjacent blocks
+// (trade16) so interior tiles move 8 columns per 16-byte access.
 // Contract as k_gemm2, plus k_per_split > 64 and, for MN-major operands,
 // k_per_split * ld * sizeof(T) < 2^31.
 template <class T, int LA, int LB, int MODE>
 __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
   static_assert(LA == LB || (LA == KMAJ && LB == MNMAJ), "K/K, K/MN or MN/MN");
   __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
-  Acc4 acc;
-  zero_acc4(acc);
+  Acc16 acc;
+  zero_acc16(acc);
   const int tiles = P.tiles_m * P.tiles_n;
   const int total = tiles * P.splits;
   const int grid = gridDim.x;
@@ -1328,189 +1346,118 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
     return x;
   };
   auto opnd = [](const TI& x, int op) { return op == 0 ? x.a : x.b; };
-  auto epilogue = [&](int, const TI& x, Acc4& c) __attribute__((always_inline)) {
+  auto epilogue = [&](int, const TI& x, Acc16& c) __attribute__((always_inline)) {
     const int lane = opaque_lane();
     const int wm = w4_m(), wn = w4_n();
     const int64_t ldc = P.ldc;
     const int mlim = (int)min<int64_t>(P.M - x.m0, 256), nlim = (int)min<int64_t>(P.N - x.n0, 256);
-    const int cl = wn * 64 + (lane >> 5) * 4;  // tile column of this lane's group 0, block 0
-    auto col = [&](int nb, int g) { return (nb >> 1) * 128 + (nb & 1) * 32 + g * 8; };
+    const int rl = lane & 15;          // C row of the lane within a block
+    const int cq = 4 * (lane >> 4);    // first of the lane's 4 columns within a block (before the trade)
+    const int cg = g8(lane);           // first of the lane's 8 columns within a block pair (after the trade)
     if constexpr (MODE == GEMM_SPLIT) {
       float* D = P.C32 + (int64_t)x.split * P.split_stride + (int64_t)x.m0 * ldc + x.n0;
-      // interior tiles take a path with only full 16-byte stores: in one loop
-      // with the ragged-edge stores the compiler merges the two and splits
-      // every full store into narrower ones under divergent branches
-      auto part = [&](auto edge) __attribute__((always_inline)) {
-        constexpr bool E = decltype(edge)::value;
+      if (mlim == 256 && nlim == 256) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const int mm = wm * 128 + mb * 32 + (lane & 31);
-          float* rp = D + (int64_t)mm * ldc + cl;
+        for (int mb = 0; mb < 8; ++mb) {
+          float* rp = D + (int64_t)(wm * 128 + mb * 16 + rl) * ldc;
 #pragma unroll
-          for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              float o[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
-              if (!E) {
-                store4(rp + col(nb, g), o, true, 4);
-              } else {
-                const int rem = nlim - (cl + col(nb, g));
-                const int cnt = rem <= 0 ? 0 : (rem >= 4 ? 4 : rem);
-                if (mm < mlim && cnt > 0) store4(rp + col(nb, g), o, cnt == 4, cnt);
-              }
-              __builtin_amdgcn_sched_barrier(0);
-            }
+          for (int pr = 0; pr < 4; ++pr) {
+            const int nb = (pr >> 1) * 4 + (pr & 1) * 2;  // block pairs (0,1) (2,3) (4,5) (6,7)
+            float xv[4], yv[4];
+            trade16(c[mb][nb], c[mb][nb + 1], xv, yv);
+            float* p = rp + col16(nb, wn) + cg;
+            *reinterpret_cast<float4*>(p) = make_float4(xv[0], xv[1], xv[2], xv[3]);
+            *reinterpret_cast<float4*>(p + 4) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
-      };
-      if (mlim == 256 && nlim == 256) part(std::false_type{});
-      else part(std::true_type{});
+        return;
+      }
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        const int mm = wm * 128 + mb * 16 + rl;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const int cc = col16(nb, wn) + cq;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float v = acc16_get(c[mb][nb], e);
+            if (mm < mlim && cc + e < nlim) D[(int64_t)mm * ldc + cc + e] = v;
+          }
+        }
+      }
       return;
     }
     T* C = static_cast<T*>(P.C) + (int64_t)x.m0 * ldc + x.n0;
-    // 16-byte accesses need 16-byte aligned rows (uniform test: the library's
-    // own outputs always pass; the general entry may not)
     const bool wide = sizeof(T) == 2 && ldc % 8 == 0 && reinterpret_cast<uintptr_t>(P.C) % 16 == 0;
     if (mlim == 256 && nlim == 256 && wide) {
-      // Interior tile, 16-byte accesses.  Lanes l and l + 32 hold the two
-      // 4-column halves of each 8-column group of the same row;
-      // v_permlane32_swap trades lane l's half of group g + 1 for lane
-      // l + 32's half of group g (no LDS round trip), so lane l then holds
-      // group g whole and lane l + 32 group g + 1: one 16-byte store each.
-      // GEMM_ACC_T trades the fp32 sums, adds the 8 old values of the lane's
-      // group (one 16-byte load) and rounds once.  The loads of C for two
-      // row blocks go out before the first add, so one memory latency covers
-      // 16 groups.
-      const bool hi = lane >= 32;
-      const int cq = wn * 64;  // tile column of the lanes' 8-column group 0, block 0
-      auto gcol = [&](int nb, int g) { return cq + col(nb, g + (hi ? 1 : 0)); };
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        uint4 cv[2][4][2];
+      for (int hh = 0; hh < 4; ++hh) {
+        uint4 cv[2][4];
         if constexpr (MODE == GEMM_ACC_T) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const T* rp = C + (int64_t)(wm * 128 + (2 * hh + j) * 32 + (lane & 31)) * ldc;
+            const T* rp = C + (int64_t)(wm * 128 + (2 * hh + j) * 16 + rl) * ldc;
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-              for (int q = 0; q < 2; ++q) cv[j][nb][q] = *reinterpret_cast<const uint4*>(rp + gcol(nb, 2 * q));
+            for (int pr = 0; pr < 4; ++pr) {
+              const int nb = (pr >> 1) * 4 + (pr & 1) * 2;
+              cv[j][pr] = *reinterpret_cast<const uint4*>(rp + col16(nb, wn) + cg);
+            }
           }
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int mb = 2 * hh + j;
-          T* rp = C + (int64_t)(wm * 128 + mb * 32 + (lane & 31)) * ldc;
+          T* rp = C + (int64_t)(wm * 128 + mb * 16 + rl) * ldc;
 #pragma unroll
-          for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const int g = 2 * q;
-              uint4 out;
-              if constexpr (MODE == GEMM_ACC_T) {
-                float lo[4], up[4];  // the lane's group after the trade: columns 0-3, 4-7
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  const float a = acc_get(c[mb][nb], g * 4 + e), b = acc_get(c[mb][nb], (g + 1) * 4 + e);
-                  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
-                                                                  false);
-                  lo[e] = __uint_as_float(r[0]);
-                  up[e] = __uint_as_float(r[1]);
-                }
-                const uint4 old = cv[j][nb][q];
-                out.x = pack2<T>(lo[0] + lo16<T>(old.x), lo[1] + hi16<T>(old.x));
-                out.y = pack2<T>(lo[2] + lo16<T>(old.y), lo[3] + hi16<T>(old.y));
-                out.z = pack2<T>(up[0] + lo16<T>(old.z), up[1] + hi16<T>(old.z));
-                out.w = pack2<T>(up[2] + lo16<T>(old.w), up[3] + hi16<T>(old.w));
-              } else {
-                float a[4], b[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  a[e] = acc_get(c[mb][nb], g * 4 + e);
-                  b[e] = acc_get(c[mb][nb], (g + 1) * 4 + e);
-                }
-                const auto r0 = __builtin_amdgcn_permlane32_swap(pack2<T>(a[0], a[1]), pack2<T>(b[0], b[1]), false,
-                                                                 false);
-                const auto r1 = __builtin_amdgcn_permlane32_swap(pack2<T>(a[2], a[3]), pack2<T>(b[2], b[3]), false,
-                                                                 false);
-                out = make_uint4(r0[0], r1[0], r0[1], r1[1]);
-              }
-              *reinterpret_cast<uint4*>(rp + gcol(nb, g)) = out;
-              __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-      }
-      return;
-    }
-    if (mlim == 256 && nlim == 256) {
-      // interior tile, 8-byte accesses (rows not 16-byte aligned)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        uint2 cv[2][4][4];
-        if constexpr (MODE == GEMM_ACC_T) {
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const T* rp = C + (int64_t)(wm * 128 + (2 * hh + j) * 32 + (lane & 31)) * ldc + cl;
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-              for (int g = 0; g < 4; ++g) cv[j][nb][g] = *reinterpret_cast<const uint2*>(rp + col(nb, g));
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int mb = 2 * hh + j;
-          T* rp = C + (int64_t)(wm * 128 + mb * 32 + (lane & 31)) * ldc + cl;
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              float o[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
-              if constexpr (MODE == GEMM_ACC_T) {
-                union { T e[4]; uint2 u; } v;
-                v.u = cv[j][nb][g];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] += to_f32(v.e[e]);
-              }
-              store4(rp + col(nb, g), o, true, 4);
-              __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-      }
-      return;
-    }
-    // edge tile: rows past M and columns past N are skipped
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const int mm = wm * 128 + mb * 32 + (lane & 31);
-      T* rp = C + (int64_t)mm * ldc + cl;
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = acc_get(c[mb][nb], g * 4 + e);
-          const int rem = nlim - (cl + col(nb, g));
-          const int cnt = rem <= 0 ? 0 : (rem >= 4 ? 4 : rem);
-          if (mm < mlim && cnt > 0) {
+          for (int pr = 0; pr < 4; ++pr) {
+            const int nb = (pr >> 1) * 4 + (pr & 1) * 2;
+            float xv[4], yv[4];
+            trade16(c[mb][nb], c[mb][nb + 1], xv, yv);
+            uint4 out;
             if constexpr (MODE == GEMM_ACC_T) {
-              float cvf[4];
-              load4(rp + col(nb, g), cvf, cnt == 4, cnt);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) o[e] += cvf[e];
+              const uint4 old = cv[j][pr];
+              out.x = pack2<T>(xv[0] + lo16<T>(old.x), xv[1] + hi16<T>(old.x));
+              out.y = pack2<T>(xv[2] + lo16<T>(old.y), xv[3] + hi16<T>(old.y));
+              out.z = pack2<T>(yv[0] + lo16<T>(old.z), yv[1] + hi16<T>(old.z));
+              out.w = pack2<T>(yv[2] + lo16<T>(old.w), yv[3] + hi16<T>(old.w));
+            } else {
+              out = make_uint4(pack2<T>(xv[0], xv[1]), pack2<T>(xv[2], xv[3]), pack2<T>(yv[0], yv[1]),
+                               pack2<T>(yv[2], yv[3]));
             }
-            store4(rp + col(nb, g), o, cnt == 4, cnt);
+            *reinterpret_cast<uint4*>(rp + col16(nb, wn) + cg) = out;
+            __builtin_amdgcn_sched_barrier(0);
           }
-          __builtin_amdgcn_sched_barrier(0);
         }
+      }
+      return;
+    }
+    // edge tiles and rows that are not 16-byte aligned: 4 columns at a time
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const int mm = wm * 128 + mb * 16 + rl;
+      T* rp = C + (int64_t)mm * ldc;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        const int cc = col16(nb, wn) + cq;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = acc16_get(c[mb][nb], e);
+        const int rem = nlim - cc;
+        const int cnt = rem <= 0 ? 0 : (rem >= 4 ? 4 : rem);
+        if (mm < mlim && cnt > 0) {
+          if constexpr (MODE == GEMM_ACC_T) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (e < cnt) o[e] += to_f32(rp[cc + e]);
+          }
+          store4(rp + cc, o, cnt == 4 && sizeof(T) == 2 && ldc % 4 == 0, cnt);
+        }
+      }
     }
   };
-  pipeline4<T, LA, LB, true, true, true>(acc, lds, ntiles, P.k_per_split, P.lda, P.ldb, tile_info, opnd,
-                                         epilogue);
+  pipeline16<T, LA, LB, true, true, true>(acc, lds, ntiles, P.k_per_split, P.lda, P.ldb,
+                                          tile_info, opnd, epilogue);
 }
 
 // out[m][n] = sum over s of part[s][m][n] (fixed order), converted to T.
