@@ -127,14 +127,30 @@ __device__ __forceinline__ void fused_logits(f32x16 (&acc)[4][2], char* lds, con
 }
 
 // ------------------------------------------------------------- scan kernel
+// Where a lane's values of one token sit in the tile: kMB x kR accumulator
+// elements (mb, r) at vocabulary row vlane0 + row(mb, r) (vlane0: the lane's
+// first row).  32x32 blocks: 4 blocks x 16 elements, rows 8 (r / 4) + r % 4
+// apart within a block; 16x16 blocks: 8 blocks x 4 consecutive rows.
+struct Layout32 {
+  static constexpr int kMB = 4, kR = 16;
+  __device__ static constexpr int row(int mb, int r) { return mb * 32 + (r >> 2) * 8 + (r & 3); }
+};
+struct Layout16 {
+  static constexpr int kMB = 8, kR = 4;
+  __device__ static constexpr int row(int mb, int r) { return mb * 16 + r; }
+};
+
 // Logit accessors for the scan epilogues: s(mb, r) / t(mb, r) = student /
-// teacher logit of the lane's token at accumulator row (mb, r) of the tile.
+// teacher logit of the lane's token at accumulator element (mb, r) of the
+// tile, laid out as Lay says.
 struct AccPair2 {  // two-stage engine: acc[mb][0] student, acc[mb][1] teacher
+  using Lay = Layout32;
   const f32x16 (&a)[4][2];
   __device__ __forceinline__ float s(int mb, int r) const { return a[mb][0][r]; }
   __device__ __forceinline__ float t(int mb, int r) const { return a[mb][1][r]; }
 };
 struct AccPair4 {  // ring engine, the lane's token j: acc[mb][j] student, acc[mb][j + 2] teacher
+  using Lay = Layout32;
   const Acc4& a;
   int j;
   __device__ __forceinline__ float s(int mb, int r) const { return acc_get(a[mb][j], r); }
@@ -148,8 +164,8 @@ struct AccPair4 {  // ring engine, the lane's token j: acc[mb][j] student, acc[m
 template <class AP>
 __device__ __forceinline__ void acc_fence(const AP&) {}
 
-// Phase 0: online softmax statistics of this lane's token over its 64
-// vocabulary rows of the tile.  Template flags remove work that the problem
+// Phase 0: online softmax statistics of this lane's token over its
+// vocabulary rows of the tile (64 or 32, AP::Lay).  Template flags remove work that the problem
 // does not need (NPOW: the power family's terms, 1 or up to 3, P.npow).
 template <bool HAS_T, int FAM, bool T1, bool MASK, class AP, int NPOW = 3>
 __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0, int64_t vlimit,
@@ -157,10 +173,10 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
   const float invT = P.invT;
   float tms = -kInf, tmt = -kInf, tmu0 = -kInf, tmu1 = -kInf, tmu2 = -kInf;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < AP::Lay::kMB; ++mb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
+    for (int r = 0; r < AP::Lay::kR; ++r) {
+      if (MASK && vlane0 + AP::Lay::row(mb, r) >= vlimit) continue;
       const float xs = acc.s(mb, r);
       tms = fmaxf(tms, xs);
       if (HAS_T) {
@@ -226,10 +242,10 @@ __device__ __forceinline__ void scan_tile(RowState& S, const AP& acc, int vlane0
   const float cT = invT * kLog2e, msT2 = nms * cT, mtT2 = nmt * cT;
   float lx2 = 0.f;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < AP::Lay::kMB; ++mb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
+    for (int r = 0; r < AP::Lay::kR; ++r) {
+      if (MASK && vlane0 + AP::Lay::row(mb, r) >= vlimit) continue;
       const float xs = acc.s(mb, r);
       const float es = __builtin_amdgcn_exp2f(fmaf(xs, kLog2e, -ms2));
       S.ss += es;
@@ -315,10 +331,10 @@ __device__ __forceinline__ void rowsum_tile(RowState& S, const AP& acc, int vlan
   const float invT = P.invT;
   float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < AP::Lay::kMB; ++mb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if (MASK && vlane0 + mb * 32 + (r >> 2) * 8 + (r & 3) >= vlimit) continue;
+    for (int r = 0; r < AP::Lay::kR; ++r) {
+      if (MASK && vlane0 + AP::Lay::row(mb, r) >= vlimit) continue;
       const float lps = acc.s(mb, r) * invT - lse_sT;
       const float lpt = acc.t(mb, r) * invT - lse_tT;
       two_term<DIV>(lps, lpt, P.mix_w, P.mix_w1, s0, s1);
@@ -724,6 +740,7 @@ __device__ __forceinline__ void store_block4(const Acc4& acc, const FusedParams&
     }
 }
 struct AccPairS {  // student only: accumulator block nb (the teacher accessor is never used)
+  using Lay = Layout32;
   const Acc4& a;
   int nb;
   __device__ __forceinline__ float s(int mb, int r) const { return acc_get(a[mb][nb], r); }
@@ -731,6 +748,7 @@ struct AccPairS {  // student only: accumulator block nb (the teacher accessor i
 };
 template <class T>
 struct AccPairTL {  // student from accumulator block nb, teacher from ordered raw registers
+  using Lay = Layout32;
   const Acc4& a;
   int nb;
   const uint2 (&tr)[16];
@@ -898,6 +916,185 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
       const float* sv = xch + ((wn * NJ + j) * kNStat) * 32 + lane;
 #pragma unroll
       for (int f = 0; f < kNStat; ++f) od[f] = sv[f * 32];
+      merge_any<kPhase1>(st[j], o, P);
+      if (tok[j] < P.N) {
+        float* dst = P.partial + (int64_t)vr * kNStat * P.N + tok[j];
+        const float* v = reinterpret_cast<const float*>(&st[j]);
+#pragma unroll
+        for (int f = 0; f < kNStat; ++f) dst[(int64_t)f * P.N] = v[f];
+      }
+    }
+  }
+}
+
+// ------------------------------------------- tied scan, 16x16x32 MFMAs
+// The tied scan (TL_NONE: 128 tokens per workgroup, B = the student's hidden
+// rows then the teacher's) on pipeline16.  Wave (wm, wn): vocabulary rows
+// wm * 128 .., tokens wn * 64 + 16 j + lane % 16 (j < 4): student block j,
+// teacher block j + 4; each lane holds 4 tokens x 32 rows (8 blocks x 4
+// consecutive rows from 4 (lane / 16)).
+struct AccPair16 {
+  using Lay = Layout16;
+  const Acc16& a;
+  int j;
+  __device__ __forceinline__ float s(int mb, int r) const { return acc16_get(a[mb][j], r); }
+  __device__ __forceinline__ float t(int mb, int r) const { return acc16_get(a[mb][j + 4], r); }
+};
+
+// The quad's 4 tokens x 1 row of block (mb, nb), packed and transposed in the
+// quad (lane q of the quad holds row 4 (lane / 16) + q).
+template <class T>
+__device__ __forceinline__ uint2 quad_row16(const Acc16& acc, int mb, int nb) {
+  uint32_t x[2], o[2];
+  x[0] = pack2<T>(acc16_get(acc[mb][nb], 0), acc16_get(acc[mb][nb], 1));
+  x[1] = pack2<T>(acc16_get(acc[mb][nb], 2), acc16_get(acc[mb][nb], 3));
+  quad_transpose16(x, o);
+  return make_uint2(o[0], o[1]);
+}
+
+// The tile's logits to Lout[v][t] (student columns from 0, teacher columns
+// from tcolL when store_t), as store_logits4: full 8-byte stores by each quad
+// whose first token is below N (a quad straddling N writes into the padding
+// columns [N, nP) of its half).
+template <class T>
+__device__ __forceinline__ void store_logits16(const Acc16& acc, const FusedParams& P, int64_t v0, int64_t t0) {
+  const int lane = opaque_lane();
+  const int wm = w4_m(), wn = w4_n();
+  const int q = lane & 3;
+  T* L = static_cast<T*>(P.Lout);
+  if (t0 + 128 <= P.N) {
+    const int64_t ldb = P.ldL * (int64_t)sizeof(T);
+    const int64_t rows = min<int64_t>(P.V - v0, 256);
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(L + v0 * P.ldL + t0, rows * ldb);
+    const uint32_t lane_off = (uint32_t)(wm * 128 + (lane >> 4) * 4 + q) * (uint32_t)ldb +
+                              (uint32_t)(wn * 64 + (lane & 15) - q) * (uint32_t)sizeof(T);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      if (nb >= 4 && !P.store_t) break;
+      const int64_t tok = (nb & 3) * 16 + (nb >= 4 ? P.tcolL : 0);
+      const uint32_t nb_off = lane_off + (uint32_t)(tok * (int64_t)sizeof(T));
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        const uint2 o = quad_row16<T>(acc, mb, nb);
+        const u2v_t d = {o.x, o.y};
+        __builtin_amdgcn_raw_buffer_store_b64(d, rs, (int)(nb_off + (uint32_t)(mb * 16) * (uint32_t)ldb), 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    if (nb >= 4 && !P.store_t) break;
+    const int64_t tb = t0 + wn * 64 + (nb & 3) * 16 + (lane & 15) - q;  // quad's first token
+    const bool tok_ok = tb < P.N;
+    const int64_t col = tb + (nb >= 4 ? P.tcolL : 0);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const int64_t v = v0 + wm * 128 + mb * 16 + (lane >> 4) * 4 + q;
+      const uint2 o = quad_row16<T>(acc, mb, nb);
+      if (v < P.V && tok_ok) *reinterpret_cast<uint2*>(L + v * P.ldL + col) = o;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+// Exchange a RowState with lane l ^ m of the same wave.
+__device__ __forceinline__ RowState shfl_state(const RowState& s, int m) {
+  RowState o;
+  o.ms = __shfl_xor(s.ms, m); o.ss = __shfl_xor(s.ss, m);
+  o.mt = __shfl_xor(s.mt, m); o.st = __shfl_xor(s.st, m);
+  o.sst = __shfl_xor(s.sst, m); o.stt = __shfl_xor(s.stt, m);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) o.x[i] = __shfl_xor(s.x[i], m);
+  return o;
+}
+
+// k_scan4's tied path (TL_NONE, 16-bit) on pipeline16: the same workgroup ->
+// (128 tokens, vocabulary range) mapping, partial output and logits store.
+template <class T, int SV, bool STORE>
+__global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
+  constexpr int NJ = 4;  // tokens per lane
+  __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
+  Acc16 acc;
+  zero_acc16(acc);
+  constexpr bool kPhase1 = sv_phase1(SV);
+  const int lane = threadIdx.x & 63;
+  const int wm = w4_m(), wn = w4_n();
+  int tt, vr;
+  grouped_tile<4>(xcd_order(blockIdx.x, gridDim.x), P.n_ttiles, P.n_vranges, tt, vr);
+  const int64_t t0 = (int64_t)tt * 128;
+  const int vt_begin = vr * P.tiles_per_range;
+  const int ntiles = min(vt_begin + P.tiles_per_range, P.n_vtiles) - vt_begin;
+
+  RowState st[NJ];
+  int64_t tok[NJ];
+  float lse_sT[NJ], lse_tT[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    state_init_fam(st[j], kPhase1 ? FAM_NONE : P.fam);
+    tok[j] = t0 + wn * 64 + j * 16 + (lane & 15);
+    lse_sT[j] = lse_tT[j] = 0.f;
+    if (kPhase1 && tok[j] < P.N) {
+      lse_sT[j] = P.rowp[1 * P.N + tok[j]];
+      lse_tT[j] = P.rowp[3 * P.N + tok[j]];
+    }
+  }
+  const T* W = static_cast<const T*>(P.W);
+  const T* hs = static_cast<const T*>(P.hs);
+  const T* ht = static_cast<const T*>(P.ht);
+  const KOp4 bop = kop4_split(hs + t0 * P.H, P.N - t0, ht + t0 * P.H, P.N - t0, P.H);
+  struct TI {
+    int v0;
+    KOp4 a;
+  };
+  auto tile_info = [&](int i) {
+    TI x;
+    x.v0 = (vt_begin + (i < ntiles ? i : 0)) * 256;
+    x.a = kop4(W + (int64_t)x.v0 * P.H, P.H, P.V - x.v0);
+    return x;
+  };
+  auto opnd = [&](const TI& x, int op) { return op == 0 ? x.a : bop; };
+  auto epilogue = [&](int, const TI& x, Acc16& c) __attribute__((always_inline)) {
+    const int vlane0 = wm * 128 + (opaque_lane() >> 4) * 4;
+    const int64_t vlimit = P.V - x.v0;
+    if constexpr (STORE) store_logits16<T>(c, P, x.v0, t0);
+    static_for<0, NJ>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      scan_variant<SV>(st[j], AccPair16{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+    });
+  };
+  pipeline16<T, KMAJ, KMAJ, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
+
+  // combine lanes l ^ 16 and l ^ 32 (other vocabulary rows of the same
+  // tokens), then the two waves sharing the tokens (wm 0 / 1)
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    RowState o = shfl_state(st[j], 16);
+    merge_any<kPhase1>(st[j], o, P);
+    o = shfl_state(st[j], 32);
+    merge_any<kPhase1>(st[j], o, P);
+  }
+  __syncthreads();
+  float* xch = reinterpret_cast<float*>(lds);  // [wn][j][kNStat][16]
+  if (wm == 1 && lane < 16) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      float* d = xch + ((wn * NJ + j) * kNStat) * 16 + lane;
+      const float* sv = reinterpret_cast<const float*>(&st[j]);
+#pragma unroll
+      for (int f = 0; f < kNStat; ++f) d[f * 16] = sv[f];
+    }
+  }
+  __syncthreads();
+  if (wm == 0 && lane < 16) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      RowState o;
+      float* od = reinterpret_cast<float*>(&o);
+      const float* sv = xch + ((wn * NJ + j) * kNStat) * 16 + lane;
+#pragma unroll
+      for (int f = 0; f < kNStat; ++f) od[f] = sv[f * 16];
       merge_any<kPhase1>(st[j], o, P);
       if (tok[j] < P.N) {
         float* dst = P.partial + (int64_t)vr * kNStat * P.N + tok[j];
@@ -2214,7 +2411,7 @@ inline bool scan_on_ring(const FusedParams& P) {
   case SV:                                                                                       \
     if constexpr (sizeof(T) == 2) {                                                              \
       if (scan_on_ring<T>(P)) {                                                                  \
-        hipLaunchKernelGGL((k_scan4<T, SV, false, TL_NONE>), dim3(grid), dim3(kThreads4), 0, s, P);       \
+        hipLaunchKernelGGL((k_scan16<T, SV, false>), dim3(grid), dim3(kThreads4), 0, s, P);      \
         break;                                                                                   \
       }                                                                                          \
     }                                                                                            \
@@ -2601,7 +2798,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
         break;                                                                                   \
       }                                                                                          \
       if (scan_on_ring<T>(P)) {                                                                  \
-        hipLaunchKernelGGL((k_scan4<T, SV, true, TL_NONE>), dim3(grid), dim3(kThreads4), 0, s, P); \
+        hipLaunchKernelGGL((k_scan16<T, SV, true>), dim3(grid), dim3(kThreads4), 0, s, P);       \
         break;                                                                                   \
       }                                                                                          \
     }                                                                                            \
