@@ -62,20 +62,30 @@ template <> struct Mma16<f16> {
 // lane l holds K elements 8 (l / 16) .. + 7.  K-major: one 16-byte read;
 // MN-major: two transposed reads (4 K rows each; waited for and tied by the
 // caller).
-template <class T, int L>
+// MN-major slots: chunk c (8 columns) of K row k at c ^ mn_swz(k).  With
+// both operands MN-major (PERM) the swizzle takes k % 8 and a lane's K
+// elements are 4 (l / 16) .. + 3 and 16 + 4 (l / 16) .. + 3 (any K order
+// serves when both operands use it): the 32 lanes of a transposed read then
+// cover 8 consecutive K rows of 16 columns on distinct banks.  Otherwise
+// (one operand K-major, whose 16-byte reads give 8 consecutive K) k % 4.
+template <bool PERM>
+__device__ __forceinline__ int mn_swz(int k) { return PERM ? (k & 7) << 1 : (k & 3) << 2; }
+
+template <class T, int L, bool PERM = false>
 __device__ __forceinline__ typename Traits<T>::Frag frag16(const char* tile, int row0, int hf, int lane) {
   if constexpr (L == KMAJ) {
+    static_assert(!PERM, "K-major fragments hold 8 consecutive K");
     const int r = row0 + (lane & 15);
     const int c = hf * 4 + (lane >> 4);
     return *reinterpret_cast<const typename Traits<T>::Frag*>(tile + r * 128 + ((c ^ kswz(r)) << 4));
   } else {
     const int g = lane >> 4, s = lane & 15;
-    const int k = hf * 32 + 8 * g + (s >> 2);
+    const int k = PERM ? hf * 32 + 4 * g + (s >> 2) : hf * 32 + 8 * g + (s >> 2);
     const int m = row0 + 4 * (s & 3);
     const int c = m >> 3, b = (m & 7) * 2;
-    const s16x4 lo = lds_read_tr16(tile + k * 512 + ((c ^ ((k & 3) << 2)) << 4) + b);
-    const int k4 = k + 4;
-    const s16x4 hi = lds_read_tr16(tile + k4 * 512 + ((c ^ ((k4 & 3) << 2)) << 4) + b);
+    const s16x4 lo = lds_read_tr16(tile + k * 512 + ((c ^ mn_swz<PERM>(k)) << 4) + b);
+    const int k4 = PERM ? k + 16 : k + 4;
+    const s16x4 hi = lds_read_tr16(tile + k4 * 512 + ((c ^ mn_swz<PERM>(k4)) << 4) + b);
     const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_bit_cast(typename Traits<T>::Frag, both);
   }
@@ -101,8 +111,9 @@ __device__ __forceinline__ void pipeline16(Acc16& acc, char* lds, int ntiles, in
   const int lane0 = threadIdx.x & 63;
   const uint32_t krow0 = (uint32_t)(w * 8 + (lane0 >> 3));
   const uint32_t kcb = (uint32_t)(((lane0 & 7) ^ kswz((int)krow0)) * 16);
+  constexpr bool kPerm = LA == MNMAJ && LB == MNMAJ;
   const uint32_t mdk = (uint32_t)(2 * w + (lane0 >> 5));
-  const int mcol = ((lane0 & 31) ^ (((int)mdk & 3) << 2)) * 8;
+  const int mcol = ((lane0 & 31) ^ mn_swz<kPerm>((int)mdk)) * 8;
   const uint32_t ldbs[2] = {(uint32_t)(lda * (int64_t)sizeof(T)), (uint32_t)(ldb * (int64_t)sizeof(T))};
   struct Step {
     KOp4 o;
@@ -167,11 +178,11 @@ __device__ __forceinline__ void pipeline16(Acc16& acc, char* lds, int ntiles, in
     constexpr int kPerQ = kMfmaHalf / 8;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      fa[br][q] = frag16<T, LA>(as, wm * 128 + q * 16, hf, lane);
+      fa[br][q] = frag16<T, LA, kPerm>(as, wm * 128 + q * 16, hf, lane);
       next();
       if (live_dma(op, q)) chunk(st, op, q, sb);
       next();
-      if (live_b(q)) fb[br][q] = frag16<T, LB>(bs, col16(q, wn), hf, lane);
+      if (live_b(q)) fb[br][q] = frag16<T, LB, kPerm>(bs, col16(q, wn), hf, lane);
 #pragma unroll
       for (int i = 2; i < kPerQ; ++i) next();
     }
@@ -200,8 +211,8 @@ __device__ __forceinline__ void pipeline16(Acc16& acc, char* lds, int ntiles, in
     const int lane = opaque_lane();
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      fa[0][q] = frag16<T, LA>(slot(0), wm * 128 + q * 16, 0, lane);
-      if (live_b(q)) fb[0][q] = frag16<T, LB>(slot(1), col16(q, wn), 0, lane);
+      fa[0][q] = frag16<T, LA, kPerm>(slot(0), wm * 128 + q * 16, 0, lane);
+      if (live_b(q)) fb[0][q] = frag16<T, LB, kPerm>(slot(1), col16(q, wn), 0, lane);
     }
     end_half(0);
   }
