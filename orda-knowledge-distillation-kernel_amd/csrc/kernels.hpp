@@ -1588,13 +1588,16 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
     T* C = static_cast<T*>(P.C) + (int64_t)x.m0 * ldc + x.n0;
     const bool wide = sizeof(T) == 2 && ldc % 8 == 0 && reinterpret_cast<uintptr_t>(P.C) % 16 == 0;
     if (mlim == 256 && nlim == 256 && wide) {
+      // GEMM_ACC_T: the old values of kRB row blocks (16 kRB rows x 256
+      // bytes per wave) are loaded before the first add
+      constexpr int kRB = 4;
 #pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        uint4 cv[2][4];
+      for (int hh = 0; hh < 8 / kRB; ++hh) {
+        uint4 cv[kRB][4];
         if constexpr (MODE == GEMM_ACC_T) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const T* rp = C + (int64_t)(wm * 128 + (2 * hh + j) * 16 + rl) * ldc;
+          for (int j = 0; j < kRB; ++j) {
+            const T* rp = C + (int64_t)(wm * 128 + (kRB * hh + j) * 16 + rl) * ldc;
 #pragma unroll
             for (int pr = 0; pr < 4; ++pr) {
               const int nb = (pr >> 1) * 4 + (pr & 1) * 2;
@@ -1603,8 +1606,8 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
           }
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int mb = 2 * hh + j;
+        for (int j = 0; j < kRB; ++j) {
+          const int mb = kRB * hh + j;
           T* rp = C + (int64_t)(wm * 128 + mb * 16 + rl) * ldc;
 #pragma unroll
           for (int pr = 0; pr < 4; ++pr) {

@@ -397,6 +397,14 @@ __device__ __forceinline__ s16x4 lds_read_tr16(const char* p) {
   asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(a));
   return v;
 }
+// The same at LDS byte address a + OFF (OFF an immediate below 65536).
+template <int OFF>
+__device__ __forceinline__ s16x4 lds_read_tr16_at(uint32_t a) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  s16x4 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+  return v;
+}
 
 // Wait for every LDS read of this wave, then pass x through an empty asm
 // so any later use of x is ordered after the wait.

@@ -141,6 +141,42 @@ __device__ __forceinline__ void pipeline16(Acc16& acc, char* lds, int ntiles, in
     __builtin_amdgcn_raw_ptr_buffer_load_lds(st.o.r[h], (__attribute__((address_space(3))) void*)(sb + (q * 4 + w) * 1024),
                                              16, st.vb, so, 0, 0);
   };
+  // K-major fragment reads (frag16's): lane l reads row l % 16 of a block
+  // whose first row is a multiple of 16, so the swizzle kswz(row) depends on
+  // l % 16 alone and the lane's byte offset in a block is one value per half
+  // (chunk 4 hf + l / 16); the block's offset is then a constant, and a
+  // fragment read one add of the slot address and an immediate offset.
+  uint32_t koff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = lane0 & 15;
+    koff[h] = (uint32_t)(r * 128 + (((h * 4 + (lane0 >> 4)) ^ kswz(r)) << 4));
+  }
+  // MN-major fragment reads (frag16's): lane l = 16 g + s reads K rows k and
+  // k + dk at columns row0 + 4 (s % 4) .., with k = 32 hf + k0(l).  For row0
+  // a multiple of 16 their byte offset in the slot is
+  //   32 hf * 512 + k0 * 512 + 8 (s % 4) + ((2 row0) ^ msw),
+  // msw = mn_swz(k0) * 16 < 256 (mn_swz sees k % 8, the same for k, k + dk
+  // and either half).  A's rows wm * 128 + 16 q give wm * 256 + (32 q ^ msw);
+  // B's col16(q, wn) give (2 col16(q, 0)) ^ (msw ^ 128 wn).  So a read is
+  // one xor-add of a constant into a per-half base, and the k + dk read an
+  // immediate offset of the k read.
+  uint32_t mbase = 0, mswa = 0, mswb = 0;
+  if constexpr (kTr) {
+    const int g = lane0 >> 4, s4 = lane0 & 15;
+    const int k0 = (kPerm ? 4 * g : 8 * g) + (s4 >> 2);
+    mbase = (uint32_t)(k0 * 512 + 8 * (s4 & 3));
+    mswa = (uint32_t)(mn_swz<kPerm>(k0) << 4);
+    mswb = mswa ^ (uint32_t)(wn * 128);
+  }
+  constexpr int kDk = (kPerm ? 16 : 4) * 512;
+  auto frag_mn = [&](uint32_t a) __attribute__((always_inline)) {
+    const s16x4 lo = lds_read_tr16_at<0>(a);
+    const s16x4 hi = lds_read_tr16_at<kDk>(a);
+    const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(Frag, both);
+  };
+  auto lds_addr = [](const char* p) { return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p; };
   constexpr int kNB = (H0 ? 4 : 0) + (H1 ? 4 : 0);  // live B blocks
   constexpr int kMfmaHalf = 8 * kNB;                // MFMAs per half step
 
@@ -164,7 +200,8 @@ __device__ __forceinline__ void pipeline16(Acc16& acc, char* lds, int ntiles, in
     char* sb = slot(jd);
     const char* as = slot(ja);
     const char* bs = slot(jb);
-    const int lane = opaque_lane();
+    const uint32_t mha = lds_addr(as) + (uint32_t)(hf * 16384 + wm * 256) + mbase;  // MN-major A: half base
+    const uint32_t mhb = lds_addr(bs) + (uint32_t)(hf * 16384) + mbase;              // MN-major B
     int n = 0;  // MFMAs issued so far (compile-time after unrolling)
     auto next = [&]() __attribute__((always_inline)) {
       // the n-th live (mb, nb), mb-major
@@ -175,16 +212,34 @@ __device__ __forceinline__ void pipeline16(Acc16& acc, char* lds, int ntiles, in
       else Mma16<T>::mma(acc[mb][nb], fa[bm][mb], fb[bm][nb]);
       ++n;
     };
-    constexpr int kPerQ = kMfmaHalf / 8;
+    constexpr int kPerQ = kMfmaHalf / 8;  // MFMAs per group q
+    const uint32_t ko = hf ? koff[1] : koff[0];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      fa[br][q] = frag16<T, LA, kPerm>(as, wm * 128 + q * 16, hf, lane);
-      next();
+      int m = 0;  // q's MFMAs issued so far (compile-time)
+      auto mm = [&]() __attribute__((always_inline)) {
+        if (m < kPerQ) {
+          next();
+          ++m;
+        }
+      };
+      if constexpr (LA == KMAJ)
+        fa[br][q] = *reinterpret_cast<const Frag*>(as + (wm * 128 + q * 16) * 128 + ko);
+      else
+        fa[br][q] = frag_mn(mha + ((uint32_t)(32 * q) ^ mswa));
+      mm();
       if (live_dma(op, q)) chunk(st, op, q, sb);
-      next();
-      if (live_b(q)) fb[br][q] = frag16<T, LB, kPerm>(bs, col16(q, wn), hf, lane);
+      mm();
+      if (live_b(q)) {
+        if constexpr (LB == KMAJ)
+          fb[br][q] = *reinterpret_cast<const Frag*>(bs + col16(q, wn) * 128 + ko);
+        else
+          fb[br][q] = frag_mn(mhb + ((uint32_t)(2 * col16(q, 0)) ^ mswb));
+      }
+      mm();
 #pragma unroll
-      for (int i = 2; i < kPerQ; ++i) next();
+      for (int i = 0; i < kPerQ; ++i)
+        if (i >= m) next();
     }
   };
   auto end_half = [&](int buf_read) {

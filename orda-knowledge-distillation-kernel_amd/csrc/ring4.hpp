@@ -220,6 +220,17 @@ __device__ __forceinline__ void pipeline4(Acc4& acc, char* lds, int ntiles, int6
     __builtin_amdgcn_raw_ptr_buffer_load_lds(st.o.r[h], (__attribute__((address_space(3))) void*)(sb + (q * 4 + w) * 1024),
                                              16, st.vb, so, 0, 0);
   };
+  // K-major fragment reads (frag4's): lane l reads row l % 32 of a block
+  // whose first row is a multiple of 32, so kswz(row) depends on l % 32 alone
+  // and the lane's byte offset in a block is one value per sub-step ks
+  // (chunk 2 ks + l / 32); a read is then one add of the slot address, with
+  // the block's offset an immediate.
+  uint32_t koff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int r = lane0 & 31;
+    koff[ks] = (uint32_t)(r * 128 + (((ks * 2 + (lane0 >> 5)) ^ kswz(r)) << 4));
+  }
   constexpr int kNB = (H0 ? 2 : 0) + (H1 ? 2 : 0);  // live B blocks
   constexpr int kMfmaHalf = 2 * 4 * kNB;            // MFMAs per half step
 
@@ -250,9 +261,17 @@ __device__ __forceinline__ void pipeline4(Acc4& acc, char* lds, int ntiles, int6
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int h = q >> 2, x = q & 3, ks = hf * 2 + h;
-      fa[buf][h][x] = frag4<T, LA>(as, wm * 128 + x * 32, ks, lane);
+      if constexpr (LA == KMAJ)
+        fa[buf][h][x] = *reinterpret_cast<const Frag*>(as + (wm * 128 + x * 32) * 128 + koff[ks]);
+      else
+        fa[buf][h][x] = frag4<T, LA>(as, wm * 128 + x * 32, ks, lane);
       if (live_dma(op, q)) chunk(st, op, q, sb);
-      if (live_b(x)) fb[buf][h][x] = frag4<T, LB>(bs, col4(x, wn), ks, lane);
+      if (live_b(x)) {
+        if constexpr (LB == KMAJ)
+          fb[buf][h][x] = *reinterpret_cast<const Frag*>(bs + col4(x, wn) * 128 + koff[ks]);
+        else
+          fb[buf][h][x] = frag4<T, LB>(bs, col4(x, wn), ks, lane);
+      }
     }
   };
   auto mfma_half = [&](int buf) {

@@ -85,6 +85,14 @@ __device__ __forceinline__ void pipeline4_f8(Acc4& acc, char* lds, int ntiles, i
                                              16, st.vb, so, 0, 0);
   };
 
+  // frag8's lane offsets, one per (ks, part): row l % 32 of a block whose
+  // first row is a multiple of 32 (kswz depends on l % 32 alone)
+  uint32_t koff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (threadIdx.x & 63) & 31;
+    koff[i] = (uint32_t)(r * 128 + ((((i >> 1) * 4 + ((threadIdx.x & 63) >> 5) * 2 + (i & 1)) ^ kswz(r)) << 4));
+  }
   i32x4 fa[2][4][2], fb[2][4][2];
   // fragment reads of sub-step ks from slots (ja, jb) into buffer buf,
   // interleaved with one operand step's DMA into slot jd: per q, A piece,
@@ -93,13 +101,13 @@ __device__ __forceinline__ void pipeline4_f8(Acc4& acc, char* lds, int ntiles, i
     char* sbuf = slot(jd);
     const char* as = slot(ja);
     const char* bs = slot(jb);
-    const int lane = opaque_lane();
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int x = q & 3, part = q >> 2;
-      fa[buf][x][part] = frag8(as, wm * 128 + x * 32, ks, part, lane);
+      const uint32_t ko = koff[ks * 2 + part];
+      fa[buf][x][part] = *reinterpret_cast<const i32x4*>(as + (wm * 128 + x * 32) * 128 + ko);
       chunk(st, q, sbuf);
-      fb[buf][x][part] = frag8(bs, col4(x, wn), ks, part, lane);
+      fb[buf][x][part] = *reinterpret_cast<const i32x4*>(bs + col4(x, wn) * 128 + ko);
     }
   };
   int sa[4];
