@@ -53,44 +53,46 @@ struct LaunchEntry {
 // dtype: 0 = bf16, 1 = f16 (orda_dtype).
 constexpr LaunchEntry kLaunchTable[] = {
     // config 2: tied, N = 8192, H = 4096, V = 128256.  1024-token chunks
-    // (2048 would pass the 2 GB memory ceiling); 4 splits: 38.7 ms/step vs
-    // 38.9-39.3 for 8-16 and 42.5-45.3 with 512-token chunks
+    // (2048 would pass the 2 GB memory ceiling); 4 splits: 35.9 ms/step vs
+    // 36.0-36.5 for 8-16 and 39.5-42.3 with 512-token chunks
     {TC_TIED, 0, 128256, 4096, 2, 4, 256, "c2: chunk 512 x 2, split 4"},
     // config 3: separate, Hs = 2048 (teacher 4096), V = 128256.  2048-token
-    // chunks: 20.9 ms/step at 1.69 GB peak extra (4096-token chunks: 20.3 at
-    // 2.82 GB, past the 2 GB the tied config keeps to); 4 splits (8, 16
-    // within noise, more scratch)
+    // chunks: 19.2 ms/step at 1.69 GB peak extra (4096-token chunks: 18.75 at
+    // 2.82 GB, past the 2 GB the tied config keeps to); 4 splits (8: 19.3,
+    // 16: 19.5, more scratch)
     {TC_STAGED, 0, 128256, 2048, 4, 4, 256, "c3: chunk 512 x 4, split 4"},
     // config 4: precomputed logits read in place, H = 4096, V = 128256.
-    // 2048-token chunks: 24.0 ms/step vs 25.8-30.2 with 1024; split 2 = 4
-    // within noise, 67 MB less split-K scratch
+    // 2048-token chunks: 22.4 ms/step vs 24.1-27.8 with 1024; split 2 (4:
+    // 22.5, 67 MB more split-K scratch)
     {TC_INPLACE, 0, 128256, 4096, 4, 2, 256, "c4: chunk 512 x 4, split 2"},
     // config 5: tied, N = 32768, H = 5120, V = 152064 (no memory ceiling
     // beyond reporting it).  2048-token chunks, 8 splits (160 tiles x 8 = 5
-    // full rounds of 256): 216.4 ms/step, peak extra 3.52 GB, vs 229.4 with
-    // 1024-token chunks and 16 splits (2.88 GB); 4 splits 224.5, 16 218.2
+    // full rounds of 256): 202.0 ms/step, peak extra 3.52 GB, vs 213.6 with
+    // 1024-token chunks and 16 splits (2.88 GB); 4 splits 209.4, 16 204.0;
+    // 4096-token chunks 197.5 at 5.14 GB
     {TC_TIED, 0, 152064, 5120, 4, 8, 256, "c5: chunk 512 x 4, split 8"},
     // configs 2-5 in fp16 (dlogits unscaled, gradients scaled once at the
-    // end).  c2f16: 1024-token chunks, 4 splits: 39.9 ms/step at 1.73 GB
-    // (8 splits 40.2, 16 40.5; 512-token chunks 43.7-47.6)
+    // end).  c2f16: 1024-token chunks, 4 splits: 37.8 ms/step at 1.73 GB
+    // (8 splits 37.9, 16 38.4; 512-token chunks 41.7-44.3)
     {TC_TIED, 1, 128256, 4096, 2, 4, 256, "c2f16: chunk 512 x 2, split 4"},
-    // c3f16: 2048-token chunks, 4 splits: 21.4 ms/step at 1.69 GB (8 splits
-    // 21.5; 4096-token chunks 21.1 at 2.82 GB, past the 2 GB budget)
+    // c3f16: 2048-token chunks, 4 splits: 20.4 ms/step at 1.69 GB (8 splits
+    // 20.55; 4096-token chunks 19.7 at 2.82 GB, past the 2 GB budget)
     {TC_STAGED, 1, 128256, 2048, 4, 4, 256, "c3f16: chunk 512 x 4, split 4"},
-    // c4f16: 2048-token chunks, 2 splits: 24.9 ms/step at 1.73 GB (4 splits
-    // equal at 1.80 GB, 8 25.2; 1024-token chunks 26.6-31.7)
+    // c4f16: 2048-token chunks, 2 splits: 23.6 ms/step at 1.73 GB (4 splits
+    // 23.7 at 1.80 GB, 8 23.9; 1024-token chunks 25.4-29.7)
     {TC_INPLACE, 1, 128256, 4096, 4, 2, 256, "c4f16: chunk 512 x 4, split 2"},
-    // c5f16: 2048-token chunks, 8 splits: 220.0 ms/step at 3.52 GB (16
-    // splits 221.7; 1024-token chunks 231.9-259.2 at 2.6-2.9 GB)
+    // c5f16: 2048-token chunks, 8 splits: 205.6 ms/step at 3.52 GB (16
+    // splits 207.5, 4 212.4; 1024-token chunks 224.1 at 2.7 GB; 4096-token
+    // 200.4 at 5.14 GB)
     {TC_TIED, 1, 152064, 5120, 4, 8, 256, "c5f16: chunk 512 x 4, split 8"},
     // two shapes beyond the benchmark configurations, tied, 8192 tokens.
     // Hidden 8192: the gradients alone take 2.2 GB, so no chunk keeps the
-    // 2 GB budget; 2048-token chunks, 2 splits: 72.1 ms/step at 3.49 GB
-    // (1024-token chunks 75.0-75.6, 512-token 82.0-92.2)
+    // 2 GB budget; 2048-token chunks, 2 splits: 65.2 ms/step at 3.49 GB
+    // (1024-token chunks 67.8-68.4; 4096-token 65.0 at 4.74 GB)
     {TC_TIED, 0, 128256, 8192, 4, 2, 256, "h8192: chunk 512 x 4, split 2"},
-    // Hidden 3584, vocabulary 152064: 1024-token chunks, 9 splits: 42.5
-    // ms/step at 1.92 GB (2048-token chunks 40.1-40.5 at 2.5-2.9 GB, past
-    // the 2 GB budget; 512-token chunks 45.9-50.3)
+    // Hidden 3584, vocabulary 152064: 1024-token chunks, 9 splits: 38.2
+    // ms/step at 1.92 GB (2048-token chunks 36.4-37.1 at 2.5-2.9 GB, past
+    // the 2 GB budget; 512-token chunks 42.6-45.6)
     {TC_TIED, 0, 152064, 3584, 2, 9, 256, "h3584: chunk 512 x 2, split 9"},
 };
 constexpr int kLaunchTableSize = (int)(sizeof(kLaunchTable) / sizeof(kLaunchTable[0]));
