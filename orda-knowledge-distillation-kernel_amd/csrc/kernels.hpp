@@ -1010,11 +1010,130 @@ __device__ __forceinline__ RowState shfl_state(const RowState& s, int m) {
   return o;
 }
 
+// Student-only tiles on pipeline16 (TL_FROM_L, TL_FROM_MEM, TL_STUDENT): 256
+// student tokens per workgroup, token block nb of wave (wm, wn) is tokens
+// col16(nb, wn) .. + 15 (lane % 16), rows wm * 128 + mb * 16 + 4 (lane / 16)
+// + e.  As the 32x32 ring's helpers above, with 16-row blocks: the lane's
+// byte offset of block nb in a vocabulary-major tile of L (the quad's first
+// token, rows 4 (lane / 16) + q), or kOob for a token at or past N.
+template <class T>
+__device__ __forceinline__ uint32_t quad_off_l16(const TileRowsL& r, const FusedParams& P, int64_t t0, int nb) {
+  const int lane = opaque_lane();
+  const int q = lane & 3;
+  const int tq = col16(nb, w4_n()) + (lane & 15) - q;
+  return t0 + tq < P.N ? (uint32_t)(w4_m() * 128 + (lane >> 4) * 4 + q) * r.ldb + (uint32_t)tq * (uint32_t)sizeof(T)
+                       : kOob;
+}
+// Token block nb's teacher logits: 8 raw 8-byte loads (one per 16-row block
+// mb), put in accumulator order by order_teacher16 (raw[mb] then holds rows
+// 4 (lane / 16) .. + 3 of block mb for the lane's token).
+template <class T, int TL>
+__device__ __forceinline__ void issue_teacher16(uint2 (&raw)[8], const FusedParams& P, int64_t v0, int64_t t0,
+                                                int nb) {
+  const int lane = opaque_lane();
+  if constexpr (TL == TL_FROM_L) {
+    const TileRowsL r = tile_rows_l<T>(P.Lout, P, v0, P.tcolL + t0);
+    const uint32_t off = quad_off_l16<T>(r, P, t0, nb);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const u2v_t d = __builtin_amdgcn_raw_buffer_load_b64(r.rs, off, (int)((uint32_t)(mb * 16) * r.ldb), 0);
+      raw[mb] = make_uint2(d.x, d.y);
+    }
+  } else {
+    const int64_t ntok = min<int64_t>(P.N - t0, 256);
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(static_cast<const T*>(P.Lt) + t0 * P.V + v0,
+                                                   (ntok * P.V - v0) * (int64_t)sizeof(T));
+    const int tk = col16(nb, w4_n()) + (lane & 15);  // the lane's token, from t0
+    const int r0 = w4_m() * 128 + (lane >> 4) * 4;   // the lane's row of block 0, from v0
+    const uint32_t dead = (t0 + tk < P.N) ? 0u : kOob;
+    const int rowlim = (int)min<int64_t>(P.V - v0 - r0, 1 << 20);
+    const uint32_t base = ((uint32_t)tk * (uint32_t)P.V + (uint32_t)r0) * (uint32_t)sizeof(T);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const int d = mb * 16;
+      const uint32_t past = (uint32_t)((rowlim - d - 1) >> 31) & kOob;  // d >= rowlim
+      const uint32_t off = (base + (uint32_t)d * (uint32_t)sizeof(T)) | past | dead;
+      const u2v_t x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+      raw[mb] = make_uint2(x.x, x.y);
+    }
+  }
+}
+template <class T, int TL>
+__device__ __forceinline__ void order_teacher16(uint2 (&raw)[8]) {
+  if constexpr (TL == TL_FROM_L) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t x[2] = {raw[i].x, raw[i].y};
+      uint32_t o[2];
+      quad_transpose16(x, o);
+      raw[i] = make_uint2(o[0], o[1]);
+    }
+  }
+}
+// Token block nb's teacher logits (ordered) to Lout's teacher columns.
+template <class T>
+__device__ __forceinline__ void store_teacher16(const uint2 (&tr)[8], const FusedParams& P, int64_t v0, int64_t t0,
+                                                int nb) {
+  const TileRowsL r = tile_rows_l<T>(P.Lout, P, v0, P.tcolL + t0);
+  const uint32_t off = quad_off_l16<T>(r, P, t0, nb);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t x[2] = {tr[i].x, tr[i].y};
+    uint32_t o[2];
+    quad_transpose16(x, o);
+    const u2v_t d = {o[0], o[1]};
+    __builtin_amdgcn_raw_buffer_store_b64(d, r.rs, off, (int)((uint32_t)(i * 16) * r.ldb), 0);
+  }
+}
+// Token block nb's student logits to Lout's student columns.
+template <class T>
+__device__ __forceinline__ void store_block16(const Acc16& acc, const FusedParams& P, int64_t v0, int64_t t0,
+                                              int nb) {
+  const TileRowsL r = tile_rows_l<T>(P.Lout, P, v0, t0);
+  const uint32_t off = quad_off_l16<T>(r, P, t0, nb);
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) {
+    const uint2 o = quad_row16<T>(acc, mb, nb);
+    const u2v_t d = {o.x, o.y};
+    __builtin_amdgcn_raw_buffer_store_b64(d, r.rs, off, (int)((uint32_t)(mb * 16) * r.ldb), 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+struct AccPair16S {  // student only: block j (the teacher accessor is never used)
+  using Lay = Layout16;
+  const Acc16& a;
+  int j;
+  __device__ __forceinline__ float s(int mb, int r) const { return acc16_get(a[mb][j], r); }
+  __device__ __forceinline__ float t(int, int) const { return 0.f; }
+};
+template <class T>
+struct AccPair16TL {  // student from block j, teacher from ordered raw registers
+  using Lay = Layout16;
+  const Acc16& a;
+  int j;
+  const uint2 (&tr)[8];
+  __device__ __forceinline__ float s(int mb, int r) const { return acc16_get(a[mb][j], r); }
+  __device__ __forceinline__ float t(int mb, int r) const {
+    const uint2& u = tr[mb];
+    const uint32_t w = (r & 2) ? u.y : u.x;
+    return (r & 1) ? hi16<T>(w) : lo16<T>(w);
+  }
+};
+template <class T>
+__device__ __forceinline__ void acc_fence(const AccPair16TL<T>& p) {
+  uint2* r = const_cast<uint2*>(p.tr);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(r[i].x), "+v"(r[i].y));
+}
+
 // k_scan4's tied path (TL_NONE, 16-bit) on pipeline16: the same workgroup ->
 // (128 tokens, vocabulary range) mapping, partial output and logits store.
-template <class T, int SV, bool STORE>
+template <class T, int SV, bool STORE, int TL = TL_NONE>
 __global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
-  constexpr int NJ = 4;  // tokens per lane
+  static_assert(TL == TL_NONE || (!sv_phase1(SV) && STORE), "teacher logits from memory: one-pass, stored");
+  static_assert(TL != TL_STUDENT || SV == SV_STUDENT || SV == SV_STUDENT_T, "student-only tiles: no teacher");
+  constexpr int NJ = TL ? 8 : 4;        // tokens per lane
+  constexpr int kTok = TL ? 256 : 128;  // tokens per workgroup
   __shared__ __attribute__((aligned(16))) char lds[kLds4Bytes];
   Acc16 acc;
   zero_acc16(acc);
@@ -1023,27 +1142,28 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
   const int wm = w4_m(), wn = w4_n();
   int tt, vr;
   grouped_tile<4>(xcd_order(blockIdx.x, gridDim.x), P.n_ttiles, P.n_vranges, tt, vr);
-  const int64_t t0 = (int64_t)tt * 128;
+  const int64_t t0 = (int64_t)tt * kTok;
   const int vt_begin = vr * P.tiles_per_range;
   const int ntiles = min(vt_begin + P.tiles_per_range, P.n_vtiles) - vt_begin;
+  // the lane's token j
+  auto tok = [&](int j) { return t0 + (TL ? col16(j, wn) : wn * 64 + j * 16) + (lane & 15); };
 
   RowState st[NJ];
-  int64_t tok[NJ];
   float lse_sT[NJ], lse_tT[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     state_init_fam(st[j], kPhase1 ? FAM_NONE : P.fam);
-    tok[j] = t0 + wn * 64 + j * 16 + (lane & 15);
     lse_sT[j] = lse_tT[j] = 0.f;
-    if (kPhase1 && tok[j] < P.N) {
-      lse_sT[j] = P.rowp[1 * P.N + tok[j]];
-      lse_tT[j] = P.rowp[3 * P.N + tok[j]];
+    if (kPhase1 && tok(j) < P.N) {
+      lse_sT[j] = P.rowp[1 * P.N + tok(j)];
+      lse_tT[j] = P.rowp[3 * P.N + tok(j)];
     }
   }
   const T* W = static_cast<const T*>(P.W);
   const T* hs = static_cast<const T*>(P.hs);
   const T* ht = static_cast<const T*>(P.ht);
-  const KOp4 bop = kop4_split(hs + t0 * P.H, P.N - t0, ht + t0 * P.H, P.N - t0, P.H);
+  const KOp4 bop = TL ? kop4(hs + t0 * P.H, P.H, P.N - t0)
+                      : kop4_split(hs + t0 * P.H, P.N - t0, ht + t0 * P.H, P.N - t0, P.H);
   struct TI {
     int v0;
     KOp4 a;
@@ -1058,11 +1178,36 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
   auto epilogue = [&](int, const TI& x, Acc16& c) __attribute__((always_inline)) {
     const int vlane0 = wm * 128 + (opaque_lane() >> 4) * 4;
     const int64_t vlimit = P.V - x.v0;
-    if constexpr (STORE) store_logits16<T>(c, P, x.v0, t0);
-    static_for<0, NJ>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      scan_variant<SV>(st[j], AccPair16{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
-    });
+    if constexpr (TL == TL_STUDENT) {
+      static_for<0, NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        store_block16<T>(c, P, x.v0, t0, j);
+        scan_variant<SV>(st[j], AccPair16S{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+      });
+    } else if constexpr (TL != TL_NONE) {
+      // blocks j and j + 1 in flight while block j is scanned; block j's
+      // student logits stored after its scan
+      uint2 raw[2][8];
+      issue_teacher16<T, TL>(raw[0], P, x.v0, t0, 0);
+      issue_teacher16<T, TL>(raw[1], P, x.v0, t0, 1);
+      static_for<0, NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        order_teacher16<T, TL>(raw[j & 1]);
+        if constexpr (TL == TL_FROM_MEM) {
+          if (P.store_t) store_teacher16<T>(raw[j & 1], P, x.v0, t0, j);  // else the dlogits pass reads them in place
+        }
+        scan_variant<SV>(st[j], AccPair16TL<T>{c, j, raw[j & 1]}, vlane0, vlimit, vlimit >= 256, lse_sT[j],
+                         lse_tT[j], P);
+        store_block16<T>(c, P, x.v0, t0, j);
+        if constexpr (j + 2 < NJ) issue_teacher16<T, TL>(raw[j & 1], P, x.v0, t0, j + 2);
+      });
+    } else {
+      if constexpr (STORE) store_logits16<T>(c, P, x.v0, t0);
+      static_for<0, NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        scan_variant<SV>(st[j], AccPair16{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
+      });
+    }
   };
   pipeline16<T, KMAJ, KMAJ, true, true, false>(acc, lds, ntiles, P.H, P.H, P.H, tile_info, opnd, epilogue);
 
@@ -1096,8 +1241,8 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
 #pragma unroll
       for (int f = 0; f < kNStat; ++f) od[f] = sv[f * 16];
       merge_any<kPhase1>(st[j], o, P);
-      if (tok[j] < P.N) {
-        float* dst = P.partial + (int64_t)vr * kNStat * P.N + tok[j];
+      if (tok(j) < P.N) {
+        float* dst = P.partial + (int64_t)vr * kNStat * P.N + tok(j);
         const float* v = reinterpret_cast<const float*>(&st[j]);
 #pragma unroll
         for (int f = 0; f < kNStat; ++f) dst[(int64_t)f * P.N] = v[f];
@@ -2786,7 +2931,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
     if constexpr (sizeof(T) == 2) {                                                              \
       if (P.tsrc == TSRC_NONE && P.student_ring) {                                               \
         if constexpr (SV == SV_STUDENT || SV == SV_STUDENT_T)                                    \
-          hipLaunchKernelGGL((k_scan4<T, SV, true, TL_STUDENT>), dim3(grid), dim3(kThreads4), 0, s, P); \
+          hipLaunchKernelGGL((k_scan16<T, SV, true, TL_STUDENT>), dim3(grid), dim3(kThreads4), 0, s, P); \
         else                                                                                     \
           return hipErrorInvalidValue;                                                           \
         break;                                                                                   \
@@ -2797,7 +2942,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bwd(NormParams P) {
         else if (P.tsrc == TSRC_L)                                                               \
           hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_L>), dim3(grid), dim3(kThreads4), 0, s, P); \
         else                                                                                     \
-          hipLaunchKernelGGL((k_scan4<T, SV, true, TL_FROM_MEM>), dim3(grid), dim3(kThreads4), 0, s, P); \
+          hipLaunchKernelGGL((k_scan16<T, SV, true, TL_FROM_MEM>), dim3(grid), dim3(kThreads4), 0, s, P); \
         break;                                                                                   \
       }                                                                                          \
       if (scan_on_ring<T>(P)) {                                                                  \
