@@ -62,8 +62,8 @@ constexpr LaunchEntry kLaunchTable[] = {
     // 16: 19.5, more scratch)
     {TC_STAGED, 0, 128256, 2048, 4, 4, 256, "c3: chunk 512 x 4, split 4"},
     // config 4: precomputed logits read in place, H = 4096, V = 128256.
-    // 2048-token chunks: 22.4 ms/step vs 24.1-27.8 with 1024; split 2 (4:
-    // 22.5, 67 MB more split-K scratch)
+    // 2048-token chunks: 21.7 ms/step vs 23.5-27.2 with 1024; split 2 (4:
+    // 21.8, 67 MB more split-K scratch)
     {TC_INPLACE, 0, 128256, 4096, 4, 2, 256, "c4: chunk 512 x 4, split 2"},
     // config 5: tied, N = 32768, H = 5120, V = 152064 (no memory ceiling
     // beyond reporting it).  2048-token chunks, 8 splits (160 tiles x 8 = 5
@@ -78,8 +78,8 @@ constexpr LaunchEntry kLaunchTable[] = {
     // c3f16: 2048-token chunks, 4 splits: 20.4 ms/step at 1.69 GB (8 splits
     // 20.55; 4096-token chunks 19.7 at 2.82 GB, past the 2 GB budget)
     {TC_STAGED, 1, 128256, 2048, 4, 4, 256, "c3f16: chunk 512 x 4, split 4"},
-    // c4f16: 2048-token chunks, 2 splits: 23.6 ms/step at 1.73 GB (4 splits
-    // 23.7 at 1.80 GB, 8 23.9; 1024-token chunks 25.4-29.7)
+    // c4f16: 2048-token chunks, 2 splits: 22.9 ms/step at 1.73 GB (4 splits
+    // 23.0 at 1.80 GB, 8 23.2; 1024-token chunks 24.6-28.6)
     {TC_INPLACE, 1, 128256, 4096, 4, 2, 256, "c4f16: chunk 512 x 4, split 2"},
     // c5f16: 2048-token chunks, 8 splits: 205.6 ms/step at 3.52 GB (16
     // splits 207.5, 4 212.4; 1024-token chunks 224.1 at 2.7 GB; 4096-token
