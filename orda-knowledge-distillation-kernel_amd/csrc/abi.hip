@@ -416,7 +416,11 @@ int make_plan(const orda_problem_t* p, Plan& pl) {
     pl.fldL = ncol * pl.fnP;
     pl.fnchunks = cdiv(pl.N, n);
     const int64_t ntt = cdiv(n, (pl.f_tl || pl.f_sring) ? 256 : 128);
-    int64_t nvr = cdiv(pl.scan_groups, ntt);
+    // vocabulary ranges per token tile: the scan's ntt x nvr workgroups stay
+    // within scan_groups, so they run in one wave of one per CU (rounding up
+    // put 10 token tiles at 260 workgroups, the last 4 a second wave that
+    // doubled the scan's time)
+    int64_t nvr = pl.scan_groups / ntt;
     if (nvr < 1) nvr = 1;
     if (nvr > pl.n_vtiles) nvr = pl.n_vtiles;
     pl.f_tpr = (int)cdiv(pl.n_vtiles, nvr);

@@ -103,9 +103,10 @@ def _grad_close(name, got, ref, max_frac=2e-2, frob_frac=2e-2):
 
 def _run_fullsize(seed, mode, N, H, V, *, Ht=None, div="forward_kl", T=1.0, w_s=1.0, w_t=None, kl_w=1.0,
                   ignore_frac=0.05, teacher_row_scale=None, profile="balanced", peak_limit=None, max_frac=2e-2,
-                  frob_frac=2e-2, dtype=torch.bfloat16):
+                  frob_frac=2e-2, dtype=torch.bfloat16, chunk=None):
     o = _orda()
-    print(f"case: {mode} N={N} H={H} Ht={Ht} V={V} div={div} T={T} profile={profile} dtype={dtype}", flush=True)
+    print(f"case: {mode} N={N} H={H} Ht={Ht} V={V} div={div} T={T} profile={profile} dtype={dtype} chunk={chunk}",
+          flush=True)
     hs, W, y, ht, Wt, lt = _inputs(seed, mode, N, H, V, Ht=Ht, ignore_frac=ignore_frac,
                                    teacher_row_scale=teacher_row_scale, dtype=dtype)
     hs_d = hs.detach().requires_grad_(True)
@@ -115,7 +116,8 @@ def _run_fullsize(seed, mode, N, H, V, *, Ht=None, div="forward_kl", T=1.0, w_s=
     base = torch.cuda.memory_allocated()
     torch.cuda.reset_peak_memory_stats()
     out = o.distillation_loss(hs_d, W_d, y, teacher, student_ce_weight=w_s, teacher_ce_weight=w_t, kl_weight=kl_w,
-                              kl_temperature=T, backend="triton", divergence=div, profile=profile)
+                              kl_temperature=T, backend="triton", divergence=div, profile=profile,
+                              config=o.KernelConfig(chunk_size=chunk) if chunk else None)
     out.loss.backward()
     torch.cuda.synchronize()
     peak_extra = torch.cuda.max_memory_allocated() - base
@@ -145,6 +147,13 @@ def test_config2_tied_forward_kl_fullsize(profile):
     schedule with fp32 grad-W accumulation."""
     _run_fullsize(1002, "tied", 8192, 4096, 128256, peak_limit=2e9 if profile == "balanced" else None,
                   profile=profile)
+
+
+def test_config2_tied_ragged_chunks_fullsize():
+    """Config 2 with a requested chunk of 640 tokens: 1280-token chunks (10
+    token tiles, which do not divide the 256 scan workgroups: the plan takes
+    25 vocabulary ranges, not 26) and a last chunk of 512."""
+    _run_fullsize(1002, "tied", 8192, 4096, 128256, peak_limit=2e9, chunk=640)
 
 
 @pytest.mark.parametrize("div", ["squared_l2", "ab"])

@@ -342,6 +342,22 @@ def test_launch_table_drives_the_benchmark_configurations(cfg, entry, chunk, spl
     assert info["forward_workspace_bytes"] == _native.forward_workspace_bytes(_cfg_problem(cfg))
 
 
+@pytest.mark.parametrize("token_chunk, tokens_per_tile", [(640, 128), (600, 128), (320, 128), (1000, 128)])
+def test_scan_grid_fits_one_wave_when_token_tiles_do_not_divide_it(token_chunk, tokens_per_tile):
+    """A chunk whose token-tile count does not divide the 256 persistent
+    workgroups (1280 tokens: 10 tiles of 128) gets floor(256 / tiles)
+    vocabulary ranges, not the ceiling: 260 workgroups would run 4 of them in
+    a second wave behind the first and double the scan."""
+    info = _native.plan_info(_problem(flags=0x33 | GIF, token_chunk=token_chunk))
+    assert info["table_entry"] == 0 and info["scan_tokens_per_tile"] == tokens_per_tile
+    ntt = -(-info["token_chunk"] // tokens_per_tile)
+    assert info["scan_workgroups"] <= 256
+    # every vocabulary tile (501 of 256 rows) is still covered by the ranges
+    ranges = info["scan_workgroups"] // ntt
+    assert ranges * ntt == info["scan_workgroups"]
+    assert ranges >= 256 // ntt - 1 and ranges * -(-501 // ranges) >= 501
+
+
 # divergence codes of include/orda_ce.h
 _HELLINGER, _RENYI, _CHI2, _L2, _AB = 4, 6, 8, 9, 10
 
