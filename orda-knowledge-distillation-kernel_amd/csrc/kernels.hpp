@@ -522,6 +522,7 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
 
 // Logits of a ring-engine tile to Lout[v][t] (see store_logits): block
 typedef unsigned int u2v_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u4v_t __attribute__((ext_vector_type(4)));
 
 // A buffer resource over [p, p + bytes) with base and size read through
 // readfirstlane, so it is scalar (p and bytes are wave-uniform, which the
@@ -999,6 +1000,80 @@ __device__ __forceinline__ void store_logits16(const Acc16& acc, const FusedPara
   }
 }
 
+// store_logits16 for a full token tile (t0 + 128 <= N), staged through the
+// free ring slot `stage` (32 KiB) so that each store writes whole row pieces:
+// 4 rounds; in round r each wave writes its row blocks 2r and 2r + 1 (32
+// rows x its 64 student and 64 teacher tokens, the quads' 8-byte rows) into
+// 64 staged rows of 256 tokens (512 bytes, row rho at rho * 512, 32-byte
+// pieces xor-swizzled by rho % 16 so a write's 16 rows fall on distinct
+// banks), then each wave stores 16 staged rows, two per 16-byte store: lanes
+// 0-15 / 16-31 / 32-47 / 48-63 write the student and teacher halves (256
+// bytes each) of two rows.  A vocabulary tail beyond V is dropped by the
+// buffer resource, as in store_logits16.  Ends with a workgroup barrier.
+// Workgroup barrier around LDS staging: the wave's LDS accesses complete
+// before it, and neither the compiler nor the scheduler moves a memory
+// access across it.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+template <class T>
+__device__ __forceinline__ void store_logits16_staged(const Acc16& acc, const FusedParams& P, int64_t v0, int64_t t0,
+                                                      char* stage) {
+  typedef __attribute__((address_space(3))) u2v_t lds_u2;
+  typedef __attribute__((address_space(3))) u4v_t lds_u4;
+  const int lane = opaque_lane();
+  const int w = wave_id(), wm = w >> 1, wn = w & 1;
+  const int q = lane & 3;
+  const bool both = P.store_t != 0;
+  T* L = static_cast<T*>(P.Lout);
+  const uint32_t ldb = (uint32_t)(P.ldL * (int64_t)sizeof(T));
+  const int64_t rows = min<int64_t>(P.V - v0, 256);
+  const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(L + v0 * P.ldL + t0, rows * (int64_t)ldb);
+  char* st = stage;
+  // writes: staged row wm * 32 + 16 (mb & 1) + 4 (lane / 16) + q, byte
+  // column 2 (128 half + 64 wn + 16 (nb & 3) + 4 ((lane % 16) / 4))
+  const uint32_t wrow = (uint32_t)(wm * 32 + (lane >> 4) * 4 + q);  // + 16 (mb & 1)
+  const uint32_t wswz = (wrow & 15) << 5;                            // (mb & 1) * 16 leaves rho % 16
+  const uint32_t wcol = (uint32_t)(2 * (wn * 64 + 4 * ((lane & 15) >> 2)));
+  // reads: staged row w * 16 + 2 i + lane / 32, half (lane / 16) % 2
+  const int half = (lane >> 4) & 1;
+  const uint32_t rrow = (uint32_t)(w * 16 + (lane >> 5));  // + 2 i
+  const uint32_t rcol = (uint32_t)(2 * (half * 128 + (lane & 15) * 8));
+  const uint32_t gcol = (uint32_t)((half ? P.tcolL : 0) + (lane & 15) * 8) * (uint32_t)sizeof(T);
+  const bool rlive = both || half == 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int mb = 2 * r + h;
+      const uint32_t rho = wrow + (uint32_t)(16 * h);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) {
+        if (nb >= 4 && !both) break;
+        const uint2 o = quad_row16<T>(acc, mb, nb);
+        const uint32_t col = wcol + (uint32_t)(2 * ((nb >= 4 ? 128 : 0) + (nb & 3) * 16));
+        *(lds_u2*)(st + rho * 512 + (col ^ wswz)) = u2v_t{o.x, o.y};
+      }
+    }
+    stage_barrier();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t rho = rrow + (uint32_t)(2 * i);
+      if (rlive) {
+        const u4v_t v = *(const lds_u4*)(st + rho * 512 + (rcol ^ ((rho & 15) << 5)));
+        // tile row (rho / 32) * 128 + 32 r + rho % 32
+        const uint32_t trow = (rho >> 5) * 128 + (uint32_t)(32 * r) + (rho & 31);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, (int)(trow * ldb + gcol), 0, 0);
+      }
+    }
+    stage_barrier();
+  }
+}
+
 // Exchange a RowState with lane l ^ m of the same wave.
 __device__ __forceinline__ RowState shfl_state(const RowState& s, int m) {
   RowState o;
@@ -1175,7 +1250,7 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
     return x;
   };
   auto opnd = [&](const TI& x, int op) { return op == 0 ? x.a : bop; };
-  auto epilogue = [&](int, const TI& x, Acc16& c) __attribute__((always_inline)) {
+  auto epilogue = [&](int, const TI& x, Acc16& c, char* stage) __attribute__((always_inline)) {
     const int vlane0 = wm * 128 + (opaque_lane() >> 4) * 4;
     const int64_t vlimit = P.V - x.v0;
     if constexpr (TL == TL_STUDENT) {
@@ -1202,7 +1277,12 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
         if constexpr (j + 2 < NJ) issue_teacher16<T, TL>(raw[j & 1], P, x.v0, t0, j + 2);
       });
     } else {
-      if constexpr (STORE) store_logits16<T>(c, P, x.v0, t0);
+      if constexpr (STORE) {
+        if (t0 + 128 <= P.N)
+          store_logits16_staged<T>(c, P, x.v0, t0, stage);
+        else
+          store_logits16<T>(c, P, x.v0, t0);
+      }
       static_for<0, NJ>([&](auto J) {
         constexpr int j = decltype(J)::value;
         scan_variant<SV>(st[j], AccPair16{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
@@ -1688,7 +1768,7 @@ __global__ __launch_bounds__(kThreads4, 1) void k_gemm4(GemmParams P) {
     return x;
   };
   auto opnd = [](const TI& x, int op) { return op == 0 ? x.a : x.b; };
-  auto epilogue = [&](int, const TI& x, Acc16& c) __attribute__((always_inline)) {
+  auto epilogue = [&](int, const TI& x, Acc16& c, char*) __attribute__((always_inline)) {
     const int lane = opaque_lane();
     const int wm = w4_m(), wn = w4_n();
     const int64_t ldc = P.ldc;

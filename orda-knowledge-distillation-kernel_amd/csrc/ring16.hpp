@@ -91,7 +91,9 @@ __device__ __forceinline__ typename Traits<T>::Frag frag16(const char* tile, int
   }
 }
 
-// pipeline4's contract, with Acc16 accumulators and 16x16x32 MFMAs.
+// pipeline4's contract, with Acc16 accumulators and 16x16x32 MFMAs; the
+// epilogue also receives a free 32 KiB ring slot (epilogue(tile, info, acc,
+// slot)), which it must leave with a workgroup barrier if it writes it.
 template <class T, int LA, int LB, bool H0, bool H1, bool SWAP, class TileInfo, class Opnd, class Epi>
 __device__ __forceinline__ void pipeline16(Acc16& acc, char* lds, int ntiles, int64_t K, int64_t lda, int64_t ldb,
                                            const TileInfo& tile_info, const Opnd& opnd, const Epi& epilogue) {
@@ -290,7 +292,10 @@ __device__ __forceinline__ void pipeline16(Acc16& acc, char* lds, int ntiles, in
     }
     // the last MFMAs' results before the epilogue reads them
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-    epilogue(tile, cur, acc);
+    // (slot mod5(j0 + 4), operand B of the tile's last step, is read by no
+    // wave and written by no DMA until the next tile's first step: the
+    // epilogue may stage data there)
+    epilogue(tile, cur, acc, slot(mod5(j0 + 4)));
     if (nxt_live) {
       zero_acc16(acc);
       cur = nxt;
