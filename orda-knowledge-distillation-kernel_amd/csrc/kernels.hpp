@@ -1000,16 +1000,6 @@ __device__ __forceinline__ void store_logits16(const Acc16& acc, const FusedPara
   }
 }
 
-// store_logits16 for a full token tile (t0 + 128 <= N), staged through the
-// free ring slot `stage` (32 KiB) so that each store writes whole row pieces:
-// 4 rounds; in round r each wave writes its row blocks 2r and 2r + 1 (32
-// rows x its 64 student and 64 teacher tokens, the quads' 8-byte rows) into
-// 64 staged rows of 256 tokens (512 bytes, row rho at rho * 512, 32-byte
-// pieces xor-swizzled by rho % 16 so a write's 16 rows fall on distinct
-// banks), then each wave stores 16 staged rows, two per 16-byte store: lanes
-// 0-15 / 16-31 / 32-47 / 48-63 write the student and teacher halves (256
-// bytes each) of two rows.  A vocabulary tail beyond V is dropped by the
-// buffer resource, as in store_logits16.  Ends with a workgroup barrier.
 // Workgroup barrier around LDS staging: the wave's LDS accesses complete
 // before it, and neither the compiler nor the scheduler moves a memory
 // access across it.
@@ -1020,15 +1010,29 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
+// A full tile's logits (256 vocabulary rows x 256 token columns, columns
+// col16(nb, wn) + lane % 16 of block nb) to Lout, staged through the free
+// ring slot `stage` (32 KiB) so that each store writes whole row pieces.
+// Columns 0-127 go to Lout[v][t0 + c], columns 128-255 to Lout[v][t0 +
+// second + c - 128] (a tied tile: the teacher's tokens at second = tcolL,
+// written only when `both`; a student-only tile: second = 128).  Every token
+// of the tile is below N (t0 + 128 <= N tied, t0 + 256 <= N student-only).
+// 4 rounds; in round r each wave writes its row blocks 2r and 2r + 1 (32
+// rows x its 2 x 64 token columns, the quads' 8-byte rows) into
+// 64 staged rows of 256 tokens (512 bytes, row rho at rho * 512, 32-byte
+// pieces xor-swizzled by rho % 16 so a write's 16 rows fall on distinct
+// banks), then each wave stores 16 staged rows, two per 16-byte store: lanes
+// 0-15 / 16-31 / 32-47 / 48-63 write the two column halves (256 bytes
+// each) of two rows.  A vocabulary tail beyond V is dropped by the
+// buffer resource, as in store_logits16.  Ends with a workgroup barrier.
 template <class T>
-__device__ __forceinline__ void store_logits16_staged(const Acc16& acc, const FusedParams& P, int64_t v0, int64_t t0,
-                                                      char* stage) {
+__device__ __forceinline__ void store_tile16_staged(const Acc16& acc, const FusedParams& P, int64_t v0, int64_t t0,
+                                                    int64_t second, bool both, char* stage) {
   typedef __attribute__((address_space(3))) u2v_t lds_u2;
   typedef __attribute__((address_space(3))) u4v_t lds_u4;
   const int lane = opaque_lane();
   const int w = wave_id(), wm = w >> 1, wn = w & 1;
   const int q = lane & 3;
-  const bool both = P.store_t != 0;
   T* L = static_cast<T*>(P.Lout);
   const uint32_t ldb = (uint32_t)(P.ldL * (int64_t)sizeof(T));
   const int64_t rows = min<int64_t>(P.V - v0, 256);
@@ -1043,7 +1047,7 @@ __device__ __forceinline__ void store_logits16_staged(const Acc16& acc, const Fu
   const int half = (lane >> 4) & 1;
   const uint32_t rrow = (uint32_t)(w * 16 + (lane >> 5));  // + 2 i
   const uint32_t rcol = (uint32_t)(2 * (half * 128 + (lane & 15) * 8));
-  const uint32_t gcol = (uint32_t)((half ? P.tcolL : 0) + (lane & 15) * 8) * (uint32_t)sizeof(T);
+  const uint32_t gcol = (uint32_t)((half ? second : 0) + (lane & 15) * 8) * (uint32_t)sizeof(T);
   const bool rlive = both || half == 0;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -1253,18 +1257,24 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
   auto epilogue = [&](int, const TI& x, Acc16& c, char* stage) __attribute__((always_inline)) {
     const int vlane0 = wm * 128 + (opaque_lane() >> 4) * 4;
     const int64_t vlimit = P.V - x.v0;
+    // a full student-only tile's logits go out staged (whole row pieces);
+    // a tile with tokens past N stores block by block
+    const bool full = t0 + 256 <= P.N;
     if constexpr (TL == TL_STUDENT) {
+      if (full) store_tile16_staged<T>(c, P, x.v0, t0, 128, true, stage);
       static_for<0, NJ>([&](auto J) {
         constexpr int j = decltype(J)::value;
-        store_block16<T>(c, P, x.v0, t0, j);
+        if (!full) store_block16<T>(c, P, x.v0, t0, j);
         scan_variant<SV>(st[j], AccPair16S{c, j}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j], P);
       });
     } else if constexpr (TL != TL_NONE) {
-      // blocks j and j + 1 in flight while block j is scanned; block j's
-      // student logits stored after its scan
+      // blocks j and j + 1 in flight while block j is scanned (the staged
+      // store of the student's logits runs while the first two land); block
+      // j's student logits stored after its scan when the tile is not full
       uint2 raw[2][8];
       issue_teacher16<T, TL>(raw[0], P, x.v0, t0, 0);
       issue_teacher16<T, TL>(raw[1], P, x.v0, t0, 1);
+      if (full) store_tile16_staged<T>(c, P, x.v0, t0, 128, true, stage);
       static_for<0, NJ>([&](auto J) {
         constexpr int j = decltype(J)::value;
         order_teacher16<T, TL>(raw[j & 1]);
@@ -1273,13 +1283,13 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan16(FusedParams P) {
         }
         scan_variant<SV>(st[j], AccPair16TL<T>{c, j, raw[j & 1]}, vlane0, vlimit, vlimit >= 256, lse_sT[j],
                          lse_tT[j], P);
-        store_block16<T>(c, P, x.v0, t0, j);
+        if (!full) store_block16<T>(c, P, x.v0, t0, j);
         if constexpr (j + 2 < NJ) issue_teacher16<T, TL>(raw[j & 1], P, x.v0, t0, j + 2);
       });
     } else {
       if constexpr (STORE) {
         if (t0 + 128 <= P.N)
-          store_logits16_staged<T>(c, P, x.v0, t0, stage);
+          store_tile16_staged<T>(c, P, x.v0, t0, P.tcolL, P.store_t != 0, stage);
         else
           store_logits16<T>(c, P, x.v0, t0);
       }
