@@ -523,6 +523,16 @@ __global__ __launch_bounds__(kThreads) void k_scan(FusedParams P) {
 // Logits of a ring-engine tile to Lout[v][t] (see store_logits): block
 typedef unsigned int u2v_t __attribute__((ext_vector_type(2)));
 typedef unsigned int u4v_t __attribute__((ext_vector_type(4)));
+// Workgroup barrier around LDS staging: the wave's LDS accesses complete
+// before it, and neither the compiler nor the scheduler moves a memory
+// access across it.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
 
 // A buffer resource over [p, p + bytes) with base and size read through
 // readfirstlane, so it is scalar (p and bytes are wave-uniform, which the
@@ -740,6 +750,53 @@ __device__ __forceinline__ void store_block4(const Acc4& acc, const FusedParams&
       __builtin_amdgcn_sched_barrier(0);
     }
 }
+// A full student-only tile's logits (256 rows x 256 tokens, token column
+// col4(nb, wn) + lane % 32 of block nb; every token below N) to Lout's
+// student columns t0 .. t0 + 255, staged through the free ring slot `stage`
+// (32 KiB) as store_tile16_staged: 4 rounds, round r holding row block r
+// of both wave rows (staged row rho = 32 wm + 8 g + 4 (lane / 32) + q, the
+// quads' 8-byte rows, 32-byte pieces xor-swizzled by rho % 16), each wave
+// then storing 16 staged rows as whole 512-byte rows (lanes 0-15 / 16-31:
+// tokens 0-127 / 128-255 of one row, 32-47 / 48-63 the next row).  A
+// vocabulary tail beyond V is dropped by the buffer resource.  Ends with a
+// workgroup barrier.
+template <class T>
+__device__ __forceinline__ void store_tile4_staged(const Acc4& acc, const FusedParams& P, int64_t v0, int64_t t0,
+                                                   char* stage) {
+  typedef __attribute__((address_space(3))) u2v_t lds_u2;
+  typedef __attribute__((address_space(3))) u4v_t lds_u4;
+  const int lane = opaque_lane();
+  const int w = wave_id(), wm = w >> 1, wn = w & 1;
+  const int q = lane & 3;
+  const TileRowsL tr = tile_rows_l<T>(P.Lout, P, v0, t0);
+  const uint32_t wrow = (uint32_t)(wm * 32 + (lane >> 5) * 4 + q);  // + 8 g
+  const uint32_t wcol = (uint32_t)(2 * ((lane & 31) - q));
+  const int half = (lane >> 4) & 1;
+  const uint32_t rrow = (uint32_t)(w * 16 + (lane >> 5));  // + 2 i
+  const uint32_t rcol = (uint32_t)(2 * (half * 128 + (lane & 15) * 8));
+  const uint32_t gcol = rcol;  // student columns: token c at t0 + c
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint2 o = quad_row4<T>(acc, r, nb, g);
+        const uint32_t rho = wrow + (uint32_t)(8 * g);
+        const uint32_t col = wcol + (uint32_t)(2 * col4(nb, wn));
+        *(lds_u2*)(stage + rho * 512 + (col ^ ((rho & 15) << 5))) = u2v_t{o.x, o.y};
+      }
+    stage_barrier();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t rho = rrow + (uint32_t)(2 * i);
+      const u4v_t v = *(const lds_u4*)(stage + rho * 512 + (rcol ^ ((rho & 15) << 5)));
+      const uint32_t trow = (rho >> 5) * 128 + (uint32_t)(32 * r) + (rho & 31);
+      __builtin_amdgcn_raw_buffer_store_b128(v, tr.rs, (int)(trow * tr.ldb + gcol), 0, 0);
+    }
+    stage_barrier();
+  }
+}
 struct AccPairS {  // student only: accumulator block nb (the teacher accessor is never used)
   using Lay = Layout32;
   const Acc4& a;
@@ -850,7 +907,8 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
     return x;
   };
   auto opnd = [&](const TI& x, int op) { return op == 0 ? x.a : bop; };
-  auto epilogue = [&](int, const TI& x, Acc4& c) __attribute__((always_inline)) {
+  // (stage: the free ring slot, null from the fp8 pipeline)
+  auto epilogue = [&](int, const TI& x, Acc4& c, char* stage = nullptr) __attribute__((always_inline)) {
     const int vlane0 = wm * 128 + (opaque_lane() >> 5) * 4;
     const int64_t vlimit = P.V - x.v0;
     if constexpr (TL == TL_STUDENT) {
@@ -863,9 +921,13 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
       // blocks j and j + 1 in flight while block j is scanned; block j's
       // student logits stored after its scan (their stores are younger than
       // the loads of block j + 1, so its wait does not cover them)
+      // A full tile's student logits go out staged through the free ring
+      // slot (whole row pieces) while the first two blocks' loads land.
+      const bool staged = stage != nullptr && t0 + 256 <= P.N;
       uint2 raw[2][16];
       issue_teacher4<T, TL>(raw[0], P, x.v0, t0, 0);
       issue_teacher4<T, TL>(raw[1], P, x.v0, t0, 1);
+      if (staged) store_tile4_staged<T>(c, P, x.v0, t0, stage);
       static_for<0, NJ>([&](auto J) {
         constexpr int j = decltype(J)::value;
         order_teacher4<T, TL>(raw[j & 1]);
@@ -874,7 +936,7 @@ __global__ __launch_bounds__(kThreads4, 1) void k_scan4(FusedParams P) {
         }
         scan_variant<SV>(st[j], AccPairTL<T>{c, j, raw[j & 1]}, vlane0, vlimit, vlimit >= 256, lse_sT[j], lse_tT[j],
                          P);
-        store_block4<T>(c, P, x.v0, t0, j);
+        if (!staged) store_block4<T>(c, P, x.v0, t0, j);
         if constexpr (j + 2 < NJ) issue_teacher4<T, TL>(raw[j & 1], P, x.v0, t0, j + 2);
       });
     } else {
@@ -1000,16 +1062,6 @@ __device__ __forceinline__ void store_logits16(const Acc16& acc, const FusedPara
   }
 }
 
-// Workgroup barrier around LDS staging: the wave's LDS accesses complete
-// before it, and neither the compiler nor the scheduler moves a memory
-// access across it.
-__device__ __forceinline__ void stage_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
 // A full tile's logits (256 vocabulary rows x 256 token columns, columns
 // col16(nb, wn) + lane % 16 of block nb) to Lout, staged through the free
 // ring slot `stage` (32 KiB) so that each store writes whole row pieces.

@@ -358,7 +358,10 @@ __device__ __forceinline__ void pipeline4(Acc4& acc, char* lds, int ntiles, int6
       end_half(0);
       j0 = j2;
     }
-    epilogue(tile, cur, acc);
+    // (slot mod5(j0 + 4), operand B of the tile's last step, is read by no
+    // wave and written by no DMA until the next tile's first step: the
+    // epilogue may stage data there, ending with a workgroup barrier)
+    epilogue(tile, cur, acc, slot(mod5(j0 + 4)));
     if (nxt_live) {
       zero_acc4(acc);
       cur = nxt;
