@@ -12,7 +12,9 @@ vocabulary tile.  Checked: the four loss values (1e-3 relative) and the
 gradients within the scale-relative bounds of ``tests/_divgrad.py``, for the
 one-pass, two-pass and one-term power divergences (the latter on the ring
 scan with staged or in-place teacher logits; chi-squared over a computed
-teacher on the two-stage scan).
+teacher on the two-stage scan).  The tied and no-teacher cases run the ring
+scans' staged logits stores on full token tiles (and the per-block stores on
+the ragged one) beside the 8-row vocabulary tail.
 """
 from __future__ import annotations
 
@@ -51,27 +53,35 @@ CASES = [
     ("separate", "skew_reverse_kl", 1.0, 0.0),
     ("separate", "hellinger", 2.0, 0.0),
     ("separate", "chi_squared", 1.0, 0.0),
+    # the ring scans' staged logits stores at full token tiles beside a
+    # vocabulary tail: tied tiles (128 tokens, both halves) and student-only
+    # tiles (256 tokens, no teacher term)
+    ("tied", "forward_kl", 1.0, 1.0),
+    ("no_teacher", "forward_kl", 1.0, 1.0),
 ]
 
 
 @pytest.mark.parametrize("mode, div, T, w_s", CASES, ids=[f"{c[0]}-{c[1]}-T{c[2]:g}" for c in CASES])
 def test_hbm_passes_with_full_and_ragged_blocks(mode, div, T, w_s):
     o = _orda()
-    hs, W, _, hts, Wt, y = D.make_inputs(29, torch.bfloat16, n=N, v=V)
+    hs, W, ht, hts, Wt, y = D.make_inputs(29, torch.bfloat16, n=N, v=V)
     hs_d, W_d = hs.cuda().requires_grad_(True), W.cuda().requires_grad_(True)
-    if mode == "in_place":
+    kl_w = 0.0 if mode == "no_teacher" else 1.0
+    if mode in ("tied", "no_teacher"):
+        teacher, omode, okw = o.TiedTeacher(ht.cuda()), "tied", dict(teacher_hidden=_np(ht))
+    elif mode == "in_place":
         lt = (hts.float() @ Wt.float().t()).to(torch.bfloat16)
         teacher, omode, okw = o.PrecomputedTeacher(logits=lt.cuda()), "precomputed", dict(teacher_logits=_np(lt))
     else:
         teacher, omode = o.SeparateTeacher(hts.cuda(), Wt.cuda()), "separate"
         okw = dict(teacher_hidden=_np(hts), teacher_weight=_np(Wt), teacher_grads=False)
     out = o.distillation_loss(hs_d, W_d, y.cuda(), teacher, student_ce_weight=w_s, teacher_ce_weight=0.0,
-                              kl_weight=1.0, kl_temperature=T, divergence=div, backend="triton",
+                              kl_weight=kl_w, kl_temperature=T, divergence=div, backend="triton",
                               config=o.KernelConfig(chunk_size=128))
     out.loss.backward()
     torch.cuda.synchronize()
     ref = distillation_loss_oracle(omode, _np(hs), _np(W), y.numpy(), student_ce_weight=w_s, teacher_ce_weight=0.0,
-                                   kl_weight=1.0, kl_temperature=T, divergence=div, grad_logits_dtype="bfloat16",
+                                   kl_weight=kl_w, kl_temperature=T, divergence=div, grad_logits_dtype="bfloat16",
                                    **okw)
     for key in ("loss", "student_ce", "teacher_ce", "kl"):
         got = float(getattr(out, key).detach())
